@@ -1,0 +1,164 @@
+/*
+ * pkv.h -- C ABI of libpkv, the MI355X (gfx950) paged KV-cache attention path.
+ *
+ * Drop-in for the attention step of phildrip/llm-mojo's
+ * model_speculative_moe_batched.mojo: per-sequence block tables, token append into
+ * partially filled blocks, LIFO block free/reuse under continuous batching, read-only
+ * KV sharing with the MTP assistant layers, and rollback after rejected drafts.
+ *
+ * Conventions
+ *   - Every pointer argument named *_pool, block_tables, table_lens, free_list,
+ *     free_count, pos, n_new, new_len, q, k_new, v_new, out, status and workspace is
+ *     DEVICE memory owned by the caller. `stream` is a hipStream_t (NULL = the null
+ *     stream). All calls are stream-ordered and asynchronous; the library keeps no
+ *     device state between calls (all state lives in caller-owned buffers).
+ *   - Return value: PKV_OK (0) or a negative PKV_ERR_* code. Nothing throws across
+ *     the ABI; pkv_last_error() gives a message for the calling thread's last error.
+ *   - Pool layout is the reference's (model_speculative_moe_batched.mojo:1427-1451):
+ *     element (block b, slot i, kv head g, dim d) of a layer pool lives at
+ *     ((b * block_size + i) * num_kv_heads + g) * head_dim + d.
+ *   - Block tables: int32 [batch][table_stride]; table_lens: int32 [batch]. Row s of
+ *     the tables is sequence slot s. The reference's List[Int] tables hold the same
+ *     values in 64-bit.
+ *   - Free list: int32 [num_blocks] used as a LIFO stack free_list[0 .. *free_count);
+ *     allocation pops the back, freeing pushes to the back (BlockManager,
+ *     model_speculative_moe_batched.mojo:789-807). Initialise it to 0..num_blocks-1
+ *     and *free_count = num_blocks to start from the reference's fresh state.
+ *   - Concurrent calls that touch the same tables / free list / workspace race; order
+ *     them on one stream.
+ */
+#ifndef PKV_H
+#define PKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PKV_OK 0
+#define PKV_ERR_INVALID (-1)     /* bad argument (shape, dtype, null pointer)       */
+#define PKV_ERR_UNSUPPORTED (-2) /* geometry or mode this build has no kernel for   */
+#define PKV_ERR_WORKSPACE (-3)   /* workspace smaller than pkv_workspace_size()     */
+#define PKV_ERR_HIP (-4)         /* a HIP runtime call failed (see pkv_last_error)  */
+
+#define PKV_DTYPE_F32 0
+#define PKV_DTYPE_BF16 1
+
+/* Per-sequence status written by pkv_append / pkv_rollback. */
+#define PKV_SEQ_OK 0
+#define PKV_SEQ_OUT_OF_BLOCKS (-1) /* BlockManager.allocate() returned -1          */
+#define PKV_SEQ_TABLE_FULL (-2)    /* position beyond table_stride blocks           */
+#define PKV_SEQ_BAD_BLOCK (-3)     /* a table entry outside [0, num_blocks)         */
+#define PKV_SEQ_FREE_OVERFLOW (-4) /* freeing would overflow the free list          */
+#define PKV_SEQ_BAD_ARGS (-5)      /* n_new[s] > max_new                            */
+
+/* Layer geometry and numerics, shared by every entry point.
+ * Mirrors paged_attention_layer's scalar arguments (attention.mojo:240-256). */
+typedef struct pkv_params {
+    int32_t num_heads;    /* query heads Hq                                            */
+    int32_t num_kv_heads; /* KV heads Hkv; Hq % Hkv == 0                               */
+    int32_t head_dim;     /* D: 64, 128, 256 or 512                                    */
+    int32_t block_size;   /* tokens per block (the engine uses 16)                     */
+    int32_t num_blocks;   /* physical blocks in each pool (bounds every table entry)   */
+    int32_t window;       /* > 0: keys t >= pos - window + 1 (attention.mojo:135-141);
+                             <= 0: full causal                                          */
+    float scale;          /* multiplies q.k before the softmax. 1.0f reproduces the
+                             reference exactly (Gemma-4 has no softmax scale)          */
+    int32_t kv_dtype;     /* PKV_DTYPE_F32 or PKV_DTYPE_BF16 (pool element type)       */
+    int32_t ring_size;    /* must be 0 (paged addressing); ring mode is not built      */
+    int32_t reserved;     /* must be 0                                                 */
+} pkv_params;
+
+/* Bytes of workspace pkv_attend / pkv_decode / pkv_verify need for `batch` sequences
+ * of `q_len` queries whose last query position is at most max_pos, and that
+ * pkv_append needs for its commit counter. 0 on invalid params. The workspace must be
+ * zero-filled once after allocation; every call leaves its counters at zero again. */
+size_t pkv_workspace_size(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos);
+
+/* K1 -- fused block allocation + K/V scatter.
+ * Replaces the engine's inline append sites: model_speculative_moe_batched.mojo
+ * :1984-2001 (decode), :2513-2523 + :2621-2630 (chunked prefill), :2808-2825 (CPU
+ * prefill), :3011-3023 + :3106-3116 (verify).
+ * For each sequence s (in index order), the n_new[s] tokens at positions
+ * pos[s] .. pos[s]+n_new[s]-1 grow the table while p / block_size >= table_lens[s],
+ * popping blocks from the back of the free list, then their K and V rows are copied
+ * bit-exactly to row table[p / bs] * bs + p % bs of k_pool / v_pool.
+ * Out of blocks: blocks popped before the list ran dry stay in the table, none of the
+ * sequence's rows is written and status[s] = PKV_SEQ_OUT_OF_BLOCKS.
+ * pos[s] < 0 or n_new[s] <= 0 skips sequence s; n_new[s] > max_new changes nothing
+ * for s and gives PKV_SEQ_BAD_ARGS.
+ * k_new, v_new: [batch][max_new][num_kv_heads * head_dim] in kv_dtype.
+ * status: int32 [batch] (device), written for every sequence. */
+int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
+                   int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
+                   int32_t* free_list, int32_t* free_count, const int32_t* pos,
+                   const int32_t* n_new, int32_t max_new, const void* k_new, const void* v_new,
+                   int32_t batch, int32_t* status, void* workspace, size_t workspace_bytes);
+
+/* K2 -- split-K paged attention for decode and multi-token verify (fp32 or bf16 pools).
+ * Replaces paged_attention_layer + _eval_head_range + _softmax (attention.mojo:151-294)
+ * as called per query token by execute_attention_for_token
+ * (model_speculative_moe_batched.mojo:601-657), the verify loop (:3090-3123) and
+ * mtp_paged_attention (:577-599, read-only on the target's pool and table).
+ * Query j of sequence s sits at position pos[s] + j and attends keys
+ * [window_start(pos[s]+j), pos[s]+j] of its own table: softmax(scale * q.k) . V with
+ * the reference's sum + 1e-10 denominator. pos[s] < 0 gives zeros (attention.mojo
+ * :180-185).
+ * q, out: fp32 [batch][q_len][num_heads][head_dim].
+ * max_pos: an upper bound on pos[s] + q_len - 1 over the batch (sizes the grid); a
+ * sequence that exceeds it, or whose table holds an entry outside [0, num_blocks),
+ * gets NaN outputs. q_len * (num_heads / num_kv_heads) must be <= 16. */
+int32_t pkv_attend(void* stream, const pkv_params* p, const float* q, const void* k_pool,
+                   const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                   const int32_t* pos, int32_t q_len, int32_t batch, int32_t max_pos,
+                   float* out, void* workspace, size_t workspace_bytes);
+
+/* pkv_attend with q_len = 1: one decode token per sequence (the B=32 hot path). */
+int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void* k_pool,
+                   const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                   const int32_t* pos, int32_t batch, int32_t max_pos, float* out,
+                   void* workspace, size_t workspace_bytes);
+
+/* K5 -- rollback / retire. No reference counterpart for draft rollback (the engine
+ * leaves rejected rows in place and only advances pos, :3295-3368); retire is
+ * model_speculative_moe_batched.mojo:3626-3628 and chat reset :2424-2439.
+ * For each sequence s in index order with new_len[s] >= 0: keep
+ * ceil(new_len[s] / block_size) table entries (never more than it holds) and push the
+ * rest onto the back of the free list in ascending logical order. new_len[s] = 0
+ * retires the sequence; new_len[s] < 0 leaves it untouched. Pool rows are not
+ * modified. status (optional, int32 [batch]) receives PKV_SEQ_* per sequence; a
+ * sequence whose freed blocks would overflow the free list frees nothing and gets
+ * PKV_SEQ_FREE_OVERFLOW. */
+int32_t pkv_rollback(void* stream, const pkv_params* p, int32_t* block_tables,
+                     int32_t table_stride, int32_t* table_lens, int32_t* free_list,
+                     int32_t* free_count, const int32_t* new_len, int32_t batch,
+                     int32_t* status);
+
+/* Single-sequence drop-in with paged_attention_layer's argument list
+ * (attention.mojo:240-256): q, k_pool, v_pool, block_table (device int32, at least
+ * pos / block_size + 1 entries), block_size, pos, num_heads, num_kv_heads, head_dim,
+ * window, attn_out. The reference's `scores` / `rows` scratch is replaced by
+ * `workspace` (pkv_workspace_size(p, 1, 1, pos) bytes); the pool size and element
+ * type the GPU needs for bounds checks come in num_blocks / kv_dtype. ring_size must
+ * be 0. Softmax scale 1 (the reference has none). */
+int32_t pkv_paged_attention_layer(void* stream, const float* q, const void* k_pool,
+                                  const void* v_pool, const int32_t* block_table,
+                                  int32_t block_size, int32_t pos, int32_t num_heads,
+                                  int32_t num_kv_heads, int32_t head_dim, int32_t window,
+                                  float* attn_out, int32_t ring_size, int32_t ring_base,
+                                  int32_t num_blocks, int32_t kv_dtype, void* workspace,
+                                  size_t workspace_bytes);
+
+/* Message for the calling thread's most recent error ("" if none). */
+const char* pkv_last_error(void);
+
+/* ABI version: (major << 16) | minor. */
+int32_t pkv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PKV_H */

@@ -1,0 +1,93 @@
+// Host-side plumbing of libpkv: error reporting, parameter validation, workspace
+// layout, and the single-sequence paged_attention_layer drop-in.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "pkv_internal.h"
+
+namespace pkv {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+int32_t fail(int32_t code, const std::string& msg) {
+    set_error(msg);
+    return code;
+}
+
+int32_t check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(PKV_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    return PKV_OK;
+}
+
+int32_t validate_params(const pkv_params* p) {
+    if (!p) return fail(PKV_ERR_INVALID, "params is NULL");
+    if (p->num_heads <= 0 || p->num_kv_heads <= 0 || p->num_heads % p->num_kv_heads != 0)
+        return fail(PKV_ERR_INVALID, "num_kv_heads must be positive and divide num_heads");
+    if (p->head_dim != 64 && p->head_dim != 256 && p->head_dim != 512)
+        return fail(PKV_ERR_UNSUPPORTED, "head_dim must be 64, 256 or 512");
+    if (p->block_size <= 0 || p->block_size > 256)
+        return fail(PKV_ERR_INVALID, "block_size must be in [1, 256]");
+    if (p->num_blocks <= 0) return fail(PKV_ERR_INVALID, "num_blocks must be positive");
+    if (p->kv_dtype != PKV_DTYPE_F32 && p->kv_dtype != PKV_DTYPE_BF16)
+        return fail(PKV_ERR_INVALID, "kv_dtype must be PKV_DTYPE_F32 or PKV_DTYPE_BF16");
+    if (p->ring_size != 0)
+        return fail(PKV_ERR_UNSUPPORTED, "ring-buffer addressing (ring_size > 0) is not built");
+    if (p->reserved != 0) return fail(PKV_ERR_INVALID, "reserved must be 0");
+    // Row offsets are computed in 64-bit; the element index of a pool must still fit
+    // the int64 range comfortably, which any real pool does.
+    return PKV_OK;
+}
+
+AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos) {
+    AttendLayout L{};
+    // Keys per split: 256 rounded down to a whole number of blocks (at least one block).
+    int32_t bs = p->block_size;
+    int32_t chunk = (256 / bs) * bs;
+    if (chunk <= 0) chunk = bs;
+    L.chunk = chunk;
+    // Key range of one sequence: [window_start(pos0), pos0 + q_len - 1], pos0 + q_len - 1
+    // <= max_pos. Chunks are aligned to multiples of `chunk` in absolute positions.
+    int64_t full = (int64_t)max_pos / chunk + 1;
+    int64_t mc = full;
+    if (p->window > 0) {
+        int64_t span = (int64_t)p->window + q_len - 1;  // keys touched by the queries
+        int64_t win = (span + chunk - 1) / chunk + 1;
+        if (win < mc) mc = win;
+    }
+    if (mc < 1) mc = 1;
+    L.max_chunks = (int32_t)mc;
+    auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    size_t rows = (size_t)batch * q_len * p->num_heads;
+    L.counters_off = kTicketBytes;
+    size_t ctr_bytes = align((size_t)batch * p->num_kv_heads * sizeof(int32_t));
+    L.ml_off = L.counters_off + ctr_bytes;
+    size_t ml_bytes = align(rows * L.max_chunks * 2 * sizeof(float));
+    L.o_off = L.ml_off + ml_bytes;
+    size_t o_bytes = align(rows * L.max_chunks * (size_t)p->head_dim * sizeof(float));
+    L.total = L.o_off + o_bytes;
+    return L;
+}
+
+}  // namespace pkv
+
+extern "C" {
+
+size_t pkv_workspace_size(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos) {
+    if (pkv::validate_params(p) != PKV_OK) return 0;
+    if (batch <= 0 || q_len <= 0 || max_pos < 0) return 0;
+    return pkv::attend_layout(p, batch, q_len, max_pos).total;
+}
+
+const char* pkv_last_error(void) { return pkv::g_last_error.c_str(); }
+
+int32_t pkv_version(void) { return (1 << 16) | 0; }
+
+}  // extern "C"

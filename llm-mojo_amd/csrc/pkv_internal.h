@@ -1,0 +1,54 @@
+// Internal helpers shared by the libpkv HIP sources (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/pkv.h"
+
+namespace pkv {
+
+constexpr int kWave = 64;          // CDNA wavefront width
+constexpr int kBlockThreads = 256; // 4 waves per workgroup for every kernel here
+
+// Thread-local message behind pkv_last_error().
+void set_error(const std::string& msg);
+void clear_error();
+int32_t fail(int32_t code, const std::string& msg);
+int32_t check_launch(const char* what);
+
+// Validates the geometry shared by every entry point. Returns PKV_OK or an error code
+// (message set).
+int32_t validate_params(const pkv_params* p);
+
+inline size_t kv_elt_bytes(int32_t dtype) { return dtype == PKV_DTYPE_BF16 ? 2 : 4; }
+
+// Workspace layout (bytes from the base; every region 256-byte aligned):
+//   [0, 256)                    append commit ticket (int32)
+//   [256, 256 + ctr)            attention per-(sequence, kv head) chunk counters
+//   then part_ml                float2 per (row, chunk): running max m, sum l
+//   then part_o                 float [head_dim] per (row, chunk)
+struct AttendLayout {
+    int32_t chunk;       // keys per split
+    int32_t max_chunks;  // grid.x
+    size_t counters_off;
+    size_t ml_off;
+    size_t o_off;
+    size_t total;
+};
+constexpr size_t kTicketBytes = 256;
+AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos);
+
+__host__ __device__ inline int32_t window_start(int32_t pos, int32_t window) {
+    if (window <= 0) return 0;
+    int32_t s = pos - window + 1;
+    return s > 0 ? s : 0;
+}
+
+// bf16 (stored as uint16) -> fp32, exact.
+__device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+}  // namespace pkv

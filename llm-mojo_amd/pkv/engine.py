@@ -1,0 +1,225 @@
+"""Host-side mirror of the reference engine's paged-KV operator surface over libpkv.
+
+Reference host code (phildrip/llm-mojo, Mojo):
+  - attention_window_start / ring_row      attention.mojo:135-148
+  - paged_attention_layer                  attention.mojo:240-294
+  - BlockManager / Sequence state          model_speculative_moe_batched.mojo:789-845
+  - pools, one table per sequence shared by all layers   :1427-1451, :1995-1998
+  - inline KV append                       :1984-2001 (and the prefill/verify sites)
+  - retire (free table ascending)          :3626-3628
+
+Here the block-manager state (tables, lengths, LIFO free list) lives in device memory
+and every mutation is a libpkv kernel, so a batched decode step never round-trips
+through the host. Numbers on the host side are only what the caller feeds in
+(positions, token counts, new lengths).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import hip, lib
+
+F32 = "f32"
+BF16 = "bf16"
+_DTYPES = {F32: lib.PKV_DTYPE_F32, BF16: lib.PKV_DTYPE_BF16}
+_NP_KV = {F32: np.float32, BF16: np.uint16}  # bf16 is carried as its 16-bit pattern
+
+
+def attention_window_start(pos: int, window: int) -> int:
+    """First key position attended by the query at `pos` (attention.mojo:135-141)."""
+    if window <= 0:
+        return 0
+    start = pos - window + 1
+    return start if start > 0 else 0
+
+
+def ring_row(slot: int, ring_size: int, t: int) -> int:
+    """Physical row of token t in ring slot `slot` (attention.mojo:144-148)."""
+    return slot * ring_size + t % ring_size
+
+
+@dataclass(frozen=True)
+class LayerSpec:
+    """Geometry of one attention layer's pools (Gemma-4: sliding 16/8/256 window 1024,
+    global 16/2/512 full causal; the benchmark configs use 16/8/256 for both)."""
+
+    num_heads: int = 16
+    num_kv_heads: int = 8
+    head_dim: int = 256
+    window: int = 0
+    kv_dtype: str = F32
+
+    @property
+    def kv_stride(self) -> int:
+        return self.num_kv_heads * self.head_dim
+
+
+def make_params(spec: LayerSpec, block_size: int, num_blocks: int,
+                scale: float = 1.0) -> lib.PkvParams:
+    p = lib.PkvParams()
+    p.num_heads = spec.num_heads
+    p.num_kv_heads = spec.num_kv_heads
+    p.head_dim = spec.head_dim
+    p.block_size = block_size
+    p.num_blocks = num_blocks
+    p.window = spec.window
+    p.scale = scale
+    p.kv_dtype = _DTYPES[spec.kv_dtype]
+    p.ring_size = 0
+    p.reserved = 0
+    return p
+
+
+def _ptr(x) -> int | None:
+    if x is None:
+        return None
+    if isinstance(x, hip.DeviceArray):
+        return x.ptr
+    return int(x)
+
+
+class PagedKVCache:
+    """Device-resident paged KV cache: per-layer K/V pools of `num_blocks` blocks of
+    `block_size` tokens, one block table per sequence slot shared by every layer, and
+    the BlockManager's LIFO free list.
+
+    Pools are zero-filled at creation like the reference's (…batched.mojo:1444-1447);
+    the free list starts as [0 .. num_blocks-1] with every block free (:795-799)."""
+
+    def __init__(self, layers: list[LayerSpec], *, block_size: int, num_blocks: int,
+                 max_seqs: int, max_blocks_per_seq: int, max_q_len: int = 1,
+                 max_pos: int | None = None, scale: float = 1.0, stream: hip.Stream | None = None):
+        lib.load()
+        self.layers = list(layers)
+        self.block_size = block_size
+        self.num_blocks = num_blocks
+        self.max_seqs = max_seqs
+        self.table_stride = max_blocks_per_seq
+        self.max_q_len = max_q_len
+        self.max_pos = max_pos if max_pos is not None else max_blocks_per_seq * block_size - 1
+        self.scale = scale
+        self.stream = stream
+        self.params = [make_params(s, block_size, num_blocks, scale) for s in self.layers]
+        self.k_pools, self.v_pools = [], []
+        for s in self.layers:
+            shape = (num_blocks, block_size, s.num_kv_heads, s.head_dim)
+            self.k_pools.append(hip.DeviceArray(shape, _NP_KV[s.kv_dtype], zero=True))
+            self.v_pools.append(hip.DeviceArray(shape, _NP_KV[s.kv_dtype], zero=True))
+        self.tables = hip.DeviceArray((max_seqs, max_blocks_per_seq), np.int32, zero=True)
+        self.table_lens = hip.DeviceArray((max_seqs,), np.int32, zero=True)
+        self.free_list = hip.DeviceArray.from_numpy(np.arange(num_blocks, dtype=np.int32))
+        self.free_count = hip.DeviceArray.from_numpy(np.array([num_blocks], dtype=np.int32))
+        self.status = hip.DeviceArray((max_seqs,), np.int32, zero=True)
+        ws = 0
+        for p in self.params:
+            need = lib.load().pkv_workspace_size(ctypes.byref(p), max_seqs, max_q_len,
+                                                 self.max_pos)
+            if need == 0:
+                raise lib.PkvError(-1, "pkv_workspace_size", lib.load().pkv_last_error().decode())
+            ws = max(ws, need)
+        self.workspace = hip.DeviceArray((ws,), np.uint8, zero=True)
+        # Small host->device staging buffers for per-call integer arguments.
+        self._i32_a = hip.DeviceArray((max_seqs,), np.int32, zero=True)
+        self._i32_b = hip.DeviceArray((max_seqs,), np.int32, zero=True)
+
+    # -------------------------------------------------------------- helpers
+    def _stream(self):
+        return self.stream.handle if self.stream else None
+
+    def _ints(self, x, staging: hip.DeviceArray, n: int):
+        """Device pointer for an int32[n] argument given as numpy/list or device array."""
+        if isinstance(x, (np.ndarray, list, tuple)):
+            arr = np.ascontiguousarray(np.asarray(x, dtype=np.int32).reshape(-1))
+            if arr.size != n:
+                raise ValueError(f"expected {n} ints, got {arr.size}")
+            staging.upload_at(0, arr)
+            return staging.ptr
+        return _ptr(x)
+
+    # ------------------------------------------------------------ operators
+    def append(self, layer: int, pos, n_new, k_new, v_new, max_new: int, batch: int | None = None):
+        """KV append for `batch` sequence slots (K1). pos / n_new: int32[batch] (numpy or
+        device); k_new / v_new: device [batch][max_new][kv_stride] in the pool dtype.
+        Returns the device status array (PKV_SEQ_* per sequence)."""
+        b = batch or self.max_seqs
+        p = self.params[layer]
+        lib.call("pkv_append", self._stream(), ctypes.byref(p), self.k_pools[layer].ptr,
+                 self.v_pools[layer].ptr, self.tables.ptr, self.table_stride,
+                 self.table_lens.ptr, self.free_list.ptr, self.free_count.ptr,
+                 self._ints(pos, self._i32_a, b), self._ints(n_new, self._i32_b, b), max_new,
+                 _ptr(k_new), _ptr(v_new), b, self.status.ptr, self.workspace.ptr,
+                 self.workspace.nbytes)
+        return self.status
+
+    def attend(self, layer: int, q, pos, q_len: int, out, batch: int | None = None,
+               max_pos: int | None = None):
+        """Paged attention (K2): q/out device fp32 [batch][q_len][Hq][D]; query j of
+        sequence s at position pos[s] + j."""
+        b = batch or self.max_seqs
+        p = self.params[layer]
+        lib.call("pkv_attend", self._stream(), ctypes.byref(p), _ptr(q),
+                 self.k_pools[layer].ptr, self.v_pools[layer].ptr, self.tables.ptr,
+                 self.table_stride, self._ints(pos, self._i32_a, b), q_len, b,
+                 self.max_pos if max_pos is None else max_pos, _ptr(out), self.workspace.ptr,
+                 self.workspace.nbytes)
+
+    def rollback(self, new_len, batch: int | None = None, status=None):
+        """Truncate tables to ceil(new_len / block_size) blocks, freeing the tail in
+        ascending logical order (K5). new_len[s] < 0 leaves slot s alone; 0 retires it."""
+        b = batch or self.max_seqs
+        p = self.params[0]
+        lib.call("pkv_rollback", self._stream(), ctypes.byref(p), self.tables.ptr,
+                 self.table_stride, self.table_lens.ptr, self.free_list.ptr,
+                 self.free_count.ptr, self._ints(new_len, self._i32_a, b), b,
+                 _ptr(status) if status is not None else self.status.ptr)
+        return self.status
+
+    def retire(self, slots, batch: int | None = None):
+        """Free every block of the given slots (…batched.mojo:3626-3628)."""
+        b = batch or self.max_seqs
+        nl = np.full(b, -1, dtype=np.int32)
+        nl[list(slots)] = 0
+        return self.rollback(nl, b)
+
+    # ---------------------------------------------------------------- state
+    def snapshot(self) -> dict:
+        hip.synchronize()
+        fc = int(self.free_count.numpy()[0])
+        return {
+            "tables": self.tables.numpy(),
+            "table_lens": self.table_lens.numpy(),
+            "free_list": self.free_list.numpy()[:fc].copy(),
+            "free_count": fc,
+        }
+
+    def free(self):
+        for a in self.k_pools + self.v_pools:
+            a.free()
+        for a in (self.tables, self.table_lens, self.free_list, self.free_count, self.status,
+                  self.workspace, self._i32_a, self._i32_b):
+            a.free()
+
+
+def paged_attention_layer(q, k_pool, v_pool, block_table, block_size: int, pos: int,
+                          num_heads: int, num_kv_heads: int, head_dim: int, window: int,
+                          attn_out, ring_size: int = 0, ring_base: int = 0, *,
+                          num_blocks: int, kv_dtype: str = F32, workspace=None,
+                          stream: hip.Stream | None = None) -> None:
+    """Single-sequence drop-in with the reference's argument list (attention.mojo:240-256).
+
+    All buffers are device memory. The reference's `scores` / `rows` scratch becomes
+    `workspace` (allocated here when not given); num_blocks / kv_dtype bound the pool."""
+    L = lib.load()
+    ws = workspace
+    if ws is None:
+        p = make_params(LayerSpec(num_heads, num_kv_heads, head_dim, window, kv_dtype),
+                        block_size, num_blocks)
+        need = L.pkv_workspace_size(ctypes.byref(p), 1, 1, max(pos, 0))
+        ws = hip.DeviceArray((max(need, 256),), np.uint8, zero=True)
+    lib.call("pkv_paged_attention_layer", stream.handle if stream else None, _ptr(q),
+             _ptr(k_pool), _ptr(v_pool), _ptr(block_table), block_size, pos, num_heads,
+             num_kv_heads, head_dim, window, _ptr(attn_out), ring_size, ring_base, num_blocks,
+             _DTYPES[kv_dtype], ws.ptr, ws.nbytes)

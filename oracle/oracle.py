@@ -1,0 +1,248 @@
+"""numpy bindings of the CPU oracle (oracle/pkv_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the parity checker and the timed CPU baseline. Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg import this module. Function
+docstrings name the reference code each restates (phildrip/llm-mojo, file:line).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(ORACLE_DIR, "libpkv_oracle.so")
+
+F32, BF16 = 0, 1
+_lib = None
+
+
+def _L():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle not built: run `make -C {ORACLE_DIR}`")
+        L = ctypes.CDLL(LIB_PATH)
+        i64, i32, vp, f32 = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float
+        sig = {
+            "pkvo_window_start": (i64, [i64, i64]),
+            "pkvo_ring_row": (i64, [i64, i64, i64]),
+            "pkvo_paged_attention_layer": (ctypes.c_int, [vp, vp, vp, ctypes.c_int, vp, i64, i64,
+                                                          i64, i64, i64, i64, i64, vp, vp, vp,
+                                                          i64, i64, ctypes.c_int]),
+            "pkvo_legacy_paged_attention": (None, [vp, vp, vp, ctypes.c_int, vp, i64, i64, i64,
+                                                   i64, i64, vp, vp]),
+            "pkvo_attention_f64": (None, [vp, vp, vp, ctypes.c_int, vp, i64, i64, i64, i64, i64,
+                                          i64, vp]),
+            "pkvo_lcg_init": (ctypes.c_uint64, [ctypes.c_uint64]),
+            "pkvo_fill_random": (ctypes.c_uint64, [vp, i64, f32, ctypes.c_uint64]),
+            "pkvo_f32_to_bf16_array": (None, [vp, vp, i64]),
+            "pkvo_bm_init": (None, [vp, vp, i32]),
+            "pkvo_bm_allocate": (i32, [vp, vp]),
+            "pkvo_bm_free": (None, [vp, vp, i32]),
+            "pkvo_append": (None, [ctypes.c_int, i32, i32, vp, vp, vp, i32, vp, vp, vp, vp, vp,
+                                   i32, vp, vp, i32, vp]),
+            "pkvo_rollback": (None, [i32, vp, i32, vp, vp, vp, vp, i32]),
+            "pkvo_attend": (ctypes.c_int, [ctypes.c_int, i32, i32, i32, i32, i32, f32, vp, vp, vp,
+                                           vp, i32, vp, vp, i32, i32, vp, ctypes.c_int,
+                                           ctypes.c_int]),
+            "pkvo_max_threads": (ctypes.c_int, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _dtype_of(pool: np.ndarray) -> int:
+    if pool.dtype == np.float32:
+        return F32
+    if pool.dtype == np.uint16:
+        return BF16
+    raise TypeError(f"pool dtype {pool.dtype} (want float32 or uint16 bf16 bits)")
+
+
+def max_threads() -> int:
+    return _L().pkvo_max_threads()
+
+
+def window_start(pos: int, window: int) -> int:
+    """attention.mojo:135-141"""
+    return _L().pkvo_window_start(pos, window)
+
+
+def ring_row(slot: int, ring_size: int, t: int) -> int:
+    """attention.mojo:144-148"""
+    return _L().pkvo_ring_row(slot, ring_size, t)
+
+
+def paged_attention_layer(q, k_pool, v_pool, block_table, block_size, pos, num_heads,
+                          num_kv_heads, head_dim, window, scores=None, rows=None, attn_out=None,
+                          ring_size=0, ring_base=0, nthreads=1):
+    """3-pass fp32 attention, attention.mojo:240-294 (+ :151-237). Returns attn_out.
+    scores / rows may be given to check the scratch contract (scores >= Hq*n, rows >= n)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    tab = np.ascontiguousarray(np.asarray(block_table, dtype=np.int64))
+    n = pos + 1 - window_start(pos, window)
+    if scores is None:
+        scores = np.empty(max(num_heads * n, 1), np.float32)
+    if rows is None:
+        rows = np.empty(max(n, 1), np.int64)
+    if attn_out is None:
+        attn_out = np.empty(num_heads * head_dim, np.float32)
+    rc = _L().pkvo_paged_attention_layer(_p(q), _p(k_pool), _p(v_pool), _dtype_of(k_pool),
+                                         _p(tab), tab.size, block_size, pos, num_heads,
+                                         num_kv_heads, head_dim, window, _p(scores), _p(rows),
+                                         _p(attn_out), ring_size, ring_base, nthreads)
+    if rc != 0:
+        raise RuntimeError(f"paged_attention_layer rc={rc}")
+    return attn_out
+
+
+def legacy_paged_attention(q, k_pool, v_pool, block_table, block_size, pos, heads, kv_heads,
+                           head_dim):
+    """test_attention.mojo:62-117 (the engine's pre-refactor loop)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    tab = np.ascontiguousarray(np.asarray(block_table, dtype=np.int64))
+    scores = np.empty(pos + 1, np.float32)
+    out = np.empty(heads * head_dim, np.float32)
+    _L().pkvo_legacy_paged_attention(_p(q), _p(k_pool), _p(v_pool), _dtype_of(k_pool), _p(tab),
+                                     block_size, pos, heads, kv_heads, head_dim, _p(scores),
+                                     _p(out))
+    return out
+
+
+def attention_f64(q, k_pool, v_pool, block_table, block_size, pos, start_t, heads, kv_heads,
+                  head_dim):
+    """test_attention.mojo:123-163 (naive float64 reference)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    tab = np.ascontiguousarray(np.asarray(block_table, dtype=np.int64))
+    out = np.empty(heads * head_dim, np.float64)
+    _L().pkvo_attention_f64(_p(q), _p(k_pool), _p(v_pool), _dtype_of(k_pool), _p(tab),
+                            block_size, pos, start_t, heads, kv_heads, head_dim, _p(out))
+    return out
+
+
+class Lcg:
+    """test_attention.mojo:27-37 -- uniform [-1, 1) from a 64-bit LCG."""
+
+    def __init__(self, seed: int):
+        self.state = _L().pkvo_lcg_init(seed)
+
+    def fill(self, n: int, scale: float) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        self.state = _L().pkvo_fill_random(_p(out), n, scale, self.state)
+        return out
+
+
+def shuffled_block_table(num_logical: int, num_blocks: int) -> np.ndarray:
+    """test_attention.mojo:45-50 -- (i*37 + 11) % num_blocks."""
+    return (np.arange(num_logical, dtype=np.int64) * 37 + 11) % num_blocks
+
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    _L().pkvo_f32_to_bf16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+class BlockManager:
+    """model_speculative_moe_batched.mojo:789-807 (LIFO free list)."""
+
+    def __init__(self, max_blocks: int):
+        self.free_list = np.empty(max_blocks, np.int32)
+        self.count = np.zeros(1, np.int32)
+        _L().pkvo_bm_init(_p(self.free_list), _p(self.count), max_blocks)
+
+    def allocate(self) -> int:
+        return _L().pkvo_bm_allocate(_p(self.free_list), _p(self.count))
+
+    def free(self, block_id: int) -> None:
+        _L().pkvo_bm_free(_p(self.free_list), _p(self.count), block_id)
+
+    @property
+    def free_blocks(self) -> np.ndarray:
+        return self.free_list[: int(self.count[0])].copy()
+
+
+class CacheState:
+    """CPU mirror of the device block-manager state + pools, mutated by the oracle's
+    append / rollback (the engine's inline append sites and retire, see pkv_oracle.c)."""
+
+    def __init__(self, num_layers, kv_stride, block_size, num_blocks, max_seqs, table_stride,
+                 dtype=np.float32):
+        self.kv_stride = kv_stride
+        self.block_size = block_size
+        self.num_blocks = num_blocks
+        self.table_stride = table_stride
+        self.dtype = np.dtype(dtype)
+        self.k_pools = [np.zeros(num_blocks * block_size * kv_stride, self.dtype)
+                        for _ in range(num_layers)]
+        self.v_pools = [np.zeros(num_blocks * block_size * kv_stride, self.dtype)
+                        for _ in range(num_layers)]
+        self.tables = np.zeros((max_seqs, table_stride), np.int32)
+        self.table_lens = np.zeros(max_seqs, np.int32)
+        self.bm = BlockManager(num_blocks)
+
+    @property
+    def free_list(self) -> np.ndarray:
+        return self.bm.free_blocks
+
+    def append(self, layer, pos, n_new, k_new, v_new, max_new):
+        pos = np.ascontiguousarray(pos, np.int32)
+        n_new = np.ascontiguousarray(n_new, np.int32)
+        k_new = np.ascontiguousarray(k_new, self.dtype)
+        v_new = np.ascontiguousarray(v_new, self.dtype)
+        batch = pos.size
+        status = np.zeros(batch, np.int32)
+        _L().pkvo_append(BF16 if self.dtype == np.uint16 else F32, self.kv_stride,
+                         self.block_size, _p(self.k_pools[layer]), _p(self.v_pools[layer]),
+                         _p(self.tables), self.table_stride, _p(self.table_lens),
+                         _p(self.bm.free_list), _p(self.bm.count), _p(pos), _p(n_new), max_new,
+                         _p(k_new), _p(v_new), batch, _p(status))
+        return status
+
+    def rollback(self, new_len):
+        new_len = np.ascontiguousarray(new_len, np.int32)
+        _L().pkvo_rollback(self.block_size, _p(self.tables), self.table_stride,
+                           _p(self.table_lens), _p(self.bm.free_list), _p(self.bm.count),
+                           _p(new_len), new_len.size)
+
+
+def attend(q, k_pool, v_pool, tables, table_lens, pos, q_len, num_heads, num_kv_heads,
+           head_dim, block_size, window, scale=1.0, nthreads=1, par=0):
+    """Batched reference attention: one paged_attention_layer call per query token
+    (…batched.mojo:601-657, :3090-3123). q: [batch, q_len, Hq, D] fp32."""
+    q = np.ascontiguousarray(q, np.float32)
+    tables = np.ascontiguousarray(tables, np.int32)
+    table_lens = np.ascontiguousarray(table_lens, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    batch = pos.size
+    out = np.empty((batch, q_len, num_heads, head_dim), np.float32)
+    rc = _L().pkvo_attend(_dtype_of(k_pool), num_heads, num_kv_heads, head_dim, block_size,
+                          window, scale, _p(q), _p(k_pool), _p(v_pool), _p(tables),
+                          tables.shape[1], _p(table_lens), _p(pos), q_len, batch, _p(out),
+                          nthreads, par)
+    if rc != 0:
+        raise RuntimeError(f"pkvo_attend rc={rc}")
+    return out
+
+
+def max_rel_err(x, ref) -> float:
+    """test_attention.mojo:259-266 -- max |x - ref| / (|ref| + 1e-3)."""
+    x = np.asarray(x, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(x - ref) / (np.abs(ref) + 1e-3))) if x.size else 0.0

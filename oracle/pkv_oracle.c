@@ -1,0 +1,505 @@
+/*
+ * pkv_oracle.c -- CPU restatement of the reference paged KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the parity checker and the timed CPU
+ * baseline; it is never part of the product. Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load the library built from it.
+ *
+ * The reference is Mojo (phildrip/llm-mojo, mojo 1.0.0b2). Mojo is not available
+ * to build or run, so each function below restates the reference code it cites.
+ *
+ *   oracle function                  reference (file:line)
+ *   -------------------------------  ------------------------------------------------
+ *   pkvo_window_start                attention.mojo:135-141
+ *   pkvo_ring_row                    attention.mojo:144-148
+ *   softmax_ref (static)             attention.mojo:151-162
+ *   eval_head_range (static)         attention.mojo:165-237
+ *   pkvo_paged_attention_layer       attention.mojo:240-294
+ *   pkvo_legacy_paged_attention      test_attention.mojo:62-117 (pre-refactor engine loop)
+ *   pkvo_attention_f64               test_attention.mojo:123-163 (float64 naive oracle)
+ *   pkvo_lcg_* / pkvo_fill_random    test_attention.mojo:27-42
+ *   pkvo_bm_*                        model_speculative_moe_batched.mojo:789-807 (BlockManager)
+ *   pkvo_append                      model_speculative_moe_batched.mojo:1984-2001 (decode),
+ *                                    :2513-2523 + :2621-2630 (chunked prefill),
+ *                                    :2808-2825 (CPU prefill), :3011-3023 + :3106-3116 (verify)
+ *   pkvo_rollback                    retire :3626-3628 / reset :2424-2439 (ascending free order);
+ *                                    truncation after rejected drafts has no reference code and
+ *                                    follows the build's definition (keep ceil(len/bs) blocks,
+ *                                    free the tail in ascending logical order).
+ *   pkvo_attend                      execute_attention_for_token :601-657 / mtp_paged_attention
+ *                                    :577-599, one paged_attention_layer call per query token.
+ *
+ * Bit-level notes (parity of the fp32 attention output is a tolerance, not bits):
+ *   - SIMD[f32, 8] accumulation is restated as 8 independent lane accumulators; the
+ *     horizontal reduce_add is a halving tree. Mojo's exact reduce order and its exp()
+ *     are not pinned (the Mojo stdlib is absent); compile with -ffp-contract=off so no
+ *     FMA contraction is introduced here.
+ *   - bf16 pools are read by exact upcast (bits << 16), i.e. the reference run on the
+ *     bf16-rounded values.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define PKVO_F32 0
+#define PKVO_BF16 1
+
+/* ---------------------------------------------------------------- helpers */
+
+static inline float bf16_to_f32(uint16_t b) {
+    uint32_t u = ((uint32_t)b) << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* Round-to-nearest-even fp32 -> bf16 (NaN kept quiet). */
+uint16_t pkvo_f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+void pkvo_f32_to_bf16_array(const float* src, uint16_t* dst, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = pkvo_f32_to_bf16(src[i]);
+}
+
+/* Load 8 consecutive pool elements as fp32 (SIMD[f32, 8] load). */
+static inline void load8(const void* pool, int dtype, int64_t off, float* out) {
+    if (dtype == PKVO_BF16) {
+        const uint16_t* p = (const uint16_t*)pool + off;
+        for (int j = 0; j < 8; ++j) out[j] = bf16_to_f32(p[j]);
+    } else {
+        const float* p = (const float*)pool + off;
+        for (int j = 0; j < 8; ++j) out[j] = p[j];
+    }
+}
+
+static inline float load1(const void* pool, int dtype, int64_t off) {
+    if (dtype == PKVO_BF16) return bf16_to_f32(((const uint16_t*)pool)[off]);
+    return ((const float*)pool)[off];
+}
+
+/* SIMD[f32, 8].reduce_add restated as a halving tree. */
+static inline float reduce_add8(const float* a) {
+    float b0 = a[0] + a[4], b1 = a[1] + a[5], b2 = a[2] + a[6], b3 = a[3] + a[7];
+    float c0 = b0 + b2, c1 = b1 + b3;
+    return c0 + c1;
+}
+
+/* ------------------------------------------------- attention.mojo:135-148 */
+
+int64_t pkvo_window_start(int64_t pos, int64_t window) {
+    if (window <= 0) return 0;
+    int64_t start = pos - window + 1;
+    return start > 0 ? start : 0;
+}
+
+int64_t pkvo_ring_row(int64_t slot, int64_t ring_size, int64_t t) {
+    return slot * ring_size + t % ring_size;
+}
+
+/* ------------------------------------------------- attention.mojo:151-162 */
+
+static void softmax_ref(float* scores, int64_t size) {
+    float max_val = scores[0];
+    for (int64_t i = 1; i < size; ++i)
+        if (scores[i] > max_val) max_val = scores[i];
+    float sum_exp = 0.0f;
+    for (int64_t i = 0; i < size; ++i) {
+        scores[i] = expf(scores[i] - max_val);
+        sum_exp += scores[i];
+    }
+    for (int64_t i = 0; i < size; ++i) scores[i] /= (sum_exp + 1e-10f);
+}
+
+/* ------------------------------------------------- attention.mojo:165-237 */
+
+static void eval_head_range(const float* q, const void* k_pool, const void* v_pool, int dtype,
+                            const int64_t* rows, float* scores, float* attn_out, int64_t n,
+                            int64_t g_offset, int64_t h_start, int64_t h_end, int64_t head_dim) {
+    if (n <= 0) {
+        for (int64_t h = h_start; h < h_end; ++h)
+            for (int64_t d = 0; d < head_dim; ++d) attn_out[h * head_dim + d] = 0.0f;
+        return;
+    }
+    float kv[8];
+    /* 1. scores: head pairs share each K row load */
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t k_off = rows[i] + g_offset;
+        int64_t h = h_start;
+        while (h + 1 < h_end) {
+            const float* q0 = q + h * head_dim;
+            const float* q1 = q + (h + 1) * head_dim;
+            float s0[8] = {0}, s1[8] = {0};
+            for (int64_t d = 0; d < head_dim; d += 8) {
+                load8(k_pool, dtype, k_off + d, kv);
+                for (int j = 0; j < 8; ++j) {
+                    s0[j] = s0[j] + q0[d + j] * kv[j];
+                    s1[j] = s1[j] + q1[d + j] * kv[j];
+                }
+            }
+            scores[h * n + i] = reduce_add8(s0);
+            scores[(h + 1) * n + i] = reduce_add8(s1);
+            h += 2;
+        }
+        while (h < h_end) {
+            const float* q0 = q + h * head_dim;
+            float s0[8] = {0};
+            for (int64_t d = 0; d < head_dim; d += 8) {
+                load8(k_pool, dtype, k_off + d, kv);
+                for (int j = 0; j < 8; ++j) s0[j] = s0[j] + q0[d + j] * kv[j];
+            }
+            scores[h * n + i] = reduce_add8(s0);
+            h += 1;
+        }
+    }
+    /* 2. softmax and zero-init output per head */
+    for (int64_t h = h_start; h < h_end; ++h) {
+        softmax_ref(scores + h * n, n);
+        for (int64_t d = 0; d < head_dim; ++d) attn_out[h * head_dim + d] = 0.0f;
+    }
+    /* 3. values: head pairs share each V row load */
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t v_off = rows[i] + g_offset;
+        int64_t h = h_start;
+        while (h + 1 < h_end) {
+            float* o0 = attn_out + h * head_dim;
+            float* o1 = attn_out + (h + 1) * head_dim;
+            float a0 = scores[h * n + i], a1 = scores[(h + 1) * n + i];
+            for (int64_t d = 0; d < head_dim; d += 8) {
+                load8(v_pool, dtype, v_off + d, kv);
+                for (int j = 0; j < 8; ++j) {
+                    o0[d + j] = o0[d + j] + a0 * kv[j];
+                    o1[d + j] = o1[d + j] + a1 * kv[j];
+                }
+            }
+            h += 2;
+        }
+        while (h < h_end) {
+            float* o0 = attn_out + h * head_dim;
+            float a0 = scores[h * n + i];
+            for (int64_t d = 0; d < head_dim; d += 8) {
+                load8(v_pool, dtype, v_off + d, kv);
+                for (int j = 0; j < 8; ++j) o0[d + j] = o0[d + j] + a0 * kv[j];
+            }
+            h += 1;
+        }
+    }
+}
+
+/* ------------------------------------------------- attention.mojo:240-294
+ * Returns 0, or -1 when the ring is smaller than the attended window (the
+ * reference aborts there, :265-266), or -2 when pos lies beyond the table
+ * (the reference's debug_assert, :271).
+ * nthreads > 1 runs the head-pair tasks on OpenMP threads, mirroring the
+ * reference's parallelize over num_heads // 2 tasks (:276-287).            */
+int pkvo_paged_attention_layer(const float* q, const void* k_pool, const void* v_pool, int dtype,
+                               const int64_t* block_table, int64_t table_len, int64_t block_size,
+                               int64_t pos, int64_t num_heads, int64_t num_kv_heads,
+                               int64_t head_dim, int64_t window, float* scores, int64_t* rows,
+                               float* attn_out, int64_t ring_size, int64_t ring_base, int nthreads) {
+    int64_t kv_stride = num_kv_heads * head_dim;
+    int64_t ratio = num_heads / num_kv_heads;
+    int64_t start_t = pkvo_window_start(pos, window);
+    int64_t n = pos + 1 - start_t;
+
+    if (ring_size > 0) {
+        if (n > ring_size) return -1;
+        for (int64_t i = 0; i < n; ++i) {
+            int64_t t = start_t + i;
+            rows[i] = (ring_base + t % ring_size) * kv_stride;
+        }
+    } else {
+        if (pos >= 0 && pos / block_size >= table_len) return -2;
+        for (int64_t i = 0; i < n; ++i) {
+            int64_t t = start_t + i;
+            rows[i] = (block_table[t / block_size] * block_size + t % block_size) * kv_stride;
+        }
+    }
+
+    if (n >= 64 && num_heads >= 4 && (num_heads % 2 == 0) && (ratio % 2 == 0)) {
+        int64_t num_pairs = num_heads / 2;
+#pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static, 1) if (nthreads > 1)
+        for (int64_t t = 0; t < num_pairs; ++t) {
+            int64_t h_start = t * 2;
+            int64_t g = h_start / ratio;
+            eval_head_range(q, k_pool, v_pool, dtype, rows, scores, attn_out, n, g * head_dim,
+                            h_start, h_start + 2, head_dim);
+        }
+    } else {
+        for (int64_t g = 0; g < num_kv_heads; ++g) {
+            int64_t h_first = g * ratio;
+            eval_head_range(q, k_pool, v_pool, dtype, rows, scores, attn_out, n, g * head_dim,
+                            h_first, h_first + ratio, head_dim);
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------- test_attention.mojo:62-117
+ * The engine's pre-refactor loop (full causal, one head at a time). The
+ * reference asserts paged_attention_layer is bit-exact with it.           */
+void pkvo_legacy_paged_attention(const float* q, const void* k_pool, const void* v_pool, int dtype,
+                                 const int64_t* block_table, int64_t block_size, int64_t pos,
+                                 int64_t layer_heads, int64_t layer_kv_heads,
+                                 int64_t layer_head_dim, float* attn_scores, float* attn_out) {
+    int64_t kv_stride = layer_kv_heads * layer_head_dim;
+    int64_t ratio = layer_heads / layer_kv_heads;
+    float kv[8];
+    for (int64_t h = 0; h < layer_heads; ++h) {
+        int64_t h_offset = h * layer_head_dim;
+        int64_t g_offset = (h / ratio) * layer_head_dim;
+        for (int64_t t = 0; t <= pos; ++t) {
+            int64_t off = (block_table[t / block_size] * block_size + t % block_size) * kv_stride +
+                          g_offset;
+            float sv[8] = {0};
+            for (int64_t d = 0; d < layer_head_dim; d += 8) {
+                load8(k_pool, dtype, off + d, kv);
+                for (int j = 0; j < 8; ++j) sv[j] = sv[j] + q[h_offset + d + j] * kv[j];
+            }
+            attn_scores[t] = reduce_add8(sv);
+        }
+        softmax_ref(attn_scores, pos + 1);
+        for (int64_t d = 0; d < layer_head_dim; ++d) attn_out[h_offset + d] = 0.0f;
+        for (int64_t t = 0; t <= pos; ++t) {
+            int64_t off = (block_table[t / block_size] * block_size + t % block_size) * kv_stride +
+                          g_offset;
+            float a = attn_scores[t];
+            for (int64_t d = 0; d < layer_head_dim; d += 8) {
+                load8(v_pool, dtype, off + d, kv);
+                for (int j = 0; j < 8; ++j)
+                    attn_out[h_offset + d + j] = attn_out[h_offset + d + j] + a * kv[j];
+            }
+        }
+    }
+}
+
+/* ------------------------------------------ test_attention.mojo:123-163
+ * Naive float64 attention over keys [start_t, pos].                         */
+void pkvo_attention_f64(const float* q, const void* k_pool, const void* v_pool, int dtype,
+                        const int64_t* block_table, int64_t block_size, int64_t pos,
+                        int64_t start_t, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                        double* out_ref) {
+    int64_t kv_stride = kv_heads * head_dim;
+    int64_t ratio = heads / kv_heads;
+    int64_t n = pos + 1 - start_t;
+    double* s = (double*)malloc(sizeof(double) * (size_t)(n > 0 ? n : 1));
+    for (int64_t h = 0; h < heads; ++h) {
+        int64_t g = h / ratio;
+        double mx = -1e300;
+        for (int64_t i = 0; i < n; ++i) {
+            int64_t t = start_t + i;
+            int64_t row = (block_table[t / block_size] * block_size + t % block_size) * kv_stride +
+                          g * head_dim;
+            double acc = 0.0;
+            for (int64_t d = 0; d < head_dim; ++d)
+                acc += (double)q[h * head_dim + d] * (double)load1(k_pool, dtype, row + d);
+            s[i] = acc;
+            if (acc > mx) mx = acc;
+        }
+        double tot = 0.0;
+        for (int64_t i = 0; i < n; ++i) {
+            s[i] = exp(s[i] - mx);
+            tot += s[i];
+        }
+        for (int64_t d = 0; d < head_dim; ++d) out_ref[h * head_dim + d] = 0.0;
+        for (int64_t i = 0; i < n; ++i) {
+            int64_t t = start_t + i;
+            int64_t row = (block_table[t / block_size] * block_size + t % block_size) * kv_stride +
+                          g * head_dim;
+            double w = s[i] / tot;
+            for (int64_t d = 0; d < head_dim; ++d)
+                out_ref[h * head_dim + d] += w * (double)load1(v_pool, dtype, row + d);
+        }
+    }
+    free(s);
+}
+
+/* -------------------------------------------- test_attention.mojo:27-42 */
+
+uint64_t pkvo_lcg_init(uint64_t seed) {
+    return seed * 6364136223846793005ULL + 1442695040888963407ULL;
+}
+
+/* Fills p[0..n) with uniform [-1, 1) * scale; returns the advanced state. */
+uint64_t pkvo_fill_random(float* p, int64_t n, float scale, uint64_t state) {
+    for (int64_t i = 0; i < n; ++i) {
+        state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+        uint64_t bits = (state >> 40) & 0xFFFFFFULL;
+        float x = (float)bits / (float)0x800000 - 1.0f;
+        p[i] = x * scale;
+    }
+    return state;
+}
+
+/* ------------------------- model_speculative_moe_batched.mojo:789-807
+ * BlockManager: the free list is initialised [0..max-1]; allocate() pops the
+ * back (-1 when empty); free() pushes to the back.                          */
+void pkvo_bm_init(int32_t* free_list, int32_t* free_count, int32_t max_blocks) {
+    for (int32_t i = 0; i < max_blocks; ++i) free_list[i] = i;
+    *free_count = max_blocks;
+}
+
+int32_t pkvo_bm_allocate(int32_t* free_list, int32_t* free_count) {
+    if (*free_count == 0) return -1;
+    *free_count -= 1;
+    return free_list[*free_count];
+}
+
+void pkvo_bm_free(int32_t* free_list, int32_t* free_count, int32_t block_id) {
+    free_list[*free_count] = block_id;
+    *free_count += 1;
+}
+
+/* ------------------------------------------------------------- KV append
+ * For each sequence s in index order (the engine serves sequences one after
+ * another): for each new token b in order, position p = pos[s] + b grows the
+ * table while p // bs >= len(table) (allocate() pops the LIFO back). If a pop
+ * fails the sequence is marked out of blocks (status -1): blocks popped before
+ * the failure stay in its table and none of its K/V rows is written (decode
+ * returns before the copy, :1989-1992; verify sets oom_abort before any write,
+ * :3017-3026; chunked prefill breaks before the layer pass, :2516-2530).
+ * Otherwise the rows row = table[p // bs] * bs + p % bs receive exact copies
+ * of k_new / v_new (:1994-2001).
+ * pos[s] < 0 or n_new[s] <= 0 skips the sequence (status 0); n_new[s] > max_new is
+ * rejected with status -5 (the C ABI's PKV_SEQ_BAD_ARGS).
+ * A table that would exceed table_stride entries gives status -2 and no change.
+ * k_new/v_new: [batch][max_new][kv_stride] in the pool dtype.               */
+void pkvo_append(int dtype, int32_t kv_stride, int32_t block_size, void* k_pool, void* v_pool,
+                 int32_t* tables, int32_t table_stride, int32_t* table_lens, int32_t* free_list,
+                 int32_t* free_count, const int32_t* pos, const int32_t* n_new, int32_t max_new,
+                 const void* k_new, const void* v_new, int32_t batch, int32_t* status) {
+    size_t elt = dtype == PKVO_BF16 ? 2 : 4;
+    for (int32_t s = 0; s < batch; ++s) {
+        status[s] = 0;
+        if (pos[s] < 0 || n_new[s] <= 0) continue;
+        if (n_new[s] > max_new) {
+            status[s] = -5;
+            continue;
+        }
+        int64_t last = (int64_t)pos[s] + n_new[s] - 1;
+        if (last / block_size >= table_stride) {
+            status[s] = -2;
+            continue;
+        }
+        int32_t* table = tables + (int64_t)s * table_stride;
+        int oom = 0;
+        for (int32_t b = 0; b < n_new[s] && !oom; ++b) {
+            int64_t p = (int64_t)pos[s] + b;
+            while (p / block_size >= table_lens[s]) {
+                int32_t blk = pkvo_bm_allocate(free_list, free_count);
+                if (blk < 0) {
+                    oom = 1;
+                    break;
+                }
+                table[table_lens[s]] = blk;
+                table_lens[s] += 1;
+            }
+        }
+        if (oom) {
+            status[s] = -1;
+            continue;
+        }
+        for (int32_t b = 0; b < n_new[s]; ++b) {
+            int64_t p = (int64_t)pos[s] + b;
+            int64_t row = (int64_t)table[p / block_size] * block_size + p % block_size;
+            size_t src = ((size_t)s * max_new + b) * kv_stride * elt;
+            memcpy((char*)k_pool + row * kv_stride * elt, (const char*)k_new + src, kv_stride * elt);
+            memcpy((char*)v_pool + row * kv_stride * elt, (const char*)v_new + src, kv_stride * elt);
+        }
+    }
+}
+
+/* ------------------------------------------------------- rollback / retire
+ * For each sequence s in index order with new_len[s] >= 0: keep
+ * ceil(new_len / bs) blocks (never more than it holds) and free the rest in
+ * ascending logical order, pushing each on the back of the free list. Retire
+ * is new_len = 0 (the engine frees table[0..len) ascending, :3627-3628).
+ * new_len[s] < 0 leaves sequence s untouched. Pool rows are not modified.   */
+void pkvo_rollback(int32_t block_size, int32_t* tables, int32_t table_stride, int32_t* table_lens,
+                   int32_t* free_list, int32_t* free_count, const int32_t* new_len, int32_t batch) {
+    for (int32_t s = 0; s < batch; ++s) {
+        if (new_len[s] < 0) continue;
+        int32_t keep = (new_len[s] + block_size - 1) / block_size;
+        if (keep > table_lens[s]) keep = table_lens[s];
+        int32_t* table = tables + (int64_t)s * table_stride;
+        for (int32_t j = keep; j < table_lens[s]; ++j) pkvo_bm_free(free_list, free_count, table[j]);
+        table_lens[s] = keep;
+    }
+}
+
+/* ---------------------------------------------------- batched attention
+ * q:   [batch][q_len][num_heads][head_dim] fp32
+ * out: [batch][q_len][num_heads][head_dim] fp32
+ * Query j of sequence s sits at position pos[s] + j and attends
+ * [window_start(pos[s] + j), pos[s] + j] through the sequence's table, one
+ * paged_attention_layer call per query (the verify loop calls it per draft
+ * token, :3090-3123). pos[s] < 0 gives zeros (n <= 0, attention.mojo:180-185).
+ * q_scale multiplies q before the call (1.0 = the reference; a power of two is
+ * exact, so a softmax scale of 2^-k is emulated without rounding).
+ * par: 0 = serial over sequences, head-pair tasks on `nthreads` threads
+ *      (reference-faithful); 1 = sequences spread over `nthreads` threads.   */
+int pkvo_attend(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                int32_t block_size, int32_t window, float q_scale, const float* q,
+                const void* k_pool, const void* v_pool, const int32_t* tables,
+                int32_t table_stride, const int32_t* table_lens, const int32_t* pos,
+                int32_t q_len, int32_t batch, float* out, int nthreads, int par) {
+    int64_t max_n = 0;
+    for (int32_t s = 0; s < batch; ++s) {
+        int64_t p = (int64_t)pos[s] + q_len;
+        if (p > max_n) max_n = p;
+    }
+    int64_t hd = (int64_t)num_heads * head_dim;
+    int err = 0;
+    int outer = (par == 1 && nthreads > 1) ? nthreads : 1;
+    int inner = (par == 1) ? 1 : nthreads;
+#pragma omp parallel num_threads(outer) if (outer > 1)
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)(num_heads * (max_n + 1)));
+        int64_t* rows = (int64_t*)malloc(sizeof(int64_t) * (size_t)(max_n + 1));
+        int64_t* tab = (int64_t*)malloc(sizeof(int64_t) * (size_t)(table_stride > 0 ? table_stride : 1));
+        float* qs = (float*)malloc(sizeof(float) * (size_t)hd);
+#pragma omp for schedule(dynamic, 1)
+        for (int32_t s = 0; s < batch; ++s) {
+            for (int32_t i = 0; i < table_stride; ++i) tab[i] = tables[(int64_t)s * table_stride + i];
+            for (int32_t j = 0; j < q_len; ++j) {
+                const float* qj = q + ((int64_t)s * q_len + j) * hd;
+                float* oj = out + ((int64_t)s * q_len + j) * hd;
+                if (pos[s] < 0) {
+                    for (int64_t i = 0; i < hd; ++i) oj[i] = 0.0f;
+                    continue;
+                }
+                for (int64_t i = 0; i < hd; ++i) qs[i] = qj[i] * q_scale;
+                int rc = pkvo_paged_attention_layer(qs, k_pool, v_pool, dtype, tab, table_lens[s],
+                                                    block_size, (int64_t)pos[s] + j, num_heads,
+                                                    num_kv_heads, head_dim, window, scores, rows,
+                                                    oj, 0, 0, inner);
+                if (rc != 0) {
+#pragma omp atomic write
+                    err = rc;
+                }
+            }
+        }
+        free(scores);
+        free(rows);
+        free(tab);
+        free(qs);
+    }
+    return err;
+}
+
+int pkvo_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,85 @@
+"""CPU checks of the C ABI: libpkv.so loads and exports every symbol include/pkv.h
+declares; argument validation runs host-side (no device call is made)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from pkv import lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "pkv.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib.load()
+    names = declared_symbols()
+    assert "pkv_append" in names and "pkv_attend" in names and "pkv_rollback" in names
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in pkv.h but not exported"
+    assert set(names) == set(lib.PROTOTYPES), "ctypes prototypes out of sync with pkv.h"
+
+
+def test_version_and_error_string():
+    L = lib.load()
+    assert L.pkv_version() >> 16 == 1
+    assert isinstance(L.pkv_last_error(), bytes)
+
+
+def _params(**kw):
+    p = lib.PkvParams()
+    vals = dict(num_heads=16, num_kv_heads=8, head_dim=256, block_size=16, num_blocks=64,
+                window=0, scale=1.0, kv_dtype=0, ring_size=0, reserved=0)
+    vals.update(kw)
+    for k, v in vals.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_workspace_size_is_monotone_and_validates():
+    L = lib.load()
+    p = _params()
+    a = L.pkv_workspace_size(ctypes.byref(p), 32, 1, 8192)
+    b = L.pkv_workspace_size(ctypes.byref(p), 32, 1, 32768)
+    assert 0 < a < b
+    w = _params(window=1024)
+    assert L.pkv_workspace_size(ctypes.byref(w), 32, 1, 32768) < b  # window bounds the chunks
+    for bad in (_params(num_kv_heads=3), _params(head_dim=100), _params(ring_size=8),
+                _params(kv_dtype=7), _params(block_size=0)):
+        assert L.pkv_workspace_size(ctypes.byref(bad), 1, 1, 10) == 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(num_kv_heads=3), lib.PKV_ERR_INVALID),
+    (dict(head_dim=96), lib.PKV_ERR_UNSUPPORTED),
+    (dict(ring_size=1024), lib.PKV_ERR_UNSUPPORTED),
+])
+def test_invalid_params_rejected_before_launch(kw, code):
+    L = lib.load()
+    p = _params(**kw)
+    rc = L.pkv_attend(None, ctypes.byref(p), 1, 1, 1, 1, 4, 1, 1, 1, 10, 1, 1, 1 << 20)
+    assert rc == code
+    assert L.pkv_last_error()
+
+
+def test_null_pointers_and_small_workspace_rejected():
+    L = lib.load()
+    p = _params()
+    assert L.pkv_attend(None, ctypes.byref(p), None, 1, 1, 1, 4, 1, 1, 1, 10, 1, 1, 1 << 20) \
+        == lib.PKV_ERR_INVALID
+    assert L.pkv_attend(None, ctypes.byref(p), 1, 1, 1, 1, 4, 1, 1, 1, 10, 1, 1, 16) \
+        == lib.PKV_ERR_WORKSPACE
+    assert L.pkv_rollback(None, ctypes.byref(p), None, 4, 1, 1, 1, 1, 1, None) \
+        == lib.PKV_ERR_INVALID
+    assert L.pkv_append(None, ctypes.byref(p), 1, 1, 1, 4, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 8) \
+        == lib.PKV_ERR_WORKSPACE
+    # verify with too many query rows per kv head (q_len 9 x ratio 2 > 16)
+    assert L.pkv_attend(None, ctypes.byref(p), 1, 1, 1, 1, 4, 1, 9, 1, 10, 1, 1, 1 << 30) \
+        == lib.PKV_ERR_UNSUPPORTED

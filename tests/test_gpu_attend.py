@@ -1,0 +1,229 @@
+"""GPU parity of K2 (split-K paged attention) against the oracle's restatement of
+paged_attention_layer (attention.mojo:240-294), on the reference's own test fixtures
+(test_attention.mojo) and on seeded N(0,1) data. Tolerance: max |x-ref|/(|ref|+1e-3)
+<= 1e-4 for fp32 pools and <= 2e-2 for bf16 pools (oracle on the upcast values)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pkv import BF16, F32, LayerSpec, hip, lib, paged_attention_layer
+from pkv.engine import make_params
+from tests.refcase import BLOCK_SIZE, CAPACITY, NUM_BLOCKS, Fixture
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 2e-2
+
+
+class DevFixture:
+    """The reference Fixture uploaded to the device."""
+
+    def __init__(self, fx: Fixture, kv_dtype=F32):
+        self.fx = fx
+        self.kv_dtype = kv_dtype
+        if kv_dtype == BF16:
+            self.k_host, self.v_host = O.to_bf16(fx.k_pool), O.to_bf16(fx.v_pool)
+        else:
+            self.k_host, self.v_host = fx.k_pool, fx.v_pool
+        self.k = hip.DeviceArray.from_numpy(self.k_host)
+        self.v = hip.DeviceArray.from_numpy(self.v_host)
+        self.table = hip.DeviceArray.from_numpy(fx.table.astype(np.int32))
+        self.q = hip.DeviceArray.from_numpy(fx.q)
+        self.out = hip.DeviceArray((fx.heads * fx.head_dim + 64,), np.float32)
+
+    def refresh(self):
+        self.k.upload(O.to_bf16(self.fx.k_pool) if self.kv_dtype == BF16 else self.fx.k_pool)
+        self.v.upload(O.to_bf16(self.fx.v_pool) if self.kv_dtype == BF16 else self.fx.v_pool)
+
+    def run(self, pos, window):
+        fx = self.fx
+        canary = np.full(fx.heads * fx.head_dim + 64, -12345.678, np.float32)
+        self.out.upload(canary)
+        paged_attention_layer(self.q, self.k, self.v, self.table, BLOCK_SIZE, pos, fx.heads,
+                              fx.kv_heads, fx.head_dim, window, self.out, num_blocks=NUM_BLOCKS,
+                              kv_dtype=self.kv_dtype)
+        o = self.out.numpy()
+        assert np.all(o[fx.heads * fx.head_dim:] == np.float32(-12345.678)), "attn_out overflow"
+        return o[: fx.heads * fx.head_dim]
+
+    def oracle(self, pos, window):
+        return O.paged_attention_layer(self.fx.q, self.k_host, self.v_host, self.fx.table,
+                                       BLOCK_SIZE, pos, self.fx.heads, self.fx.kv_heads,
+                                       self.fx.head_dim, window)
+
+
+@pytest.mark.parametrize("geom", [(16, 2, 512), (16, 8, 256), (8, 8, 64), (12, 4, 256)],
+                         ids=["global", "sliding", "ratio1", "ratio3"])
+@pytest.mark.parametrize("window", [0, 1024])
+def test_fixture_positions_match_oracle(gpu, geom, window):
+    print(f"[attend] geom={geom} window={window}", flush=True)
+    d = DevFixture(Fixture(*geom, seed=42, k_scale=0.25))
+    for p in [0, 1, 15, 16, 17, 63, 64, 99, 255, 256, 257, 777, 1023, 1024, 1500, CAPACITY - 1]:
+        err = O.max_rel_err(d.run(p, window), d.oracle(p, window))
+        assert err <= TOL_F32, (p, err)
+
+
+def test_short_windows_and_f64(gpu):
+    print("[attend] short windows", flush=True)
+    d = DevFixture(Fixture(16, 8, 256, seed=99, k_scale=0.25))
+    for p in [1024, 1025, 1500, 2047, CAPACITY - 1]:
+        for w in [1, 7, 1024]:
+            got = d.run(p, w)
+            assert O.max_rel_err(got, d.oracle(p, w)) <= TOL_F32
+        assert O.max_rel_err(d.run(p, 1024), d.fx.run_reference(p, p - 1023)) < 1e-4
+
+
+def test_single_key_is_value_row(gpu):
+    d = DevFixture(Fixture(16, 8, 256, seed=4, k_scale=1.0))
+    out = d.run(777, 1)
+    r = d.fx.row_of(777)
+    for h in range(16):
+        g = h // 2
+        np.testing.assert_array_equal(out[h * 256:(h + 1) * 256],
+                                      d.fx.v_pool[r + g * 256:r + (g + 1) * 256])
+
+
+def test_window_edges_planted(gpu):
+    # test_attention.mojo:324-365 and :440-497 on the GPU.
+    print("[attend] planted keys", flush=True)
+    fx = Fixture(16, 8, 256, seed=3, k_scale=0.01)
+    d = DevFixture(fx)
+    pos = 2000
+    fx.plant(pos - 1024)
+    d.refresh()
+    assert np.all(np.abs(d.run(pos, 1024)) < 10.0)
+    fx.plant(pos - 1023)
+    d.refresh()
+    assert np.all(d.run(pos, 1024) > 900.0)
+    fx2 = Fixture(16, 8, 256, seed=21, k_scale=0.01)
+    pos2 = 1024 + 16 * 3 + 1023
+    start = O.window_start(pos2, 1024)
+    fx2.plant(start - 1)
+    d2 = DevFixture(fx2)
+    assert np.all(np.abs(d2.run(pos2, 1024)) < 10.0)
+    fx2.plant(start)
+    d2.refresh()
+    assert np.all(d2.run(pos2, 1024) > 900.0)
+    fx3 = Fixture(16, 8, 256, seed=22, k_scale=0.01)
+    fx3.plant(1777)
+    assert np.all(DevFixture(fx3).run(1777, 1024) > 900.0)
+
+
+def test_large_scores_finite(gpu):
+    d = DevFixture(Fixture(16, 2, 512, seed=11, k_scale=4.0))
+    for p in [0, 300, CAPACITY - 1]:
+        out = d.run(p, 0)
+        assert np.all(np.isfinite(out))
+        assert O.max_rel_err(out, d.oracle(p, 0)) <= TOL_F32
+
+
+@pytest.mark.parametrize("geom", [(16, 8, 256), (16, 2, 512)])
+def test_bf16_pools(gpu, geom):
+    print(f"[attend] bf16 {geom}", flush=True)
+    d = DevFixture(Fixture(*geom, seed=5, k_scale=0.5), kv_dtype=BF16)
+    for p in [0, 100, 1023, 2047, CAPACITY - 1]:
+        err = O.max_rel_err(d.run(p, 0), d.oracle(p, 0))
+        assert err <= TOL_BF16, (p, err)
+        assert err <= 1e-4  # same upcast values and fp32 math: far inside the bf16 bound
+
+
+def _batched_case(rng, B, q_len, ctx, hq, hkv, d, bs, window, kv_dtype, scale):
+    kvs = hkv * d
+    blocks_per = [(int(c) + q_len + bs - 1) // bs for c in ctx]
+    nb = sum(blocks_per) + 8
+    stride = max(blocks_per) + 2
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((B, stride), np.int32)
+    lens = np.zeros(B, np.int32)
+    off = 0
+    for s in range(B):
+        tables[s, :blocks_per[s]] = perm[off:off + blocks_per[s]]
+        lens[s] = blocks_per[s]
+        off += blocks_per[s]
+    k = rng.standard_normal(nb * bs * kvs, dtype=np.float32)
+    v = rng.standard_normal(nb * bs * kvs, dtype=np.float32)
+    if kv_dtype == BF16:
+        k, v = O.to_bf16(k), O.to_bf16(v)
+    q = rng.standard_normal((B, q_len, hq, d), dtype=np.float32)
+    pos = np.asarray(ctx, np.int32)
+    ref = O.attend(q, k, v, tables, lens, pos, q_len, hq, hkv, d, bs, window, scale=scale,
+                   nthreads=O.max_threads(), par=1)
+    spec = LayerSpec(hq, hkv, d, window, kv_dtype)
+    p = make_params(spec, bs, nb, scale)
+    import ctypes
+    max_pos = int(pos.max()) + q_len - 1
+    ws_bytes = lib.load().pkv_workspace_size(ctypes.byref(p), B, q_len, max_pos)
+    ws = hip.DeviceArray((ws_bytes,), np.uint8, zero=True)
+    dk, dv = hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(v)
+    dt, dq = hip.DeviceArray.from_numpy(tables), hip.DeviceArray.from_numpy(q)
+    dpos = hip.DeviceArray.from_numpy(pos)
+    out = hip.DeviceArray((B, q_len, hq, d), np.float32)
+    for rep in range(2):  # the second call reuses the self-resetting chunk counters
+        lib.call("pkv_attend", None, ctypes.byref(p), dq.ptr, dk.ptr, dv.ptr, dt.ptr, stride,
+                 dpos.ptr, q_len, B, max_pos, out.ptr, ws.ptr, ws.nbytes)
+        got = out.numpy()
+        err = O.max_rel_err(got, ref)
+        assert err <= (TOL_BF16 if kv_dtype == BF16 else TOL_F32), (rep, err)
+        assert err <= 1e-4
+    return got
+
+
+@pytest.mark.parametrize("window", [0, 1024])
+def test_batched_mixed_contexts(gpu, window):
+    print(f"[attend] batched mixed window={window}", flush=True)
+    rng = np.random.default_rng(7)
+    ctx = rng.integers(128, 3000, 12)
+    ctx[0], ctx[1] = 0, 255  # single key and exactly one chunk
+    _batched_case(rng, 12, 1, ctx, 16, 8, 256, 16, window, F32, 0.0625)
+
+
+@pytest.mark.parametrize("q_len", [2, 4, 8])
+def test_verify_queries_causal(gpu, q_len):
+    print(f"[attend] verify q_len={q_len}", flush=True)
+    rng = np.random.default_rng(q_len)
+    ctx = rng.integers(500, 2500, 6)
+    _batched_case(rng, 6, q_len, ctx, 16, 8, 256, 16, 0, F32, 0.0625)
+
+
+def test_verify_sliding_bf16(gpu):
+    rng = np.random.default_rng(11)
+    ctx = rng.integers(900, 2100, 5)
+    _batched_case(rng, 5, 4, ctx, 16, 8, 256, 16, 1024, BF16, 0.0625)
+
+
+def test_gqa8_d512(gpu):
+    rng = np.random.default_rng(12)
+    ctx = rng.integers(1, 4000, 4)
+    _batched_case(rng, 4, 1, ctx, 16, 2, 512, 16, 0, F32, 1.0)
+
+
+def test_inactive_sequence_gives_zeros_and_bad_table_gives_nan(gpu):
+    print("[attend] inactive / bad table", flush=True)
+    import ctypes
+    rng = np.random.default_rng(3)
+    B, hq, hkv, d, bs, nb, stride = 3, 16, 8, 256, 16, 64, 8
+    spec = LayerSpec(hq, hkv, d)
+    p = make_params(spec, bs, nb, 1.0)
+    tables = rng.integers(0, nb, (B, stride)).astype(np.int32)
+    tables[2, 3] = nb + 5  # out of the pool
+    k = hip.DeviceArray((nb * bs * hkv * d,), np.float32, zero=True)
+    q = hip.DeviceArray.from_numpy(rng.standard_normal((B, 1, hq, d), dtype=np.float32))
+    pos = np.array([40, -1, 60], np.int32)
+    out = hip.DeviceArray((B, 1, hq, d), np.float32)
+    ws_bytes = lib.load().pkv_workspace_size(ctypes.byref(p), B, 1, 127)
+    ws = hip.DeviceArray((ws_bytes,), np.uint8, zero=True)
+    lib.call("pkv_attend", None, ctypes.byref(p), q.ptr, k.ptr, k.ptr,
+             hip.DeviceArray.from_numpy(tables).ptr, stride,
+             hip.DeviceArray.from_numpy(pos).ptr, 1, B, 127, out.ptr, ws.ptr, ws.nbytes)
+    o = out.numpy()
+    np.testing.assert_allclose(o[0], 0.0, atol=0)  # zero V rows
+    assert np.all(o[1] == 0.0)
+    assert np.all(np.isnan(o[2]))
+    # pos beyond max_pos -> NaN, never an out-of-grid read
+    pos2 = np.array([40, 200, 0], np.int32)
+    lib.call("pkv_attend", None, ctypes.byref(p), q.ptr, k.ptr, k.ptr,
+             hip.DeviceArray.from_numpy(np.clip(tables, 0, nb - 1)).ptr, stride,
+             hip.DeviceArray.from_numpy(pos2).ptr, 1, B, 127, out.ptr, ws.ptr, ws.nbytes)
+    o = out.numpy()
+    assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[0])) and np.all(np.isfinite(o[2]))

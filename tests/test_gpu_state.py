@@ -1,0 +1,124 @@
+"""GPU parity of K1 (fused allocate + scatter) and K5 (rollback / retire) against the
+oracle's restatement of the engine's bookkeeping: block tables, table lengths, the free
+list and every pool byte must match bit-exactly."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pkv import BF16, F32, LayerSpec, PagedKVCache, hip, lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _compare(cache: PagedKVCache, st: O.CacheState, layers=(0,), pools=True):
+    snap = cache.snapshot()
+    np.testing.assert_array_equal(snap["table_lens"], st.table_lens)
+    np.testing.assert_array_equal(snap["tables"], st.tables)
+    np.testing.assert_array_equal(snap["free_list"], st.free_list)
+    if pools:
+        for l in layers:
+            np.testing.assert_array_equal(cache.k_pools[l].numpy().reshape(-1), st.k_pools[l])
+            np.testing.assert_array_equal(cache.v_pools[l].numpy().reshape(-1), st.v_pools[l])
+
+
+def _mk(kv_dtype, nseq, bs, num_blocks, stride, kvh=2, d=64, layers=1):
+    spec = LayerSpec(num_heads=kvh * 2, num_kv_heads=kvh, head_dim=d, kv_dtype=kv_dtype)
+    cache = PagedKVCache([spec] * layers, block_size=bs, num_blocks=num_blocks, max_seqs=nseq,
+                         max_blocks_per_seq=stride)
+    st = O.CacheState(layers, spec.kv_stride, bs, num_blocks, nseq, stride,
+                      dtype=np.uint16 if kv_dtype == BF16 else np.float32)
+    return spec, cache, st
+
+
+@pytest.mark.parametrize("kv_dtype", [F32, BF16])
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_append_rollback_sequences(gpu, kv_dtype, seed):
+    print(f"[state] kv={kv_dtype} seed={seed}", flush=True)
+    rng = np.random.default_rng(seed)
+    nseq, bs, num_blocks, stride, max_new = 7, 4, 40, 24, 9
+    spec, cache, st = _mk(kv_dtype, nseq, bs, num_blocks, stride, layers=2)
+    length = np.zeros(nseq, np.int64)
+    npdt = np.uint16 if kv_dtype == BF16 else np.float32
+    kd = hip.DeviceArray((nseq, max_new, spec.kv_stride), npdt)
+    vd = hip.DeviceArray((nseq, max_new, spec.kv_stride), npdt)
+    for step in range(40):
+        if rng.random() < 0.7:
+            n_new = rng.integers(0, max_new + 1, nseq).astype(np.int32)
+            pos = length.astype(np.int32).copy()
+            pos[rng.random(nseq) < 0.1] = -1  # inactive slots
+            raw = rng.standard_normal((2, nseq, max_new, spec.kv_stride)).astype(np.float32)
+            k = O.to_bf16(raw[0]) if kv_dtype == BF16 else raw[0]
+            v = O.to_bf16(raw[1]) if kv_dtype == BF16 else raw[1]
+            kd.upload(k)
+            vd.upload(v)
+            layer = int(rng.integers(0, 2))
+            ref_status = st.append(layer, pos, n_new, k, v, max_new)
+            status = cache.append(layer, pos, n_new, kd, vd, max_new).numpy()
+            np.testing.assert_array_equal(status, ref_status, err_msg=f"step {step}")
+            ok = (ref_status == 0) & (pos >= 0)
+            length[ok] += n_new[ok]
+        else:
+            new_len = np.full(nseq, -1, np.int32)
+            pick = rng.random(nseq) < 0.5
+            new_len[pick] = [rng.integers(0, length[s] + 1) for s in np.nonzero(pick)[0]]
+            length[pick] = new_len[pick]
+            st.rollback(new_len)
+            cache.rollback(new_len)
+        _compare(cache, st, layers=(0, 1), pools=(step % 5 == 4))
+    _compare(cache, st, layers=(0, 1))
+    cache.free()
+
+
+def test_out_of_blocks_and_table_full(gpu):
+    print("[state] oom / table full", flush=True)
+    nseq, bs, num_blocks, stride = 4, 4, 6, 3
+    spec, cache, st = _mk(F32, nseq, bs, num_blocks, stride)
+    k = np.arange(nseq * 13 * spec.kv_stride, dtype=np.float32).reshape(nseq, 13, -1)
+    kd, vd = hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(-k)
+    pos = np.array([0, 0, 0, 0], np.int32)
+    n_new = np.array([5, 13, 9, 2], np.int32)  # needs 2, 4 (> stride 3: full), 3, 1
+    ref = st.append(0, pos, n_new, k, -k, 13)
+    got = cache.append(0, pos, n_new, kd, vd, 13).numpy()
+    np.testing.assert_array_equal(got, ref)
+    assert list(ref) == [lib.PKV_SEQ_OK, lib.PKV_SEQ_TABLE_FULL, lib.PKV_SEQ_OK, lib.PKV_SEQ_OK]
+    _compare(cache, st)
+    # The pool now has 0 free blocks: a second round runs dry part-way.
+    pos2 = np.array([5, -1, 9, 2], np.int32)
+    n2 = np.array([4, 0, 4, 7], np.int32)
+    ref = st.append(0, pos2, n2, k, -k, 13)
+    got = cache.append(0, pos2, n2, kd, vd, 13).numpy()
+    np.testing.assert_array_equal(got, ref)
+    assert lib.PKV_SEQ_OUT_OF_BLOCKS in list(ref)
+    _compare(cache, st)
+    cache.free()
+
+
+def test_config1_append_into_new_block(gpu):
+    # Config 1 bookkeeping: 256-block pool, the sequence owns a seeded permutation prefix
+    # of 32 blocks (512 tokens); appending at pos 512 pops the LIFO back of the free list.
+    print("[state] config 1 append", flush=True)
+    rng = np.random.default_rng(1)
+    bs, nb = 16, 256
+    spec = LayerSpec(16, 8, 256)
+    cache = PagedKVCache([spec], block_size=bs, num_blocks=nb, max_seqs=1, max_blocks_per_seq=64)
+    st = O.CacheState(1, spec.kv_stride, bs, nb, 1, 64)
+    perm = rng.permutation(nb).astype(np.int32)
+    table = perm[:32]
+    free = np.sort(perm[32:]).astype(np.int32)
+    st.tables[0, :32] = table
+    st.table_lens[0] = 32
+    st.bm.free_list[:free.size] = free
+    st.bm.count[0] = free.size
+    cache.tables.upload(st.tables)
+    cache.table_lens.upload(st.table_lens)
+    fl = np.zeros(nb, np.int32)
+    fl[:free.size] = free
+    cache.free_list.upload(fl)
+    cache.free_count.upload(np.array([free.size], np.int32))
+    k = rng.standard_normal((1, 1, spec.kv_stride)).astype(np.float32)
+    v = rng.standard_normal((1, 1, spec.kv_stride)).astype(np.float32)
+    st.append(0, [512], [1], k, v, 1)
+    cache.append(0, [512], [1], hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(v), 1)
+    assert st.table_lens[0] == 33 and st.tables[0, 32] == free[-1]
+    _compare(cache, st)
+    cache.free()
