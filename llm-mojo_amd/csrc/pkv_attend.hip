@@ -5,17 +5,26 @@
 // head (GQA group x verify queries, <= 16 rows) are evaluated together, so every K/V
 // byte of the chunk is read from HBM exactly once:
 //   1. Q rows -> registers (each lane holds the slice of D it multiplies).
-//   2. Scores: each wave streams K rows of its tokens with 16-byte loads (one row of a
-//      head = 64 x 16 B for fp32 D=256), forms per-lane partial dots for every row and
-//      reduces them across the lanes that share the row; masked scores go to LDS.
+//   2. Scores: each wave streams K rows of its tokens with 16-byte loads (one fp32 row of
+//      a D=256 head = 64 lanes x 16 B), forms per-lane partial dots for U tokens x R rows
+//      and reduces all of them across the row's lanes with a halving exchange (each
+//      step sends half of the values, so U*R dots cost ~U*R shuffles instead of
+//      U*R*log2(lanes)). Masked scores go to LDS.
 //   3. Chunk softmax statistics: m = max, p = exp(s - m), l = sum p (in LDS).
-//   4. PV: each wave streams V rows and accumulates p * v in registers; waves are
-//      summed through LDS.
+//   4. PV: each wave streams V rows and accumulates p * v in registers; the per-wave
+//      sums are added in LDS one wave after another.
 //   5. A single-chunk sequence writes o / (l + 1e-10) directly. Otherwise the chunk
 //      writes (m, l, o) to the workspace and the last chunk of (sequence, kv head) to
 //      finish (atomic counter) merges all chunks:
 //      out = sum_c o_c e^(m_c - M) / (sum_c l_c e^(m_c - M) + 1e-10), M = max_c m_c,
 //      which is the reference's softmax(x)_i = e^(x_i - max) / (sum + 1e-10).
+//
+// Arithmetic: fp32 pools accumulate in double (scores, exponentials, PV sums, merge),
+// so the output is the exact attention rounded once to fp32; the fp32 reference path
+// carries ~1e-7 absolute error of its own, and the parity bound (1e-4 relative with a
+// 1e-3 floor) leaves no room for a second fp32 error of that size. On CDNA a non-packed
+// double FMA issues at the fp32 rate, and the kernel is HBM-bound. bf16 pools (2e-2
+// bound, twice the tokens per byte) accumulate in fp32.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -29,60 +38,104 @@ constexpr int kNT = kBlockThreads;
 constexpr int kNW = kNT / kWave;  // waves per workgroup
 constexpr int kMaxChunk = 256;    // keys per chunk (compile-time LDS bound)
 constexpr int kMaxPages = 257;    // pages one chunk can touch (block_size >= 1)
-constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename KV>
 struct KVT;
 template <>
 struct KVT<float> {
     static constexpr int VE = 4;  // elements per 16-byte vector
+    using Acc = double;
 };
 template <>
 struct KVT<uint16_t> {  // bf16 bits
     static constexpr int VE = 8;
+    using Acc = float;
 };
 
 template <int D, typename KV>
 struct Lay {
     static constexpr int VE = KVT<KV>::VE;
-    static constexpr int VPR = D / VE;                  // 16-byte vectors per head row
+    static constexpr int VPR = D / VE;                     // 16-byte vectors per head row
     static constexpr int LPR = VPR < kWave ? VPR : kWave;  // lanes sharing one token row
-    static constexpr int NLD = VPR / LPR;               // 16-byte loads per lane per row
-    static constexpr int TPW = kWave / LPR;             // tokens per wave per load step
-    static constexpr int EPL = NLD * VE;                // row elements held per lane
+    static constexpr int NLD = VPR / LPR;                  // 16-byte loads per lane per row
+    static constexpr int TPW = kWave / LPR;                // tokens per wave per load step
+    static constexpr int EPL = NLD * VE;                   // row elements held per lane
     static_assert(VPR % LPR == 0, "row must split evenly over lanes");
 };
 
-// Unpack one 16-byte vector into VE floats.
-__device__ inline void unpack(const uint4& v, float* out, float) {
-    out[0] = __uint_as_float(v.x);
-    out[1] = __uint_as_float(v.y);
-    out[2] = __uint_as_float(v.z);
-    out[3] = __uint_as_float(v.w);
+// Unpack one 16-byte vector into VE values.
+template <typename A>
+__device__ inline void unpack(const uint4& v, A* out, float) {
+    out[0] = (A)__uint_as_float(v.x);
+    out[1] = (A)__uint_as_float(v.y);
+    out[2] = (A)__uint_as_float(v.z);
+    out[3] = (A)__uint_as_float(v.w);
 }
-__device__ inline void unpack(const uint4& v, float* out, uint16_t) {
-    out[0] = bf16_lo(v.x);
-    out[1] = bf16_hi(v.x);
-    out[2] = bf16_lo(v.y);
-    out[3] = bf16_hi(v.y);
-    out[4] = bf16_lo(v.z);
-    out[5] = bf16_hi(v.z);
-    out[6] = bf16_lo(v.w);
-    out[7] = bf16_hi(v.w);
+template <typename A>
+__device__ inline void unpack(const uint4& v, A* out, uint16_t) {
+    out[0] = (A)bf16_lo(v.x);
+    out[1] = (A)bf16_hi(v.x);
+    out[2] = (A)bf16_lo(v.y);
+    out[3] = (A)bf16_hi(v.y);
+    out[4] = (A)bf16_lo(v.z);
+    out[5] = (A)bf16_hi(v.z);
+    out[6] = (A)bf16_lo(v.w);
+    out[7] = (A)bf16_hi(v.w);
 }
 
-template <int W>
-__device__ inline float reduce_sum_lanes(float v) {
+__device__ inline double exp_acc(double x) { return exp(x); }
+__device__ inline float exp_acc(float x) { return expf(x); }
+
+// Sum of N values per lane across each aligned group of W lanes (W a power of two).
+// Halving exchange: at offset O a lane keeps one half of its values (upper half if
+// lane & O) and receives the partner's copy of that half. When it returns, lane `l`
+// holds F = max(1, N / W) totals, those of value indices base(l) .. base(l) + F - 1.
+template <int N, int O, typename T>
+struct XRed {
+    static __device__ inline void run(T* v, int lane) {
+        if constexpr (O == 0) {
+            return;
+        } else if constexpr (N == 1) {
+            v[0] += __shfl_xor(v[0], O);
+            XRed<1, O / 2, T>::run(v, lane);
+        } else {
+            const bool upper = (lane & O) != 0;
 #pragma unroll
-    for (int off = W / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+            for (int i = 0; i < N / 2; ++i) {
+                T send = upper ? v[i] : v[i + N / 2];
+                T keep = upper ? v[i + N / 2] : v[i];
+                v[i] = keep + __shfl_xor(send, O);
+            }
+            XRed<N / 2, O / 2, T>::run(v, lane);
+        }
+    }
+};
+
+template <int N, int W>
+__device__ inline int xred_base(int lane) {
+    int base = 0, n = N;
+#pragma unroll
+    for (int o = W / 2; o >= 1; o >>= 1) {
+        if (n > 1) {
+            if (lane & o) base += n / 2;
+            n /= 2;
+        }
+    }
+    return base;
+}
+
+template <typename T>
+__device__ inline T wave_max(T v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmax(v, __shfl_xor(v, off));
     return v;
 }
-__device__ inline float wave_max(float v) {
+template <typename T>
+__device__ inline T wave_sum(T v) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
     return v;
 }
-__device__ inline float wave_sum(float v) { return reduce_sum_lanes<64>(v); }
 
 struct AttendArgs {
     const float* q;
@@ -102,8 +155,8 @@ struct AttendArgs {
     float scale;
     int32_t chunk;
     int32_t max_chunks;
-    float* part_ml;
-    float* part_o;
+    void* part_ml;  // Acc pairs (m, l) per (row, chunk)
+    void* part_o;   // Acc [D] per (row, chunk)
     int32_t* counters;
     float* out;
 };
@@ -118,21 +171,25 @@ __device__ inline size_t out_index(const AttendArgs& a, int s, int g, int r, int
 template <int D, typename KV, int R>
 __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     using L = Lay<D, KV>;
+    using Acc = typename KVT<KV>::Acc;
     constexpr int EPL = L::EPL;
     constexpr int NLD = L::NLD;
     constexpr int LPR = L::LPR;
     constexpr int TPW = L::TPW;
     constexpr int VE = L::VE;
-    // Token steps kept in flight per wave (bounded by register pressure).
-    constexpr int U = (R * EPL <= 16) ? 8 : ((R * EPL <= 32) ? 4 : 2);
+    constexpr int AW = sizeof(Acc) / 4;  // 32-bit registers per accumulator
+    // Token steps kept in flight per wave, bounded by register pressure.
+    constexpr int U = (R * EPL * AW <= 16) ? 8 : ((R * EPL * AW <= 32) ? 4 : 2);
+    constexpr int NV = U * R;  // dots reduced together
+    constexpr int F = NV >= LPR ? NV / LPR : 1;
     constexpr int SMEM_SCORES = R * kMaxChunk;
-    constexpr int SMEM_RED = kNW * TPW * R * D;
+    constexpr int SMEM_RED = R * D;
     constexpr int SMEM = SMEM_SCORES > SMEM_RED ? SMEM_SCORES : SMEM_RED;
 
-    __shared__ float smem[SMEM];
+    __shared__ Acc smem[SMEM];
     __shared__ int s_page[kMaxPages];
-    __shared__ float s_m[R], s_l[R];
-    __shared__ int s_flag;
+    __shared__ Acc s_m[R], s_l[R];
+    __shared__ int s_flag, s_last;
 
     const int c = blockIdx.x;
     const int g = blockIdx.y;
@@ -181,7 +238,7 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     }
 
     // Q rows -> registers (scaled). Rows beyond `rows` stay zero.
-    float qr[R][EPL];
+    Acc qr[R][EPL];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (r < rows) {
@@ -192,15 +249,15 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
 #pragma unroll
                 for (int e = 0; e < VE; e += 4) {
                     float4 v = *reinterpret_cast<const float4*>(qp + d0 + e);
-                    qr[r][i * VE + e + 0] = v.x * a.scale;
-                    qr[r][i * VE + e + 1] = v.y * a.scale;
-                    qr[r][i * VE + e + 2] = v.z * a.scale;
-                    qr[r][i * VE + e + 3] = v.w * a.scale;
+                    qr[r][i * VE + e + 0] = (Acc)v.x * (Acc)a.scale;
+                    qr[r][i * VE + e + 1] = (Acc)v.y * (Acc)a.scale;
+                    qr[r][i * VE + e + 2] = (Acc)v.z * (Acc)a.scale;
+                    qr[r][i * VE + e + 3] = (Acc)v.w * (Acc)a.scale;
                 }
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) qr[r][e] = 0.f;
+            for (int e = 0; e < EPL; ++e) qr[r][e] = (Acc)0;
         }
     }
     __syncthreads();
@@ -214,8 +271,10 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
         return reinterpret_cast<const uint4*>(pool + (row * row_elems + head_off) * sizeof(KV));
     };
 
-    float* s_sc = smem;  // [R][kMaxChunk] scores, then probabilities
+    Acc* s_sc = smem;  // [R][kMaxChunk] scores, then probabilities
     const int step = kNW * TPW;
+    const int base_idx = xred_base<NV, LPR>(rl);
+    constexpr int kPlainMask = NV >= LPR ? 0 : (LPR / NV) - 1;
 
     // ---- scores
     for (int base = wave * TPW; base < ntok; base += step * U) {
@@ -232,23 +291,32 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
                 for (int i = 0; i < NLD; ++i) kv[u][i] = make_uint4(0, 0, 0, 0);
             }
         }
+        Acc dots[NV];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float kf[EPL];
+            Acc kf[EPL];
 #pragma unroll
-            for (int i = 0; i < NLD; ++i) unpack(kv[u][i], kf + i * VE, KV());
-            const int tok = base + u * step + sub;
-            const int t = t0 + tok;
+            for (int i = 0; i < NLD; ++i) unpack<Acc>(kv[u][i], kf + i * VE, KV());
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                float acc = 0.f;
+                Acc acc = (Acc)0;
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) acc = fmaf(qr[r][e], kf[e], acc);
-                acc = reduce_sum_lanes<LPR>(acc);
-                if (r < rows && rl == 0 && tok < ntok) {
+                for (int e = 0; e < EPL; ++e) acc = fma(qr[r][e], kf[e], acc);
+                dots[u * R + r] = acc;
+            }
+        }
+        XRed<NV, LPR / 2, Acc>::run(dots, rl);
+        if ((rl & kPlainMask) == 0) {
+#pragma unroll
+            for (int f = 0; f < F; ++f) {
+                const int idx = base_idx + f;
+                const int u = idx / R, r = idx % R;
+                const int tok = base + u * step + sub;
+                if (r < rows && tok < ntok) {
+                    const int t = t0 + tok;
                     const int pq = pos0 + r / a.G;  // this row's query position
                     const bool ok = t <= pq && t >= window_start(pq, a.window);
-                    s_sc[r * kMaxChunk + tok] = ok ? acc : -INFINITY;
+                    s_sc[r * kMaxChunk + tok] = ok ? dots[f] : (Acc)-INFINITY;
                 }
             }
         }
@@ -257,13 +325,13 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
 
     // ---- chunk softmax statistics (one wave per row)
     for (int r = wave; r < rows; r += kNW) {
-        float m = -INFINITY;
-        for (int i = lane; i < ntok; i += kWave) m = fmaxf(m, s_sc[r * kMaxChunk + i]);
+        Acc m = (Acc)-INFINITY;
+        for (int i = lane; i < ntok; i += kWave) m = fmax(m, s_sc[r * kMaxChunk + i]);
         m = wave_max(m);
-        float l = 0.f;
+        Acc l = (Acc)0;
         for (int i = lane; i < ntok; i += kWave) {
-            float sc = s_sc[r * kMaxChunk + i];
-            float p = (m == -INFINITY) ? 0.f : exp2f((sc - m) * kLog2e);
+            Acc sc = s_sc[r * kMaxChunk + i];
+            Acc p = (m == (Acc)-INFINITY) ? (Acc)0 : exp_acc(sc - m);
             s_sc[r * kMaxChunk + i] = p;
             l += p;
         }
@@ -276,11 +344,11 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     __syncthreads();
 
     // ---- PV
-    float acc[R][EPL];
+    Acc acc[R][EPL];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[r][e] = 0.f;
+        for (int e = 0; e < EPL; ++e) acc[r][e] = (Acc)0;
     for (int base = wave * TPW; base < ntok; base += step * U) {
         uint4 vv[U][NLD];
 #pragma unroll
@@ -299,73 +367,77 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
         for (int u = 0; u < U; ++u) {
             const int tok = base + u * step + sub;
             if (tok < ntok) {
-                float vf[EPL];
+                Acc vf[EPL];
 #pragma unroll
-                for (int i = 0; i < NLD; ++i) unpack(vv[u][i], vf + i * VE, KV());
+                for (int i = 0; i < NLD; ++i) unpack<Acc>(vv[u][i], vf + i * VE, KV());
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const float p = r < rows ? s_sc[r * kMaxChunk + tok] : 0.f;
+                    const Acc p = r < rows ? s_sc[r * kMaxChunk + tok] : (Acc)0;
 #pragma unroll
-                    for (int e = 0; e < EPL; ++e) acc[r][e] = fmaf(p, vf[e], acc[r][e]);
+                    for (int e = 0; e < EPL; ++e) acc[r][e] = fma(p, vf[e], acc[r][e]);
                 }
             }
         }
     }
-    __syncthreads();  // all waves done reading probabilities: smem becomes the reduction buffer
+    // Token slots of one wave hold the same d range: fold them first.
+#pragma unroll
+    for (int o = LPR; o < kWave; o <<= 1)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[r][e] += __shfl_xor(acc[r][e], o);
+    __syncthreads();  // all waves done reading probabilities: smem becomes red[R][D]
 
-    // ---- cross-wave / cross-slot reduction: red[wave * TPW + sub][r][d]
-    float* red = smem;
+    // ---- waves add their sums into red[R][D] one after another
+    Acc* red = smem;
+    for (int w = 0; w < kNW; ++w) {
+        if (wave == w && sub == 0) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (r < rows) {
+            for (int r = 0; r < R; ++r) {
+                if (r < rows) {
 #pragma unroll
-            for (int i = 0; i < NLD; ++i) {
-                const int d0 = (i * LPR + rl) * VE;
-                float* dst = red + ((size_t)(wave * TPW + sub) * R + r) * D + d0;
+                    for (int i = 0; i < NLD; ++i) {
+                        const int d0 = (i * LPR + rl) * VE;
+                        Acc* dst = red + (size_t)r * D + d0;
 #pragma unroll
-                for (int e = 0; e < VE; e += 4)
-                    *reinterpret_cast<float4*>(dst + e) =
-                        make_float4(acc[r][i * VE + e], acc[r][i * VE + e + 1],
-                                    acc[r][i * VE + e + 2], acc[r][i * VE + e + 3]);
+                        for (int e = 0; e < VE; ++e)
+                            dst[e] = (w == 0 ? (Acc)0 : dst[e]) + acc[r][i * VE + e];
+                    }
+                }
             }
         }
+        __syncthreads();
     }
-    __syncthreads();
 
     const bool bad = s_flag != 0;
     if (nch == 1) {
         for (int idx = tid; idx < rows * D; idx += kNT) {
             const int r = idx / D, d = idx % D;
-            float o = 0.f;
-#pragma unroll
-            for (int w = 0; w < kNW * TPW; ++w) o += red[((size_t)w * R + r) * D + d];
-            float res = o / (s_l[r] + 1e-10f);
-            a.out[out_index(a, s, g, r, d, D)] = bad ? __builtin_nanf("") : res;
+            Acc res = red[(size_t)r * D + d] / (s_l[r] + (Acc)1e-10);
+            a.out[out_index(a, s, g, r, d, D)] = bad ? __builtin_nanf("") : (float)res;
         }
         return;
     }
 
     // Partial (m, l, o) of this chunk for each row.
+    Acc* part_o = static_cast<Acc*>(a.part_o);
+    Acc* part_ml = static_cast<Acc*>(a.part_ml);
     const size_t row_base = ((size_t)s * a.q_len) * a.Hq;  // first row of sequence s
     for (int idx = tid; idx < rows * D; idx += kNT) {
         const int r = idx / D, d = idx % D;
-        float o = 0.f;
-#pragma unroll
-        for (int w = 0; w < kNW * TPW; ++w) o += red[((size_t)w * R + r) * D + d];
         const int j = r / a.G, h = g * a.G + r % a.G;
         const size_t prow = row_base + (size_t)j * a.Hq + h;
-        a.part_o[(prow * a.max_chunks + c) * D + d] = o;
+        part_o[(prow * a.max_chunks + c) * D + d] = red[(size_t)r * D + d];
     }
     if (tid < rows) {
         const int r = tid;
         const int j = r / a.G, h = g * a.G + r % a.G;
         const size_t prow = row_base + (size_t)j * a.Hq + h;
-        a.part_ml[(prow * a.max_chunks + c) * 2 + 0] = bad ? __builtin_nanf("") : s_m[r];
-        a.part_ml[(prow * a.max_chunks + c) * 2 + 1] = s_l[r];
+        part_ml[(prow * a.max_chunks + c) * 2 + 0] = bad ? (Acc)__builtin_nan("") : s_m[r];
+        part_ml[(prow * a.max_chunks + c) * 2 + 1] = s_l[r];
     }
 
     // Last chunk of (s, g) merges.
-    __shared__ int s_last;
     __syncthreads();
     if (tid == 0) {
         __threadfence();
@@ -381,45 +453,45 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     constexpr int kWTile = 256;
     static_assert(SMEM >= kWTile, "weight tile must fit the shared buffer");
     constexpr int DPT = (D + kNT - 1) / kNT;
-    float* s_w = smem;
+    Acc* s_w = smem;
     for (int r = 0; r < rows; ++r) {
         const int j = r / a.G, h = g * a.G + r % a.G;
         const size_t prow = row_base + (size_t)j * a.Hq + h;
-        const float* ml = a.part_ml + prow * a.max_chunks * 2;
+        const Acc* ml = part_ml + prow * a.max_chunks * 2;
         if (wave == 0) {
-            float M = -INFINITY;
+            Acc M = (Acc)-INFINITY;
             int nan = 0;
             for (int cc = lane; cc < nch; cc += kWave) {
-                float m = ml[cc * 2];
+                Acc m = ml[cc * 2];
                 if (m != m) nan = 1;
-                M = fmaxf(M, m);
+                M = fmax(M, m);
             }
             M = wave_max(M);
             nan = __any(nan);
-            float Ls = 0.f;
+            Acc Ls = (Acc)0;
             for (int cc = lane; cc < nch; cc += kWave) {
-                float m = ml[cc * 2];
-                float w = (M == -INFINITY || m == -INFINITY) ? 0.f : exp2f((m - M) * kLog2e);
+                Acc m = ml[cc * 2];
+                Acc w = (M == (Acc)-INFINITY || m == (Acc)-INFINITY) ? (Acc)0 : exp_acc(m - M);
                 Ls += ml[cc * 2 + 1] * w;
             }
             Ls = wave_sum(Ls);
             if (lane == 0) {
-                s_m[0] = nan ? __builtin_nanf("") : 1.f / (Ls + 1e-10f);
+                s_m[0] = nan ? (Acc)__builtin_nan("") : (Acc)1 / (Ls + (Acc)1e-10);
                 s_l[0] = M;
             }
         }
         __syncthreads();
-        const float M = s_l[0];
-        const float invL = s_m[0];
-        const float* po = a.part_o + prow * a.max_chunks * D;
-        float oacc[DPT];
+        const Acc M = s_l[0];
+        const Acc invL = s_m[0];
+        const Acc* po = part_o + prow * a.max_chunks * D;
+        Acc oacc[DPT];
 #pragma unroll
-        for (int k = 0; k < DPT; ++k) oacc[k] = 0.f;
+        for (int k = 0; k < DPT; ++k) oacc[k] = (Acc)0;
         for (int ct = 0; ct < nch; ct += kWTile) {
             const int cn = min(kWTile, nch - ct);
             for (int cc = tid; cc < cn; cc += kNT) {
-                float m = ml[(ct + cc) * 2];
-                s_w[cc] = (M == -INFINITY || m == -INFINITY) ? 0.f : exp2f((m - M) * kLog2e);
+                Acc m = ml[(ct + cc) * 2];
+                s_w[cc] = (M == (Acc)-INFINITY || m == (Acc)-INFINITY) ? (Acc)0 : exp_acc(m - M);
             }
             __syncthreads();
 #pragma unroll
@@ -427,19 +499,20 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
                 const int d = tid + k * kNT;
                 if (d < D)
                     for (int cc = 0; cc < cn; ++cc)
-                        oacc[k] = fmaf(s_w[cc], po[(size_t)(ct + cc) * D + d], oacc[k]);
+                        oacc[k] = fma(s_w[cc], po[(size_t)(ct + cc) * D + d], oacc[k]);
             }
             __syncthreads();
         }
 #pragma unroll
         for (int k = 0; k < DPT; ++k) {
             const int d = tid + k * kNT;
-            if (d < D) a.out[out_index(a, s, g, r, d, D)] = oacc[k] * invL;
+            if (d < D) a.out[out_index(a, s, g, r, d, D)] = (float)(oacc[k] * invL);
         }
         __syncthreads();
     }
     if (tid == 0) a.counters[(size_t)s * a.Hkv + g] = 0;
 }
+
 
 template <int D, typename KV, int R>
 void launch(const AttendArgs& a, dim3 grid, hipStream_t st) {
@@ -496,8 +569,8 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     a.chunk = lay.chunk;
     a.max_chunks = lay.max_chunks;
     a.counters = reinterpret_cast<int32_t*>(ws + lay.counters_off);
-    a.part_ml = reinterpret_cast<float*>(ws + lay.ml_off);
-    a.part_o = reinterpret_cast<float*>(ws + lay.o_off);
+    a.part_ml = ws + lay.ml_off;
+    a.part_o = ws + lay.o_off;
     a.out = out;
     dim3 grid(lay.max_chunks, p->num_kv_heads, batch);
     hipStream_t st = static_cast<hipStream_t>(stream);

@@ -69,9 +69,10 @@ AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, in
     L.counters_off = kTicketBytes;
     size_t ctr_bytes = align((size_t)batch * p->num_kv_heads * sizeof(int32_t));
     L.ml_off = L.counters_off + ctr_bytes;
-    size_t ml_bytes = align(rows * L.max_chunks * 2 * sizeof(float));
+    // Partials are kept in the accumulation type (double for fp32 pools).
+    size_t ml_bytes = align(rows * L.max_chunks * 2 * sizeof(double));
     L.o_off = L.ml_off + ml_bytes;
-    size_t o_bytes = align(rows * L.max_chunks * (size_t)p->head_dim * sizeof(float));
+    size_t o_bytes = align(rows * L.max_chunks * (size_t)p->head_dim * sizeof(double));
     L.total = L.o_off + o_bytes;
     return L;
 }

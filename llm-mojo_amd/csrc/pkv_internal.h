@@ -28,8 +28,9 @@ inline size_t kv_elt_bytes(int32_t dtype) { return dtype == PKV_DTYPE_BF16 ? 2 :
 // Workspace layout (bytes from the base; every region 256-byte aligned):
 //   [0, 256)                    append commit ticket (int32)
 //   [256, 256 + ctr)            attention per-(sequence, kv head) chunk counters
-//   then part_ml                float2 per (row, chunk): running max m, sum l
-//   then part_o                 float [head_dim] per (row, chunk)
+//   then part_ml                2 accumulators per (row, chunk): chunk max m, sum l
+//   then part_o                 head_dim accumulators per (row, chunk)
+// (accumulators are double for fp32 pools, float for bf16; sized for double)
 struct AttendLayout {
     int32_t chunk;       // keys per split
     int32_t max_chunks;  // grid.x

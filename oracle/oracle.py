@@ -47,6 +47,8 @@ def _L():
             "pkvo_attend": (ctypes.c_int, [ctypes.c_int, i32, i32, i32, i32, i32, f32, vp, vp, vp,
                                            vp, i32, vp, vp, i32, i32, vp, ctypes.c_int,
                                            ctypes.c_int]),
+            "pkvo_attend_f64": (ctypes.c_int, [ctypes.c_int, i32, i32, i32, i32, i32, f32, vp,
+                                               vp, vp, vp, i32, vp, i32, i32, vp, ctypes.c_int]),
             "pkvo_max_threads": (ctypes.c_int, []),
         }
         for name, (res, args) in sig.items():
@@ -238,6 +240,21 @@ def attend(q, k_pool, v_pool, tables, table_lens, pos, q_len, num_heads, num_kv_
                           nthreads, par)
     if rc != 0:
         raise RuntimeError(f"pkvo_attend rc={rc}")
+    return out
+
+
+def attend_f64(q, k_pool, v_pool, tables, pos, q_len, num_heads, num_kv_heads, head_dim,
+               block_size, window, scale=1.0, nthreads=None):
+    """Exact (float64) attention for pkvo_attend's layout (test_attention.mojo:123-163)."""
+    q = np.ascontiguousarray(q, np.float32)
+    tables = np.ascontiguousarray(tables, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    batch = pos.size
+    out = np.empty((batch, q_len, num_heads, head_dim), np.float64)
+    _L().pkvo_attend_f64(_dtype_of(k_pool), num_heads, num_kv_heads, head_dim, block_size,
+                         window, scale, _p(q), _p(k_pool), _p(v_pool), _p(tables),
+                         tables.shape[1], _p(pos), q_len, batch, _p(out),
+                         max_threads() if nthreads is None else nthreads)
     return out
 
 

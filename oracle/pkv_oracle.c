@@ -503,3 +503,41 @@ int pkvo_max_threads(void) {
     return 1;
 #endif
 }
+
+/* ---------------------------------------------- batched float64 attention
+ * pkvo_attend's layout and query positions, evaluated with the float64 naive
+ * oracle (test_attention.mojo:123-163): the exact attention that both fp32
+ * paths approximate. q_scale multiplies q in double. pos[s] < 0 gives zeros. */
+int pkvo_attend_f64(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                    int32_t block_size, int32_t window, float q_scale, const float* q,
+                    const void* k_pool, const void* v_pool, const int32_t* tables,
+                    int32_t table_stride, const int32_t* pos, int32_t q_len, int32_t batch,
+                    double* out, int nthreads) {
+    int64_t hd = (int64_t)num_heads * head_dim;
+#pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1) if (nthreads > 1)
+    {
+        int64_t* tab = (int64_t*)malloc(sizeof(int64_t) * (size_t)(table_stride > 0 ? table_stride : 1));
+        float* qs = (float*)malloc(sizeof(float) * (size_t)hd);
+#pragma omp for schedule(dynamic, 1) collapse(2)
+        for (int32_t s = 0; s < batch; ++s) {
+            for (int32_t j = 0; j < q_len; ++j) {
+                for (int32_t i = 0; i < table_stride; ++i) tab[i] = tables[(int64_t)s * table_stride + i];
+                const float* qj = q + ((int64_t)s * q_len + j) * hd;
+                double* oj = out + ((int64_t)s * q_len + j) * hd;
+                if (pos[s] < 0) {
+                    for (int64_t i = 0; i < hd; ++i) oj[i] = 0.0;
+                    continue;
+                }
+                /* q_scale is a power of two in every use, so the fp32 product is exact. */
+                for (int64_t i = 0; i < hd; ++i) qs[i] = qj[i] * q_scale;
+                int64_t p = (int64_t)pos[s] + j;
+                pkvo_attention_f64(qs, k_pool, v_pool, dtype, tab, block_size, p,
+                                   pkvo_window_start(p, window), num_heads, num_kv_heads,
+                                   head_dim, oj);
+            }
+        }
+        free(tab);
+        free(qs);
+    }
+    return 0;
+}

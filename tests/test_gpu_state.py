@@ -118,7 +118,8 @@ def test_config1_append_into_new_block(gpu):
     k = rng.standard_normal((1, 1, spec.kv_stride)).astype(np.float32)
     v = rng.standard_normal((1, 1, spec.kv_stride)).astype(np.float32)
     st.append(0, [512], [1], k, v, 1)
-    cache.append(0, [512], [1], hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(v), 1)
+    dk, dv = hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(v)
+    cache.append(0, [512], [1], dk, dv, 1)
     assert st.table_lens[0] == 33 and st.tables[0, 32] == free[-1]
     _compare(cache, st)
     cache.free()

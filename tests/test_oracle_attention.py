@@ -221,3 +221,19 @@ def test_attend_matches_per_token_calls_and_inactive_is_zero():
                                       BLOCK_SIZE, 500 + j, 16, 8, 256, 1024)
         np.testing.assert_array_equal(out[0, j].reshape(-1), ref)
     assert np.all(out[1] == 0.0)
+
+
+def test_batched_f64_oracle_agrees_with_per_token_f64():
+    fx = Fixture(16, 8, 256, seed=14, k_scale=0.25)
+    tables = fx.table[None, :].astype(np.int32)
+    q = np.random.default_rng(1).standard_normal((1, 3, 16, 256)).astype(np.float32)
+    ex = O.attend_f64(q, fx.k_pool, fx.v_pool, tables, np.array([1500], np.int32), 3, 16, 8, 256,
+                      BLOCK_SIZE, 1024, scale=0.0625)
+    for j in range(3):
+        p = 1500 + j
+        want = O.attention_f64(q[0, j].reshape(-1) * np.float32(0.0625), fx.k_pool, fx.v_pool,
+                               fx.table, BLOCK_SIZE, p, p - 1023, 16, 8, 256)
+        np.testing.assert_array_equal(ex[0, j].reshape(-1), want)
+    r32 = O.attend(q, fx.k_pool, fx.v_pool, tables, np.array([160], np.int32),
+                   np.array([1500], np.int32), 3, 16, 8, 256, BLOCK_SIZE, 1024, scale=0.0625)
+    assert O.max_rel_err(r32, ex) < 1e-4
