@@ -8,7 +8,7 @@
  *
  * Conventions
  *   - Every pointer argument named *_pool, block_tables, table_lens, free_list,
- *     free_count, pos, n_new, new_len, q, k_new, v_new, out, status and workspace is
+ *     free_count, pos, tok_off, new_len, q, k_new, v_new, out, status and workspace is
  *     DEVICE memory owned by the caller. `stream` is a hipStream_t (NULL = the null
  *     stream). All calls are stream-ordered and asynchronous; the library keeps no
  *     device state between calls (all state lives in caller-owned buffers).
@@ -52,7 +52,7 @@ extern "C" {
 #define PKV_SEQ_TABLE_FULL (-2)    /* position beyond table_stride blocks           */
 #define PKV_SEQ_BAD_BLOCK (-3)     /* a table entry outside [0, num_blocks)         */
 #define PKV_SEQ_FREE_OVERFLOW (-4) /* freeing would overflow the free list          */
-#define PKV_SEQ_BAD_ARGS (-5)      /* n_new[s] > max_new                            */
+#define PKV_SEQ_BAD_ARGS (-5)      /* token range outside [0, total_rows) or > max_new */
 
 /* Layer geometry and numerics, shared by every entry point.
  * Mirrors paged_attention_layer's scalar arguments (attention.mojo:240-256). */
@@ -60,7 +60,7 @@ typedef struct pkv_params {
     int32_t num_heads;    /* query heads Hq                                            */
     int32_t num_kv_heads; /* KV heads Hkv; Hq % Hkv == 0                               */
     int32_t head_dim;     /* D: 64, 128, 256 or 512                                    */
-    int32_t block_size;   /* tokens per block (the engine uses 16)                     */
+    int32_t block_size;   /* tokens per block, a power of two (the engine uses 16)     */
     int32_t num_blocks;   /* physical blocks in each pool (bounds every table entry)   */
     int32_t window;       /* > 0: keys t >= pos - window + 1 (attention.mojo:135-141);
                              <= 0: full causal                                          */
@@ -71,31 +71,34 @@ typedef struct pkv_params {
     int32_t reserved;     /* must be 0                                                 */
 } pkv_params;
 
-/* Bytes of workspace pkv_attend / pkv_decode / pkv_verify need for `batch` sequences
- * of `q_len` queries whose last query position is at most max_pos, and that
- * pkv_append needs for its commit counter. 0 on invalid params. The workspace must be
- * zero-filled once after allocation; every call leaves its counters at zero again. */
+/* Bytes of workspace pkv_attend / pkv_decode need for `batch` sequences of `q_len`
+ * queries whose last query position is at most max_pos (the split-K partials).
+ * 0 on invalid params. */
 size_t pkv_workspace_size(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos);
 
 /* K1 -- fused block allocation + K/V scatter.
  * Replaces the engine's inline append sites: model_speculative_moe_batched.mojo
  * :1984-2001 (decode), :2513-2523 + :2621-2630 (chunked prefill), :2808-2825 (CPU
  * prefill), :3011-3023 + :3106-3116 (verify).
- * For each sequence s (in index order), the n_new[s] tokens at positions
- * pos[s] .. pos[s]+n_new[s]-1 grow the table while p / block_size >= table_lens[s],
- * popping blocks from the back of the free list, then their K and V rows are copied
- * bit-exactly to row table[p / bs] * bs + p % bs of k_pool / v_pool.
+ * New tokens are ragged: sequence s appends n_s = tok_off[s+1] - tok_off[s] tokens whose
+ * K / V rows are rows tok_off[s] .. tok_off[s+1]-1 of k_new / v_new
+ * ([total_rows][num_kv_heads * head_dim] in kv_dtype). A decode step is tok_off = 0..B.
+ * For each sequence s (in index order), the tokens at positions pos[s] .. pos[s]+n_s-1
+ * grow the table while p / block_size >= table_lens[s], popping blocks from the back of
+ * the free list, then their K and V rows are copied bit-exactly to row
+ * table[p / bs] * bs + p % bs of k_pool / v_pool.
  * Out of blocks: blocks popped before the list ran dry stay in the table, none of the
  * sequence's rows is written and status[s] = PKV_SEQ_OUT_OF_BLOCKS.
- * pos[s] < 0 or n_new[s] <= 0 skips sequence s; n_new[s] > max_new changes nothing
- * for s and gives PKV_SEQ_BAD_ARGS.
- * k_new, v_new: [batch][max_new][num_kv_heads * head_dim] in kv_dtype.
- * status: int32 [batch] (device), written for every sequence. */
+ * pos[s] < 0 or n_s <= 0 skips sequence s. A token range outside [0, total_rows) or
+ * longer than max_new (which sizes the grid) changes nothing for s and gives
+ * PKV_SEQ_BAD_ARGS. tok_off: int32 [batch + 1] (device).
+ * status: int32 [batch] (device), written for every sequence. batch <= 4096.
+ * Two launches on `stream`: the allocation (one workgroup) and the row scatter. */
 int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
                    int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
                    int32_t* free_list, int32_t* free_count, const int32_t* pos,
-                   const int32_t* n_new, int32_t max_new, const void* k_new, const void* v_new,
-                   int32_t batch, int32_t* status, void* workspace, size_t workspace_bytes);
+                   const int32_t* tok_off, int32_t max_new, const void* k_new,
+                   const void* v_new, int32_t total_rows, int32_t batch, int32_t* status);
 
 /* K2 -- split-K paged attention for decode and multi-token verify (fp32 or bf16 pools).
  * Replaces paged_attention_layer + _eval_head_range + _softmax (attention.mojo:151-294)
@@ -128,9 +131,10 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
  * ceil(new_len[s] / block_size) table entries (never more than it holds) and push the
  * rest onto the back of the free list in ascending logical order. new_len[s] = 0
  * retires the sequence; new_len[s] < 0 leaves it untouched. Pool rows are not
- * modified. status (optional, int32 [batch]) receives PKV_SEQ_* per sequence; a
- * sequence whose freed blocks would overflow the free list frees nothing and gets
- * PKV_SEQ_FREE_OVERFLOW. */
+ * modified. status (optional, int32 [batch]) receives PKV_SEQ_* per sequence. If any
+ * length or freed entry is out of range, or the pushes would overflow the free list,
+ * the call changes nothing and the offending sequences get PKV_SEQ_BAD_BLOCK /
+ * PKV_SEQ_FREE_OVERFLOW. batch <= 4096. */
 int32_t pkv_rollback(void* stream, const pkv_params* p, int32_t* block_tables,
                      int32_t table_stride, int32_t* table_lens, int32_t* free_list,
                      int32_t* free_count, const int32_t* new_len, int32_t batch,

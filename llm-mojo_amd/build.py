@@ -20,6 +20,8 @@ REPO = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libpkv.so")
+# Workload data generator (benchmark / tests only, not part of the pkv ABI).
+SYNTH_PATH = os.path.join(PKG_DIR, "libpkv_synth.so")
 ORACLE_DIR = os.path.join(REPO, "oracle")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -60,6 +62,9 @@ def build_lib(verbose: bool = False) -> str:
     tmp = LIB_PATH + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB_PATH)
+    tmp = SYNTH_PATH + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-o", tmp, os.path.join(CSRC, "pkv_synth.hip")])
+    os.replace(tmp, SYNTH_PATH)
     return LIB_PATH
 
 

@@ -1,23 +1,28 @@
 // K2 -- split-K paged attention for decode and multi-token verify (fp32 / bf16 pools).
 //
-// Replaces the reference's three-pass CPU loop (attention.mojo:151-294). Work unit:
-// one workgroup per (key chunk, kv head, sequence). All query rows that share the KV
-// head (GQA group x verify queries, <= 16 rows) are evaluated together, so every K/V
-// byte of the chunk is read from HBM exactly once:
-//   1. Q rows -> registers (each lane holds the slice of D it multiplies).
-//   2. Scores: each wave streams K rows of its tokens with 16-byte loads (one fp32 row of
-//      a D=256 head = 64 lanes x 16 B), forms per-lane partial dots for U tokens x R rows
-//      and reduces all of them across the row's lanes with a halving exchange (each
-//      step sends half of the values, so U*R dots cost ~U*R shuffles instead of
-//      U*R*log2(lanes)). Masked scores go to LDS.
-//   3. Chunk softmax statistics: m = max, p = exp(s - m), l = sum p (in LDS).
-//   4. PV: each wave streams V rows and accumulates p * v in registers; the per-wave
-//      sums are added in LDS one wave after another.
-//   5. A single-chunk sequence writes o / (l + 1e-10) directly. Otherwise the chunk
-//      writes (m, l, o) to the workspace and the last chunk of (sequence, kv head) to
-//      finish (atomic counter) merges all chunks:
-//      out = sum_c o_c e^(m_c - M) / (sum_c l_c e^(m_c - M) + 1e-10), M = max_c m_c,
-//      which is the reference's softmax(x)_i = e^(x_i - max) / (sum + 1e-10).
+// Replaces the reference's three-pass CPU loop (attention.mojo:151-294). Two launches:
+//
+// attend_chunk_kernel -- one workgroup per (key chunk, kv head, sequence). All query rows
+// that share the KV head (GQA group x verify queries, <= 16 rows) are evaluated together,
+// so every K/V byte of the chunk is read from HBM exactly once. Each wave owns a
+// contiguous quarter of the chunk and runs an online softmax over batches of U tokens:
+//   1. K and V rows of the batch are loaded together, unconditionally, with 16-byte
+//      loads (one fp32 row of a D=256 head = 64 lanes x 16 B; a lane past the range
+//      re-reads a valid row that is masked), so all of the batch's loads are in flight.
+//   2. Scores: per-lane partial dots for U tokens x R rows, reduced across the row's
+//      lanes with a halving exchange (each step sends half of the values, so U*R dots
+//      cost ~U*R shuffles instead of U*R*log2(lanes)); afterwards lane group idx holds
+//      dot idx, so each lane evaluates one exponential per batch.
+//   3. Running max / sum per row; the accumulators are rescaled only when a row's max
+//      moves; p is broadcast lane to lane and PV is accumulated in registers.
+//   4. The four waves' (m, l, acc) are merged through LDS. A single-chunk sequence writes
+//      o / (l + 1e-10); otherwise the chunk writes its (m, l, o) to the workspace.
+// attend_merge_kernel -- one workgroup per (kv head, sequence) with several chunks:
+//   out = sum_c o_c e^(m_c - M) / (sum_c l_c e^(m_c - M) + 1e-10), M = max_c m_c,
+// which is the reference's softmax(x)_i = e^(x_i - max) / (sum + 1e-10). The launch
+// boundary orders the partials: a fused "last workgroup merges" variant needs a
+// device-scope release/acquire per workgroup, which on this 8-XCD part writes back and
+// invalidates L2 and cost more than the whole merge.
 //
 // Arithmetic: fp32 pools accumulate in double (scores, exponentials, PV sums, merge),
 // so the output is the exact attention rounded once to fp32; the fp32 reference path
@@ -157,7 +162,6 @@ struct AttendArgs {
     int32_t max_chunks;
     void* part_ml;  // Acc pairs (m, l) per (row, chunk)
     void* part_o;   // Acc [D] per (row, chunk)
-    int32_t* counters;
     float* out;
 };
 
@@ -166,6 +170,16 @@ __device__ inline size_t out_index(const AttendArgs& a, int s, int g, int r, int
     int j = r / a.G;
     int h = g * a.G + r % a.G;
     return (((size_t)s * a.q_len + j) * a.Hq + h) * (size_t)D + d;
+}
+
+// Broadcast of a lane value; `src` must be the same for every lane of the wave.
+__device__ inline double lane_bcast(double v, int src) {
+    int lo = __builtin_amdgcn_readlane(__double2loint(v), src);
+    int hi = __builtin_amdgcn_readlane(__double2hiint(v), src);
+    return __hiloint2double(hi, lo);
+}
+__device__ inline float lane_bcast(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
 
 template <int D, typename KV, int R>
@@ -178,18 +192,20 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     constexpr int TPW = L::TPW;
     constexpr int VE = L::VE;
     constexpr int AW = sizeof(Acc) / 4;  // 32-bit registers per accumulator
-    // Token steps kept in flight per wave, bounded by register pressure.
-    constexpr int U = (R * EPL * AW <= 16) ? 8 : ((R * EPL * AW <= 32) ? 4 : 2);
-    constexpr int NV = U * R;  // dots reduced together
-    constexpr int F = NV >= LPR ? NV / LPR : 1;
-    constexpr int SMEM_SCORES = R * kMaxChunk;
-    constexpr int SMEM_RED = R * D;
-    constexpr int SMEM = SMEM_SCORES > SMEM_RED ? SMEM_SCORES : SMEM_RED;
+    static_assert(R <= LPR, "query rows per kv head must not exceed the lanes of a row");
+    // Tokens per batch per token slot: every one of the U*R dots of a batch must land in
+    // its own lane group after the halving reduction (U*R <= LPR); K and V of the batch
+    // are in flight together, which bounds U by register pressure.
+    constexpr int UREG = (R * EPL * AW <= 16) ? 8 : ((R * EPL * AW <= 32) ? 4 : 2);
+    constexpr int U = UREG < LPR / R ? UREG : LPR / R;
+    constexpr int NV = U * R;
+    constexpr int REP = LPR / NV;  // lanes holding the same reduced dot
 
-    __shared__ Acc smem[SMEM];
     __shared__ int s_page[kMaxPages];
-    __shared__ Acc s_m[R], s_l[R];
-    __shared__ int s_flag, s_last;
+    __shared__ Acc s_wm[kNW][R], s_wl[kNW][R];
+    __shared__ Acc red[R * D];
+    __shared__ Acc s_M[R], s_L[R];
+    __shared__ int s_flag;
 
     const int c = blockIdx.x;
     const int g = blockIdx.y;
@@ -264,33 +280,55 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
 
     const size_t head_off = (size_t)g * D;  // element offset of this kv head in a row
     const size_t row_elems = (size_t)a.Hkv * D;
-    auto row_ptr = [&](const char* pool, int tok) -> const uint4* {
+    const int bs_shift = __builtin_ctz(a.bs);  // block_size is a power of two
+    const int bs_mask = a.bs - 1;
+    auto row_off = [&](int tok) -> size_t {  // byte offset of token `tok`'s head slice
         const int t = t0 + tok;
-        const int page = s_page[t / a.bs - pg0];
-        const size_t row = (size_t)page * a.bs + (size_t)(t % a.bs);
-        return reinterpret_cast<const uint4*>(pool + (row * row_elems + head_off) * sizeof(KV));
+        const int page = s_page[(t >> bs_shift) - pg0];
+        const size_t row = ((size_t)page << bs_shift) + (size_t)(t & bs_mask);
+        return (row * row_elems + head_off) * sizeof(KV);
     };
 
-    Acc* s_sc = smem;  // [R][kMaxChunk] scores, then probabilities
-    const int step = kNW * TPW;
-    const int base_idx = xred_base<NV, LPR>(rl);
-    constexpr int kPlainMask = NV >= LPR ? 0 : (LPR / NV) - 1;
+    // This wave's contiguous token range of the chunk.
+    const int per_wave = (((ntok + kNW - 1) / kNW) + TPW - 1) / TPW * TPW;
+    const int wt0 = wave * per_wave;
+    const int wt1 = min(ntok, wt0 + per_wave);
 
-    // ---- scores
-    for (int base = wave * TPW; base < ntok; base += step * U) {
-        uint4 kv[U][NLD];
+    // After the halving reduction lane `rl` holds dot idx = rl / REP, i.e. (u, r) =
+    // (idx / R, idx % R); the lanes of row r are closed under xor of the u bits.
+    const int idx_own = rl / REP;
+    const int r_own = idx_own % R;
+    const int u_own = idx_own / R;
+    const int pq_own = pos0 + r_own / a.G;  // query position of my row
+    const int ws_own = window_start(pq_own, a.window);
+    const bool row_live = r_own < rows;
+
+    Acc m_own = (Acc)-INFINITY;  // running max of my row over this wave's tokens
+    Acc l_own = (Acc)0;          // running sum of exp(s - m_own)
+    Acc acc[R][EPL];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[r][e] = (Acc)0;
+
+    for (int b0 = wt0; b0 < wt1; b0 += U * TPW) {
+        // Every lane loads unconditionally (a token past the wave's range re-reads the
+        // range's last row and is masked below), so the 2*U*NLD loads of the batch are
+        // all in flight together instead of each waiting inside a branch.
+        uint4 kv[U][NLD], vv[U][NLD];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int tok = base + u * step + sub;
-            if (tok < ntok) {
-                const uint4* rp = row_ptr(a.k_pool, tok);
+            const int tok = min(b0 + u * TPW + sub, wt1 - 1);
+            const size_t off = row_off(tok);
+            const uint4* kp = reinterpret_cast<const uint4*>(a.k_pool + off);
+            const uint4* vp = reinterpret_cast<const uint4*>(a.v_pool + off);
 #pragma unroll
-                for (int i = 0; i < NLD; ++i) kv[u][i] = rp[i * LPR + rl];
-            } else {
-#pragma unroll
-                for (int i = 0; i < NLD; ++i) kv[u][i] = make_uint4(0, 0, 0, 0);
+            for (int i = 0; i < NLD; ++i) {
+                kv[u][i] = kp[i * LPR + rl];
+                vv[u][i] = vp[i * LPR + rl];
             }
         }
+        // scores: per-lane partial dots, then the halving reduction over the row's lanes
         Acc dots[NV];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -299,97 +337,82 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
             for (int i = 0; i < NLD; ++i) unpack<Acc>(kv[u][i], kf + i * VE, KV());
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                Acc acc = (Acc)0;
+                Acc d = (Acc)0;
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) acc = fma(qr[r][e], kf[e], acc);
-                dots[u * R + r] = acc;
+                for (int e = 0; e < EPL; ++e) d = fma(qr[r][e], kf[e], d);
+                dots[u * R + r] = d;
             }
         }
         XRed<NV, LPR / 2, Acc>::run(dots, rl);
-        if ((rl & kPlainMask) == 0) {
+        const int tok_own = b0 + u_own * TPW + sub;
+        const int t_own = t0 + tok_own;
+        const bool ok = row_live && tok_own < wt1 && t_own <= pq_own && t_own >= ws_own;
+        const Acc sc_own = ok ? dots[0] : (Acc)-INFINITY;
+        // batch max / sum of my row: xor over the u lane bits and the token-slot bits
+        Acc mb = sc_own;
 #pragma unroll
-            for (int f = 0; f < F; ++f) {
-                const int idx = base_idx + f;
-                const int u = idx / R, r = idx % R;
-                const int tok = base + u * step + sub;
-                if (r < rows && tok < ntok) {
-                    const int t = t0 + tok;
-                    const int pq = pos0 + r / a.G;  // this row's query position
-                    const bool ok = t <= pq && t >= window_start(pq, a.window);
-                    s_sc[r * kMaxChunk + tok] = ok ? dots[f] : (Acc)-INFINITY;
-                }
+        for (int o = REP * R; o < LPR; o <<= 1) mb = fmax(mb, __shfl_xor(mb, o));
+#pragma unroll
+        for (int o = LPR; o < kWave; o <<= 1) mb = fmax(mb, __shfl_xor(mb, o));
+        const Acc m_new = fmax(m_own, mb);
+        const Acc p_own = ok ? exp_acc(sc_own - m_new) : (Acc)0;
+        Acc lb = p_own;
+#pragma unroll
+        for (int o = REP * R; o < LPR; o <<= 1) lb += __shfl_xor(lb, o);
+#pragma unroll
+        for (int o = LPR; o < kWave; o <<= 1) lb += __shfl_xor(lb, o);
+        const bool moved = m_new != m_own;
+        Acc scl = (Acc)1;
+        if (moved) scl = exp_acc(m_own - m_new);  // m_own = -inf gives 0
+        l_own = l_own * scl + lb;
+        m_own = m_new;
+        if (__any(moved)) {  // rescale every row's accumulators (row r's factor: lane r*REP)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const Acc f = lane_bcast(scl, r * REP);
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[r][e] *= f;
             }
         }
-    }
-    __syncthreads();
-
-    // ---- chunk softmax statistics (one wave per row)
-    for (int r = wave; r < rows; r += kNW) {
-        Acc m = (Acc)-INFINITY;
-        for (int i = lane; i < ntok; i += kWave) m = fmax(m, s_sc[r * kMaxChunk + i]);
-        m = wave_max(m);
-        Acc l = (Acc)0;
-        for (int i = lane; i < ntok; i += kWave) {
-            Acc sc = s_sc[r * kMaxChunk + i];
-            Acc p = (m == (Acc)-INFINITY) ? (Acc)0 : exp_acc(sc - m);
-            s_sc[r * kMaxChunk + i] = p;
-            l += p;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            s_m[r] = m;
-            s_l[r] = l;
-        }
-    }
-    __syncthreads();
-
-    // ---- PV
-    Acc acc[R][EPL];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[r][e] = (Acc)0;
-    for (int base = wave * TPW; base < ntok; base += step * U) {
-        uint4 vv[U][NLD];
+        // PV: p of (u, r) lives in lane sub*LPR + (u*R + r)*REP
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int tok = base + u * step + sub;
-            if (tok < ntok) {
-                const uint4* rp = row_ptr(a.v_pool, tok);
+            Acc vf[EPL];
 #pragma unroll
-                for (int i = 0; i < NLD; ++i) vv[u][i] = rp[i * LPR + rl];
-            } else {
+            for (int i = 0; i < NLD; ++i) unpack<Acc>(vv[u][i], vf + i * VE, KV());
 #pragma unroll
-                for (int i = 0; i < NLD; ++i) vv[u][i] = make_uint4(0, 0, 0, 0);
-            }
-        }
+            for (int r = 0; r < R; ++r) {
+                Acc p;
+                if constexpr (TPW == 1) p = lane_bcast(p_own, (u * R + r) * REP);
+                else p = __shfl(p_own, sub * LPR + (u * R + r) * REP);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int tok = base + u * step + sub;
-            if (tok < ntok) {
-                Acc vf[EPL];
-#pragma unroll
-                for (int i = 0; i < NLD; ++i) unpack<Acc>(vv[u][i], vf + i * VE, KV());
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const Acc p = r < rows ? s_sc[r * kMaxChunk + tok] : (Acc)0;
-#pragma unroll
-                    for (int e = 0; e < EPL; ++e) acc[r][e] = fma(p, vf[e], acc[r][e]);
-                }
+                for (int e = 0; e < EPL; ++e) acc[r][e] = fma(p, vf[e], acc[r][e]);
             }
         }
     }
-    // Token slots of one wave hold the same d range: fold them first.
+    // Token slots of one wave hold the same d range and share (m, l): fold them.
 #pragma unroll
     for (int o = LPR; o < kWave; o <<= 1)
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int e = 0; e < EPL; ++e) acc[r][e] += __shfl_xor(acc[r][e], o);
-    __syncthreads();  // all waves done reading probabilities: smem becomes red[R][D]
+    if (lane < NV * REP && (lane % REP) == 0 && idx_own < R) {
+        s_wm[wave][r_own] = m_own;
+        s_wl[wave][r_own] = l_own;
+    }
+    __syncthreads();
 
-    // ---- waves add their sums into red[R][D] one after another
-    Acc* red = smem;
+    // ---- merge the waves: M = max_w m_w, factor e^(m_w - M), L = sum_w l_w e^(m_w - M)
+    Acc fw[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        Acc M = s_wm[0][r];
+#pragma unroll
+        for (int w = 1; w < kNW; ++w) M = fmax(M, s_wm[w][r]);
+        const Acc mw = s_wm[wave][r];
+        fw[r] = (mw == (Acc)-INFINITY) ? (Acc)0 : exp_acc(mw - M);
+    }
     for (int w = 0; w < kNW; ++w) {
         if (wave == w && sub == 0) {
 #pragma unroll
@@ -398,125 +421,162 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
 #pragma unroll
                     for (int i = 0; i < NLD; ++i) {
                         const int d0 = (i * LPR + rl) * VE;
-                        Acc* dst = red + (size_t)r * D + d0;
+                        Acc* dst = red + r * D + d0;
 #pragma unroll
                         for (int e = 0; e < VE; ++e)
-                            dst[e] = (w == 0 ? (Acc)0 : dst[e]) + acc[r][i * VE + e];
+                            dst[e] = (w == 0 ? (Acc)0 : dst[e]) + acc[r][i * VE + e] * fw[r];
                     }
                 }
             }
         }
         __syncthreads();
     }
+    if (tid < rows) {
+        const int r = tid;
+        Acc M = s_wm[0][r];
+        for (int w = 1; w < kNW; ++w) M = fmax(M, s_wm[w][r]);
+        Acc Ls = (Acc)0;
+        for (int w = 0; w < kNW; ++w)
+            if (s_wm[w][r] != (Acc)-INFINITY) Ls += s_wl[w][r] * exp_acc(s_wm[w][r] - M);
+        s_M[r] = M;
+        s_L[r] = Ls;
+    }
+    __syncthreads();
 
     const bool bad = s_flag != 0;
     if (nch == 1) {
         for (int idx = tid; idx < rows * D; idx += kNT) {
             const int r = idx / D, d = idx % D;
-            Acc res = red[(size_t)r * D + d] / (s_l[r] + (Acc)1e-10);
+            Acc res = red[r * D + d] / (s_L[r] + (Acc)1e-10);
             a.out[out_index(a, s, g, r, d, D)] = bad ? __builtin_nanf("") : (float)res;
         }
         return;
     }
 
-    // Partial (m, l, o) of this chunk for each row.
+    // Partial (m, l, o) of this chunk for each row; attend_merge_kernel combines them.
     Acc* part_o = static_cast<Acc*>(a.part_o);
     Acc* part_ml = static_cast<Acc*>(a.part_ml);
     const size_t row_base = ((size_t)s * a.q_len) * a.Hq;  // first row of sequence s
+    auto prow_of = [&](int r) -> size_t {
+        const int j = r / a.G, h = g * a.G + r % a.G;
+        return row_base + (size_t)j * a.Hq + h;
+    };
     for (int idx = tid; idx < rows * D; idx += kNT) {
         const int r = idx / D, d = idx % D;
-        const int j = r / a.G, h = g * a.G + r % a.G;
-        const size_t prow = row_base + (size_t)j * a.Hq + h;
-        part_o[(prow * a.max_chunks + c) * D + d] = red[(size_t)r * D + d];
+        part_o[(prow_of(r) * a.max_chunks + c) * D + d] = red[r * D + d];
     }
     if (tid < rows) {
-        const int r = tid;
-        const int j = r / a.G, h = g * a.G + r % a.G;
-        const size_t prow = row_base + (size_t)j * a.Hq + h;
-        part_ml[(prow * a.max_chunks + c) * 2 + 0] = bad ? (Acc)__builtin_nan("") : s_m[r];
-        part_ml[(prow * a.max_chunks + c) * 2 + 1] = s_l[r];
+        const size_t pr = prow_of(tid);
+        part_ml[(pr * a.max_chunks + c) * 2 + 0] = bad ? (Acc)__builtin_nan("") : s_M[tid];
+        part_ml[(pr * a.max_chunks + c) * 2 + 1] = s_L[tid];
     }
-
-    // Last chunk of (s, g) merges.
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        int prev = atomicAdd(&a.counters[(size_t)s * a.Hkv + g], 1);
-        s_last = (prev == nch - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    // Per row: global max M, any-NaN flag and 1 / (L + 1e-10); then the weighted sum of
-    // the chunk outputs, with the weights e^(m_c - M) staged in LDS kWTile at a time.
-    constexpr int kWTile = 256;
-    static_assert(SMEM >= kWTile, "weight tile must fit the shared buffer");
-    constexpr int DPT = (D + kNT - 1) / kNT;
-    Acc* s_w = smem;
-    for (int r = 0; r < rows; ++r) {
-        const int j = r / a.G, h = g * a.G + r % a.G;
-        const size_t prow = row_base + (size_t)j * a.Hq + h;
-        const Acc* ml = part_ml + prow * a.max_chunks * 2;
-        if (wave == 0) {
-            Acc M = (Acc)-INFINITY;
-            int nan = 0;
-            for (int cc = lane; cc < nch; cc += kWave) {
-                Acc m = ml[cc * 2];
-                if (m != m) nan = 1;
-                M = fmax(M, m);
-            }
-            M = wave_max(M);
-            nan = __any(nan);
-            Acc Ls = (Acc)0;
-            for (int cc = lane; cc < nch; cc += kWave) {
-                Acc m = ml[cc * 2];
-                Acc w = (M == (Acc)-INFINITY || m == (Acc)-INFINITY) ? (Acc)0 : exp_acc(m - M);
-                Ls += ml[cc * 2 + 1] * w;
-            }
-            Ls = wave_sum(Ls);
-            if (lane == 0) {
-                s_m[0] = nan ? (Acc)__builtin_nan("") : (Acc)1 / (Ls + (Acc)1e-10);
-                s_l[0] = M;
-            }
-        }
-        __syncthreads();
-        const Acc M = s_l[0];
-        const Acc invL = s_m[0];
-        const Acc* po = part_o + prow * a.max_chunks * D;
-        Acc oacc[DPT];
-#pragma unroll
-        for (int k = 0; k < DPT; ++k) oacc[k] = (Acc)0;
-        for (int ct = 0; ct < nch; ct += kWTile) {
-            const int cn = min(kWTile, nch - ct);
-            for (int cc = tid; cc < cn; cc += kNT) {
-                Acc m = ml[(ct + cc) * 2];
-                s_w[cc] = (M == (Acc)-INFINITY || m == (Acc)-INFINITY) ? (Acc)0 : exp_acc(m - M);
-            }
-            __syncthreads();
-#pragma unroll
-            for (int k = 0; k < DPT; ++k) {
-                const int d = tid + k * kNT;
-                if (d < D)
-                    for (int cc = 0; cc < cn; ++cc)
-                        oacc[k] = fma(s_w[cc], po[(size_t)(ct + cc) * D + d], oacc[k]);
-            }
-            __syncthreads();
-        }
-#pragma unroll
-        for (int k = 0; k < DPT; ++k) {
-            const int d = tid + k * kNT;
-            if (d < D) a.out[out_index(a, s, g, r, d, D)] = (float)(oacc[k] * invL);
-        }
-        __syncthreads();
-    }
-    if (tid == 0) a.counters[(size_t)s * a.Hkv + g] = 0;
 }
 
+// Cross-chunk merge, one workgroup per (kv head, sequence) with more than one chunk:
+//   out = sum_c o_c w_c / (sum_c l_c w_c + 1e-10),  w_c = e^(m_c - M),  M = max_c m_c.
+// A separate launch: the kernel boundary orders the partials written by the chunk
+// kernel's workgroups (on any XCD) before these reads, with no fence inside either
+// kernel. A NaN m_c marks a chunk that met a table entry outside the pool.
+template <int D, typename Acc>
+__global__ __launch_bounds__(kNT) void attend_merge_kernel(AttendArgs a) {
+    constexpr int kRowsMax = 16;
+    constexpr int kWT = 64;  // chunk weights staged per round
+    __shared__ Acc s_M[kRowsMax], s_invL[kRowsMax];
+    __shared__ Acc s_w[kRowsMax][kWT];
+    const int g = blockIdx.x;
+    const int s = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int rows = a.G * a.q_len;
+    const int pos0 = a.pos ? a.pos[s] : a.pos_scalar;
+    if (pos0 < 0) return;
+    const int hi = pos0 + a.q_len - 1;
+    const int lo = window_start(pos0, a.window);
+    const int c_lo = lo / a.chunk;
+    const int nch = hi / a.chunk - c_lo + 1;
+    if (hi / a.bs >= a.table_stride || nch > a.max_chunks || nch == 1) return;
+
+    const Acc* part_o = static_cast<const Acc*>(a.part_o);
+    const Acc* part_ml = static_cast<const Acc*>(a.part_ml);
+    const size_t row_base = ((size_t)s * a.q_len) * a.Hq;
+    auto prow_of = [&](int r) -> size_t {
+        const int j = r / a.G, h = g * a.G + r % a.G;
+        return row_base + (size_t)j * a.Hq + h;
+    };
+    for (int r = wave; r < rows; r += kNW) {
+        const Acc* ml = part_ml + prow_of(r) * a.max_chunks * 2;
+        Acc M = (Acc)-INFINITY;
+        int nan = 0;
+        for (int cc = lane; cc < nch; cc += kWave) {
+            const Acc m = ml[cc * 2];
+            nan |= (m != m);
+            M = fmax(M, m);
+        }
+        M = wave_max(M);
+        nan = __any(nan);
+        Acc Ls = (Acc)0;
+        for (int cc = lane; cc < nch; cc += kWave) {
+            const Acc m = ml[cc * 2];
+            if (m != (Acc)-INFINITY) Ls += ml[cc * 2 + 1] * exp_acc(m - M);
+        }
+        Ls = wave_sum(Ls);
+        if (lane == 0) {
+            s_M[r] = M;
+            s_invL[r] = nan ? (Acc)__builtin_nan("") : (Acc)1 / (Ls + (Acc)1e-10);
+        }
+    }
+    __syncthreads();
+    constexpr int kOut = (kRowsMax * D + kNT - 1) / kNT;  // outputs per thread, at most
+    Acc oacc[kOut];
+#pragma unroll
+    for (int k = 0; k < kOut; ++k) oacc[k] = (Acc)0;
+    for (int ct = 0; ct < nch; ct += kWT) {
+        const int cn = min(kWT, nch - ct);
+        for (int i = tid; i < rows * cn; i += kNT) {
+            const int r = i / cn, cc = i % cn;
+            const Acc m = part_ml[(prow_of(r) * a.max_chunks + ct + cc) * 2];
+            s_w[r][cc] = (m == (Acc)-INFINITY || s_M[r] == (Acc)-INFINITY) ? (Acc)0
+                                                                             : exp_acc(m - s_M[r]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kOut; ++k) {
+            const int idx = tid + k * kNT;
+            if (idx < rows * D) {
+                const int r = idx / D, d = idx % D;
+                const Acc* po = part_o + (prow_of(r) * a.max_chunks + ct) * D + d;
+                Acc o[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) o[q] = (Acc)0;
+                int cc = 0;
+                for (; cc + 8 <= cn; cc += 8) {  // eight independent loads in flight
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        o[q] = fma(s_w[r][cc + q], po[(size_t)(cc + q) * D], o[q]);
+                }
+                for (; cc < cn; ++cc) o[0] = fma(s_w[r][cc], po[(size_t)cc * D], o[0]);
+                oacc[k] += ((o[0] + o[1]) + (o[2] + o[3])) + ((o[4] + o[5]) + (o[6] + o[7]));
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < kOut; ++k) {
+        const int idx = tid + k * kNT;
+        if (idx < rows * D) {
+            const int r = idx / D, d = idx % D;
+            a.out[out_index(a, s, g, r, d, D)] = (float)(oacc[k] * s_invL[r]);
+        }
+    }
+}
 
 template <int D, typename KV, int R>
 void launch(const AttendArgs& a, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((attend_chunk_kernel<D, KV, R>), grid, dim3(kNT), 0, st, a);
+    if (a.max_chunks > 1)
+        hipLaunchKernelGGL((attend_merge_kernel<D, typename KVT<KV>::Acc>), dim3(grid.y, grid.z),
+                           dim3(kNT), 0, st, a);
 }
 
 template <int D, typename KV>
@@ -525,8 +585,8 @@ int32_t dispatch_rows(const AttendArgs& a, int rows, dim3 grid, hipStream_t st) 
     else if (rows <= 2) launch<D, KV, 2>(a, grid, st);
     else if (rows <= 4) launch<D, KV, 4>(a, grid, st);
     else if (rows <= 8) launch<D, KV, 8>(a, grid, st);
-    else if constexpr (D <= 256) launch<D, KV, 16>(a, grid, st);
-    else return fail(PKV_ERR_UNSUPPORTED, "head_dim 512 supports at most 8 query rows per kv head");
+    else if constexpr (D <= 256 && Lay<D, KV>::LPR >= 16) launch<D, KV, 16>(a, grid, st);
+    else return fail(PKV_ERR_UNSUPPORTED, "at most 8 query rows per kv head for this head_dim / dtype");
     return PKV_OK;
 }
 
@@ -568,7 +628,6 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     a.scale = p->scale;
     a.chunk = lay.chunk;
     a.max_chunks = lay.max_chunks;
-    a.counters = reinterpret_cast<int32_t*>(ws + lay.counters_off);
     a.part_ml = ws + lay.ml_off;
     a.part_o = ws + lay.o_off;
     a.out = out;

@@ -33,8 +33,8 @@ int32_t validate_params(const pkv_params* p) {
         return fail(PKV_ERR_INVALID, "num_kv_heads must be positive and divide num_heads");
     if (p->head_dim != 64 && p->head_dim != 256 && p->head_dim != 512)
         return fail(PKV_ERR_UNSUPPORTED, "head_dim must be 64, 256 or 512");
-    if (p->block_size <= 0 || p->block_size > 256)
-        return fail(PKV_ERR_INVALID, "block_size must be in [1, 256]");
+    if (p->block_size <= 0 || p->block_size > 256 || (p->block_size & (p->block_size - 1)))
+        return fail(PKV_ERR_INVALID, "block_size must be a power of two in [1, 256]");
     if (p->num_blocks <= 0) return fail(PKV_ERR_INVALID, "num_blocks must be positive");
     if (p->kv_dtype != PKV_DTYPE_F32 && p->kv_dtype != PKV_DTYPE_BF16)
         return fail(PKV_ERR_INVALID, "kv_dtype must be PKV_DTYPE_F32 or PKV_DTYPE_BF16");
@@ -66,9 +66,7 @@ AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, in
     L.max_chunks = (int32_t)mc;
     auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
     size_t rows = (size_t)batch * q_len * p->num_heads;
-    L.counters_off = kTicketBytes;
-    size_t ctr_bytes = align((size_t)batch * p->num_kv_heads * sizeof(int32_t));
-    L.ml_off = L.counters_off + ctr_bytes;
+    L.ml_off = 0;
     // Partials are kept in the accumulation type (double for fp32 pools).
     size_t ml_bytes = align(rows * L.max_chunks * 2 * sizeof(double));
     L.o_off = L.ml_off + ml_bytes;

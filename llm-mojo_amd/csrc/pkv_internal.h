@@ -6,7 +6,7 @@
 
 #include <string>
 
-#include "../../include/pkv.h"
+#include "pkv.h"
 
 namespace pkv {
 
@@ -26,20 +26,16 @@ int32_t validate_params(const pkv_params* p);
 inline size_t kv_elt_bytes(int32_t dtype) { return dtype == PKV_DTYPE_BF16 ? 2 : 4; }
 
 // Workspace layout (bytes from the base; every region 256-byte aligned):
-//   [0, 256)                    append commit ticket (int32)
-//   [256, 256 + ctr)            attention per-(sequence, kv head) chunk counters
-//   then part_ml                2 accumulators per (row, chunk): chunk max m, sum l
+//   part_ml                     2 accumulators per (row, chunk): chunk max m, sum l
 //   then part_o                 head_dim accumulators per (row, chunk)
 // (accumulators are double for fp32 pools, float for bf16; sized for double)
 struct AttendLayout {
     int32_t chunk;       // keys per split
     int32_t max_chunks;  // grid.x
-    size_t counters_off;
     size_t ml_off;
     size_t o_off;
     size_t total;
 };
-constexpr size_t kTicketBytes = 256;
 AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos);
 
 __host__ __device__ inline int32_t window_start(int32_t pos, int32_t window) {

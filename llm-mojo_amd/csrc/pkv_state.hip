@@ -1,11 +1,21 @@
-// K1 (fused block allocation + K/V scatter) and K5 (rollback / retire).
+// K1 (block allocation + K/V scatter) and K5 (rollback / retire).
 //
 // Block-manager state lives in caller-owned device memory: tables [batch][stride],
 // table_lens [batch], the LIFO free list [num_blocks] and its count. The reference
 // keeps the same state on the host (BlockManager / Sequence,
 // model_speculative_moe_batched.mojo:789-845) and mutates it one sequence at a time;
-// here every sequence's allocation is derived from an ordered prefix sum over the
-// batch, which yields exactly the serial order's result.
+// here every sequence's blocks are derived from an ordered prefix sum over the batch,
+// which yields exactly the serial order's result, and the per-block work (table
+// entries, free-list pushes) is spread over all threads of the workgroup.
+//
+// pkv_append = two launches on the caller's stream:
+//   alloc_kernel   (1 workgroup)  pops the blocks every sequence needs, writes the new
+//                                 table entries, table_lens, free_count and status;
+//   scatter_kernel (tokens x seq) copies each token's K and V rows to
+//                                 table[p / bs] * bs + p % bs for sequences whose
+//                                 status is OK.
+// The launch boundary orders the table writes before the scatter's reads, so neither
+// kernel needs a device-scope fence.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -15,9 +25,9 @@ namespace pkv {
 namespace {
 
 constexpr int kNT = kBlockThreads;
+constexpr int kMaxBatch = 4096;  // per-sequence plan kept in LDS
 
-// Block-wide exclusive scan of one int per thread; returns the exclusive prefix and
-// writes the block total to *total. `tmp` holds kNT ints of LDS.
+// Block-wide exclusive scan of one int per thread; writes the block total to *total.
 __device__ int block_exclusive_scan(int v, int* tmp, int* total) {
     const int tid = threadIdx.x;
     tmp[tid] = v;
@@ -34,6 +44,35 @@ __device__ int block_exclusive_scan(int v, int* tmp, int* total) {
     return incl - v;
 }
 
+// Sequence s with pref[s] <= e < pref[s + 1] (pref non-decreasing, pref[0] = 0).
+__device__ inline int find_seq(const int* pref, int batch, int e) {
+    int lo = 0, hi = batch - 1;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (pref[mid] <= e) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Fills pref[0..batch] with the exclusive prefix sum of cnt[0..batch) (both in LDS)
+// and returns the total.
+__device__ int lds_prefix(const int* cnt, int* pref, int batch, int* tmp) {
+    const int seg = (batch + kNT - 1) / kNT;
+    const int b0 = threadIdx.x * seg, b1 = min(batch, b0 + seg);
+    int sum = 0;
+    for (int s = b0; s < b1; ++s) sum += cnt[s];
+    int total;
+    int run = block_exclusive_scan(sum, tmp, &total);
+    for (int s = b0; s < b1; ++s) {
+        pref[s] = run;
+        run += cnt[s];
+    }
+    if (threadIdx.x == 0) pref[batch] = total;
+    __syncthreads();
+    return total;
+}
+
 struct AppendArgs {
     char* k_pool;
     char* v_pool;
@@ -43,8 +82,9 @@ struct AppendArgs {
     const int32_t* free_list;
     int32_t* free_count;
     const int32_t* pos;
-    const int32_t* n_new;
+    const int32_t* tok_off;  // [batch + 1] rows of k_new / v_new per sequence
     int32_t max_new;
+    int32_t total_rows;
     const char* k_new;
     const char* v_new;
     int32_t batch;
@@ -53,167 +93,93 @@ struct AppendArgs {
     int32_t num_blocks;
     int32_t row_bytes;  // num_kv_heads * head_dim * element size (multiple of 16)
     int32_t tok_per_wg;
-    int32_t* ticket;
-    int32_t num_wg;
 };
 
-// Blocks sequence s still needs, or a negative PKV_SEQ_* code. Reads only state that
-// no workgroup writes before the commit.
-__device__ inline int append_need(const AppendArgs& a, int s, int* len_out) {
-    int len = a.table_lens[s];
-    *len_out = len;
-    int p = a.pos[s], n = a.n_new[s];
+// Blocks sequence s needs (>= 0), or a negative PKV_SEQ_* code.
+__device__ inline int append_need(const AppendArgs& a, int s, int len) {
+    const int p = a.pos[s];
+    const int r0 = a.tok_off[s], r1 = a.tok_off[s + 1];
+    const int n = r1 - r0;
     if (p < 0 || n <= 0) return 0;
-    if (n > a.max_new) return PKV_SEQ_BAD_ARGS;
-    long long last = (long long)p + n - 1;
-    long long last_blk = last / a.bs;
+    if (n > a.max_new || r0 < 0 || r1 > a.total_rows) return PKV_SEQ_BAD_ARGS;
+    const long long last_blk = ((long long)p + n - 1) / a.bs;
     if (last_blk >= a.table_stride) return PKV_SEQ_TABLE_FULL;
     if (len < 0 || len > a.table_stride) return PKV_SEQ_BAD_BLOCK;
-    long long need = last_blk + 1 - len;
+    const long long need = last_blk + 1 - len;
     return need > 0 ? (int)need : 0;
 }
 
-// grid = (ceil(max_new / tok_per_wg), batch); 256 threads.
-// Every workgroup recomputes the ordered allocation plan from the pre-call state and
-// scatters its tokens' rows; the last workgroup to finish (atomic ticket) commits
-// tables, table_lens, free_count and status, so no workgroup ever reads state that
-// another has already changed.
-__global__ __launch_bounds__(kNT) void append_kernel(AppendArgs a) {
+// One workgroup. Sequence s (index order) takes the free-list entries
+// free_list[fc - 1 - pref[s] - j], j < granted[s]: the LIFO pops of a serial pass.
+// A sequence that runs the list dry keeps what it popped (status OUT_OF_BLOCKS).
+__global__ __launch_bounds__(kNT) void alloc_kernel(AppendArgs a) {
     __shared__ int s_tmp[kNT];
-    __shared__ int s_info[4];  // my prefix, my granted, my len, fc
-    __shared__ int s_last;
+    __shared__ int s_len[kMaxBatch];
+    __shared__ int s_need[kMaxBatch];
+    __shared__ int s_pref[kMaxBatch + 1];
     const int tid = threadIdx.x;
-    const int s_me = blockIdx.y;
-    const int tile = blockIdx.x;
-
     int fc = *a.free_count;
-    bool fc_bad = fc < 0 || fc > a.num_blocks;
+    const bool fc_bad = fc < 0 || fc > a.num_blocks;
     if (fc_bad) fc = 0;
-
-    // Pass 1: segment sums of `need` over the batch (thread-contiguous segments keep
-    // the prefix in sequence order).
-    const int seg = (a.batch + kNT - 1) / kNT;
-    const int s_begin = tid * seg;
-    const int s_end = min(a.batch, s_begin + seg);
-    int seg_sum = 0;
-    for (int s = s_begin; s < s_end; ++s) {
-        int len;
-        int need = append_need(a, s, &len);
-        if (need > 0) seg_sum += need;
-    }
-    int total;
-    int seg_prefix = block_exclusive_scan(seg_sum, s_tmp, &total);
-    // Pass 2: the owner of s_me publishes its prefix.
-    if (s_me >= s_begin && s_me < s_end) {
-        int run = seg_prefix;
-        for (int s = s_begin; s < s_end; ++s) {
-            int len;
-            int need = append_need(a, s, &len);
-            if (s == s_me) {
-                int granted = 0;
-                int code = need < 0 ? need : 0;
-                if (need > 0) {
-                    int avail = fc - run;
-                    granted = avail <= 0 ? 0 : (avail < need ? avail : need);
-                    if (granted < need) code = fc_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_OUT_OF_BLOCKS;
-                }
-                s_info[0] = run;
-                s_info[1] = code;  // 0 = proceed
-                s_info[2] = len;
-                s_info[3] = granted;
-            }
-            if (need > 0) run += need;
-        }
+    for (int s = tid; s < a.batch; s += kNT) {
+        const int len = a.table_lens[s];
+        const int need = append_need(a, s, len);
+        s_len[s] = len;
+        s_need[s] = need > 0 ? need : 0;
+        a.status[s] = need < 0 ? need : PKV_SEQ_OK;
     }
     __syncthreads();
-
-    // Scatter this workgroup's tokens (only when the whole sequence's allocation holds).
-    const int my_prefix = s_info[0];
-    const int my_code = s_info[1];
-    const int my_len = s_info[2];
-    const int p0 = a.pos[s_me];
-    const int n = a.n_new[s_me];
-    if (my_code == 0 && p0 >= 0 && n > 0) {
-        const int tok_begin = tile * a.tok_per_wg;
-        const int tok_end = min(n, tok_begin + a.tok_per_wg);
-        const int vec_per_row = a.row_bytes / 16;
-        for (int b = tok_begin; b < tok_end; ++b) {
-            const int p = p0 + b;
-            const int lb = p / a.bs;
-            int phys;
-            if (lb < my_len) {
-                phys = a.tables[(size_t)s_me * a.table_stride + lb];
-            } else {
-                int idx = fc - 1 - my_prefix - (lb - my_len);
-                phys = (idx >= 0 && idx < a.num_blocks) ? a.free_list[idx] : -1;
-            }
-            if (phys < 0 || phys >= a.num_blocks) continue;  // reported by the commit
-            const size_t row = (size_t)phys * a.bs + (size_t)(p % a.bs);
-            const uint4* ks = reinterpret_cast<const uint4*>(
-                a.k_new + ((size_t)s_me * a.max_new + b) * a.row_bytes);
-            const uint4* vs = reinterpret_cast<const uint4*>(
-                a.v_new + ((size_t)s_me * a.max_new + b) * a.row_bytes);
-            uint4* kd = reinterpret_cast<uint4*>(a.k_pool + row * a.row_bytes);
-            uint4* vd = reinterpret_cast<uint4*>(a.v_pool + row * a.row_bytes);
-            for (int i = tid; i < vec_per_row; i += kNT) {
-                uint4 kv = ks[i];
-                uint4 vv = vs[i];
-                kd[i] = kv;
-                vd[i] = vv;
-            }
-        }
+    const int total = lds_prefix(s_need, s_pref, a.batch, s_tmp);
+    const int popped = total < fc ? total : fc;
+    // Table entries, flattened over every popped block.
+    for (int e = tid; e < popped; e += kNT) {
+        const int s = find_seq(s_pref, a.batch, e);
+        const int j = e - s_pref[s];
+        a.tables[(size_t)s * a.table_stride + s_len[s] + j] = a.free_list[fc - 1 - e];
     }
-
-    // Ticket: the last workgroup commits the state.
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        int t = atomicAdd(a.ticket, 1);
-        s_last = (t == a.num_wg - 1);
+    for (int s = tid; s < a.batch; s += kNT) {
+        const int need = s_need[s];
+        if (need == 0) continue;
+        const int avail = fc - s_pref[s];
+        const int granted = avail <= 0 ? 0 : (avail < need ? avail : need);
+        if (granted > 0) a.table_lens[s] = s_len[s] + granted;
+        if (granted < need) a.status[s] = fc_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_OUT_OF_BLOCKS;
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    if (tid == 0 && !fc_bad) *a.free_count = fc - popped;
+}
 
-    int run = seg_prefix;
-    int popped = 0;
-    for (int s = s_begin; s < s_end; ++s) {
-        int len;
-        int need = append_need(a, s, &len);
-        int code = need < 0 ? need : 0;
-        int granted = 0;
-        if (need > 0) {
-            int avail = fc - run;
-            granted = avail <= 0 ? 0 : (avail < need ? avail : need);
-            if (granted < need) code = fc_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_OUT_OF_BLOCKS;
-            run += need;
+// grid = (ceil(max_new / tok_per_wg), batch). Copies this workgroup's tokens of one
+// sequence; a table entry outside the pool is skipped and reported as BAD_BLOCK.
+__global__ __launch_bounds__(kNT) void scatter_kernel(AppendArgs a) {
+    const int s = blockIdx.y;
+    const int tid = threadIdx.x;
+    if (a.status[s] != PKV_SEQ_OK) return;
+    const int p0 = a.pos[s];
+    const int row0 = a.tok_off[s];
+    const int n = a.tok_off[s + 1] - row0;
+    if (p0 < 0 || n <= 0) return;
+    const int tok_begin = blockIdx.x * a.tok_per_wg;
+    const int tok_end = min(n, tok_begin + a.tok_per_wg);
+    const int vec_per_row = a.row_bytes / 16;
+    const int32_t* table = a.tables + (size_t)s * a.table_stride;
+    for (int b = tok_begin; b < tok_end; ++b) {
+        const int p = p0 + b;
+        const int phys = table[p / a.bs];
+        if (phys < 0 || phys >= a.num_blocks) {
+            if (tid == 0) a.status[s] = PKV_SEQ_BAD_BLOCK;
+            continue;
         }
-        int32_t* table = a.tables + (size_t)s * a.table_stride;
-        int prefix_s = run - (need > 0 ? need : 0);
-        for (int j = 0; j < granted; ++j) {
-            int blk = a.free_list[fc - 1 - prefix_s - j];
-            if (blk < 0 || blk >= a.num_blocks) code = PKV_SEQ_BAD_BLOCK;
-            table[len + j] = blk;
+        const size_t row = (size_t)phys * a.bs + (size_t)(p % a.bs);
+        const uint4* ks = reinterpret_cast<const uint4*>(a.k_new + ((size_t)row0 + b) * a.row_bytes);
+        const uint4* vs = reinterpret_cast<const uint4*>(a.v_new + ((size_t)row0 + b) * a.row_bytes);
+        uint4* kd = reinterpret_cast<uint4*>(a.k_pool + row * a.row_bytes);
+        uint4* vd = reinterpret_cast<uint4*>(a.v_pool + row * a.row_bytes);
+        for (int i = tid; i < vec_per_row; i += kNT) {
+            const uint4 kv = ks[i];
+            const uint4 vv = vs[i];
+            kd[i] = kv;
+            vd[i] = vv;
         }
-        if (code == 0 && a.pos[s] >= 0 && a.n_new[s] > 0) {
-            // Pre-existing entries covering the appended positions must be valid.
-            int lb0 = a.pos[s] / a.bs;
-            int lb1 = min(len, (a.pos[s] + a.n_new[s] - 1) / a.bs + 1);
-            for (int lb = lb0; lb < lb1; ++lb) {
-                int blk = table[lb];
-                if (blk < 0 || blk >= a.num_blocks) code = PKV_SEQ_BAD_BLOCK;
-            }
-        }
-        if (granted > 0) a.table_lens[s] = len + granted;
-        a.status[s] = code;
-        popped += granted;
-    }
-    // free_count -= popped (block-wide sum of per-thread pops).
-    int all_popped;
-    block_exclusive_scan(popped, s_tmp, &all_popped);
-    if (tid == 0) {
-        if (!fc_bad) *a.free_count = fc - all_popped;
-        *a.ticket = 0;
     }
 }
 
@@ -230,64 +196,61 @@ struct RollbackArgs {
     int32_t num_blocks;
 };
 
-__device__ inline int rollback_keep(const RollbackArgs& a, int s, int len) {
-    int nl = a.new_len[s];
-    if (nl < 0) return len;
-    int keep = (int)(((long long)nl + a.bs - 1) / a.bs);
-    return keep < len ? keep : len;
-}
-
-// One workgroup: ordered prefix over the freed counts, then each sequence pushes its
-// tail blocks (ascending logical order) at free_list[fc + prefix + j].
+// One workgroup: ordered prefix over the freed counts; freed entry e (sequence s's tail
+// blocks in ascending logical order, sequences in index order) goes to
+// free_list[fc + e]. Any inconsistency (a length or entry outside its range, or a
+// free list that would overflow) rejects the whole call and changes nothing.
 __global__ __launch_bounds__(kNT) void rollback_kernel(RollbackArgs a) {
     __shared__ int s_tmp[kNT];
+    __shared__ int s_keep[kMaxBatch];
+    __shared__ int s_cnt[kMaxBatch];
+    __shared__ int s_pref[kMaxBatch + 1];
     __shared__ int s_bad;
     const int tid = threadIdx.x;
     if (tid == 0) s_bad = 0;
     __syncthreads();
     const int fc = *a.free_count;
-    const int seg = (a.batch + kNT - 1) / kNT;
-    const int s_begin = tid * seg;
-    const int s_end = min(a.batch, s_begin + seg);
-
-    int seg_sum = 0;
-    for (int s = s_begin; s < s_end; ++s) {
-        int len = a.table_lens[s];
-        if (len < 0 || len > a.table_stride) {
-            s_bad = 1;
-            continue;
+    for (int s = tid; s < a.batch; s += kNT) {
+        const int len = a.table_lens[s];
+        const bool len_ok = len >= 0 && len <= a.table_stride;
+        int keep = len_ok ? len : 0;
+        if (len_ok && a.new_len[s] >= 0) {
+            const long long k = ((long long)a.new_len[s] + a.bs - 1) / a.bs;
+            keep = k < len ? (int)k : len;
         }
-        int keep = rollback_keep(a, s, len);
-        const int32_t* table = a.tables + (size_t)s * a.table_stride;
-        for (int j = keep; j < len; ++j)
-            if (table[j] < 0 || table[j] >= a.num_blocks) s_bad = 1;
-        seg_sum += len - keep;
-    }
-    int total;
-    int run = block_exclusive_scan(seg_sum, s_tmp, &total);
-    const bool reject = s_bad || fc < 0 || (long long)fc + total > a.num_blocks;
-    for (int s = s_begin; s < s_end; ++s) {
-        int len = a.table_lens[s];
-        bool len_ok = len >= 0 && len <= a.table_stride;
-        int keep = len_ok ? rollback_keep(a, s, len) : 0;
-        int freed = len_ok ? len - keep : 0;
-        if (reject) {
-            if (a.status) {
-                int code = PKV_SEQ_OK;
-                if (!len_ok) code = PKV_SEQ_BAD_BLOCK;
-                else if (freed > 0) code = s_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_FREE_OVERFLOW;
-                a.status[s] = code;
-            }
-            continue;
-        }
-        const int32_t* table = a.tables + (size_t)s * a.table_stride;
-        for (int j = 0; j < freed; ++j) a.free_list[fc + run + j] = table[keep + j];
-        a.table_lens[s] = keep;
-        if (a.status) a.status[s] = PKV_SEQ_OK;
-        run += freed;
+        if (!len_ok) s_bad = 1;
+        s_keep[s] = keep;
+        s_cnt[s] = len_ok ? len - keep : 0;
     }
     __syncthreads();
-    if (tid == 0 && !reject) *a.free_count = fc + total;
+    const int total = lds_prefix(s_cnt, s_pref, a.batch, s_tmp);
+    for (int e = tid; e < total; e += kNT) {  // every freed entry must name a pool block
+        const int s = find_seq(s_pref, a.batch, e);
+        const int blk = a.tables[(size_t)s * a.table_stride + s_keep[s] + (e - s_pref[s])];
+        if (blk < 0 || blk >= a.num_blocks) s_bad = 1;
+    }
+    __syncthreads();
+    const bool reject = s_bad || fc < 0 || (long long)fc + total > a.num_blocks;
+    if (reject) {
+        if (a.status)
+            for (int s = tid; s < a.batch; s += kNT) {
+                const int len = a.table_lens[s];
+                const bool len_ok = len >= 0 && len <= a.table_stride;
+                a.status[s] = !len_ok ? PKV_SEQ_BAD_BLOCK
+                              : (s_cnt[s] > 0 ? (s_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_FREE_OVERFLOW)
+                                              : PKV_SEQ_OK);
+            }
+        return;
+    }
+    for (int e = tid; e < total; e += kNT) {
+        const int s = find_seq(s_pref, a.batch, e);
+        a.free_list[fc + e] = a.tables[(size_t)s * a.table_stride + s_keep[s] + (e - s_pref[s])];
+    }
+    for (int s = tid; s < a.batch; s += kNT) {
+        if (s_cnt[s] > 0) a.table_lens[s] = s_keep[s];
+        if (a.status) a.status[s] = PKV_SEQ_OK;
+    }
+    if (tid == 0) *a.free_count = fc + total;
 }
 
 }  // namespace
@@ -298,19 +261,19 @@ extern "C" {
 int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
                    int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
                    int32_t* free_list, int32_t* free_count, const int32_t* pos,
-                   const int32_t* n_new, int32_t max_new, const void* k_new, const void* v_new,
-                   int32_t batch, int32_t* status, void* workspace, size_t workspace_bytes) {
+                   const int32_t* tok_off, int32_t max_new, const void* k_new,
+                   const void* v_new, int32_t total_rows, int32_t batch, int32_t* status) {
     using namespace pkv;
     clear_error();
     int32_t rc = validate_params(p);
     if (rc != PKV_OK) return rc;
-    if (batch <= 0 || max_new <= 0 || table_stride <= 0)
-        return fail(PKV_ERR_INVALID, "batch, max_new and table_stride must be positive");
+    if (batch <= 0 || max_new <= 0 || table_stride <= 0 || total_rows <= 0)
+        return fail(PKV_ERR_INVALID,
+                    "batch, max_new, total_rows and table_stride must be positive");
+    if (batch > kMaxBatch) return fail(PKV_ERR_UNSUPPORTED, "batch must be <= 4096");
     if (!k_pool || !v_pool || !block_tables || !table_lens || !free_list || !free_count ||
-        !pos || !n_new || !k_new || !v_new || !status || !workspace)
+        !pos || !tok_off || !k_new || !v_new || !status)
         return fail(PKV_ERR_INVALID, "null device pointer");
-    if (workspace_bytes < kTicketBytes)
-        return fail(PKV_ERR_WORKSPACE, "workspace smaller than the append ticket");
     AppendArgs a{};
     a.k_pool = static_cast<char*>(k_pool);
     a.v_pool = static_cast<char*>(v_pool);
@@ -320,8 +283,9 @@ int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool
     a.free_list = free_list;
     a.free_count = free_count;
     a.pos = pos;
-    a.n_new = n_new;
+    a.tok_off = tok_off;
     a.max_new = max_new;
+    a.total_rows = total_rows;
     a.k_new = static_cast<const char*>(k_new);
     a.v_new = static_cast<const char*>(v_new);
     a.batch = batch;
@@ -329,15 +293,13 @@ int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool
     a.bs = p->block_size;
     a.num_blocks = p->num_blocks;
     a.row_bytes = (int32_t)((size_t)p->num_kv_heads * p->head_dim * kv_elt_bytes(p->kv_dtype));
-    // Tokens per workgroup: one row pair is row_bytes*2 (8 or 16 KiB at 8 x 256);
-    // aim for ~64 KiB of copies per workgroup.
-    int tpw = (64 * 1024) / (2 * a.row_bytes);
+    // Tokens per scatter workgroup: ~64 KiB of K+V copies each (4 tokens at 8 x 256 fp32).
+    const int tpw = (64 * 1024) / (2 * a.row_bytes);
     a.tok_per_wg = tpw < 1 ? 1 : tpw;
-    a.ticket = static_cast<int32_t*>(workspace);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(alloc_kernel, dim3(1), dim3(kNT), 0, st, a);
     dim3 grid((max_new + a.tok_per_wg - 1) / a.tok_per_wg, batch);
-    if ((long long)grid.x * grid.y > 0x7fffffffLL) return fail(PKV_ERR_INVALID, "grid too large");
-    a.num_wg = (int32_t)(grid.x * grid.y);
-    hipLaunchKernelGGL(append_kernel, grid, dim3(kNT), 0, static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(scatter_kernel, grid, dim3(kNT), 0, st, a);
     return check_launch("pkv_append");
 }
 
@@ -351,6 +313,7 @@ int32_t pkv_rollback(void* stream, const pkv_params* p, int32_t* block_tables,
     if (rc != PKV_OK) return rc;
     if (batch <= 0 || table_stride <= 0)
         return fail(PKV_ERR_INVALID, "batch and table_stride must be positive");
+    if (batch > kMaxBatch) return fail(PKV_ERR_UNSUPPORTED, "batch must be <= 4096");
     if (!block_tables || !table_lens || !free_list || !free_count || !new_len)
         return fail(PKV_ERR_INVALID, "null device pointer");
     RollbackArgs a{};

@@ -123,7 +123,7 @@ class PagedKVCache:
         self.workspace = hip.DeviceArray((ws,), np.uint8, zero=True)
         # Small host->device staging buffers for per-call integer arguments.
         self._i32_a = hip.DeviceArray((max_seqs,), np.int32, zero=True)
-        self._i32_b = hip.DeviceArray((max_seqs,), np.int32, zero=True)
+        self._i32_b = hip.DeviceArray((max_seqs + 1,), np.int32, zero=True)
 
     # -------------------------------------------------------------- helpers
     def _stream(self):
@@ -140,18 +140,19 @@ class PagedKVCache:
         return _ptr(x)
 
     # ------------------------------------------------------------ operators
-    def append(self, layer: int, pos, n_new, k_new, v_new, max_new: int, batch: int | None = None):
-        """KV append for `batch` sequence slots (K1). pos / n_new: int32[batch] (numpy or
-        device); k_new / v_new: device [batch][max_new][kv_stride] in the pool dtype.
-        Returns the device status array (PKV_SEQ_* per sequence)."""
+    def append(self, layer: int, pos, tok_off, k_new, v_new, max_new: int, total_rows: int,
+               batch: int | None = None):
+        """KV append for `batch` sequence slots (K1). pos: int32[batch]; tok_off:
+        int32[batch + 1] (numpy or device) -- slot s appends rows tok_off[s] ..
+        tok_off[s+1]-1 of k_new / v_new (device [total_rows][kv_stride], pool dtype) at
+        positions pos[s], pos[s] + 1, ... Returns the device status array (PKV_SEQ_*)."""
         b = batch or self.max_seqs
         p = self.params[layer]
         lib.call("pkv_append", self._stream(), ctypes.byref(p), self.k_pools[layer].ptr,
                  self.v_pools[layer].ptr, self.tables.ptr, self.table_stride,
                  self.table_lens.ptr, self.free_list.ptr, self.free_count.ptr,
-                 self._ints(pos, self._i32_a, b), self._ints(n_new, self._i32_b, b), max_new,
-                 _ptr(k_new), _ptr(v_new), b, self.status.ptr, self.workspace.ptr,
-                 self.workspace.nbytes)
+                 self._ints(pos, self._i32_a, b), self._ints(tok_off, self._i32_b, b + 1),
+                 max_new, _ptr(k_new), _ptr(v_new), total_rows, b, self.status.ptr)
         return self.status
 
     def attend(self, layer: int, q, pos, q_len: int, out, batch: int | None = None,

@@ -48,7 +48,7 @@ _PP = ctypes.POINTER(PkvParams)
 PROTOTYPES = {
     "pkv_workspace_size": (_sz, [_PP, _i32, _i32, _i32]),
     "pkv_append": (_i32, [_vp, _PP, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp,
-                          _vp, _i32, _vp, _vp, _sz]),
+                          _vp, _i32, _i32, _vp]),
     "pkv_attend": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp,
                           _sz]),
     "pkv_decode": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _sz]),

@@ -42,7 +42,7 @@ def _L():
             "pkvo_bm_allocate": (i32, [vp, vp]),
             "pkvo_bm_free": (None, [vp, vp, i32]),
             "pkvo_append": (None, [ctypes.c_int, i32, i32, vp, vp, vp, i32, vp, vp, vp, vp, vp,
-                                   i32, vp, vp, i32, vp]),
+                                   i32, vp, vp, i32, i32, vp]),
             "pkvo_rollback": (None, [i32, vp, i32, vp, vp, vp, vp, i32]),
             "pkvo_attend": (ctypes.c_int, [ctypes.c_int, i32, i32, i32, i32, i32, f32, vp, vp, vp,
                                            vp, i32, vp, vp, i32, i32, vp, ctypes.c_int,
@@ -180,21 +180,31 @@ class BlockManager:
         return self.free_list[: int(self.count[0])].copy()
 
 
+def dense_tok_off(batch: int, rows_per_seq: int) -> np.ndarray:
+    """tok_off for a dense [batch][rows_per_seq] buffer where each sequence uses all rows."""
+    return (np.arange(batch + 1, dtype=np.int64) * rows_per_seq).astype(np.int32)
+
+
+def ragged_tok_off(n_new) -> np.ndarray:
+    """tok_off for packed rows: sequence s owns n_new[s] consecutive rows."""
+    n = np.maximum(np.asarray(n_new, np.int64), 0)
+    return np.concatenate([[0], np.cumsum(n)]).astype(np.int32)
+
+
 class CacheState:
     """CPU mirror of the device block-manager state + pools, mutated by the oracle's
     append / rollback (the engine's inline append sites and retire, see pkv_oracle.c)."""
 
     def __init__(self, num_layers, kv_stride, block_size, num_blocks, max_seqs, table_stride,
-                 dtype=np.float32):
+                 dtype=np.float32, alloc_pools=True):
         self.kv_stride = kv_stride
         self.block_size = block_size
         self.num_blocks = num_blocks
         self.table_stride = table_stride
         self.dtype = np.dtype(dtype)
-        self.k_pools = [np.zeros(num_blocks * block_size * kv_stride, self.dtype)
-                        for _ in range(num_layers)]
-        self.v_pools = [np.zeros(num_blocks * block_size * kv_stride, self.dtype)
-                        for _ in range(num_layers)]
+        n = num_blocks * block_size * kv_stride if alloc_pools else 0
+        self.k_pools = [np.zeros(n, self.dtype) for _ in range(num_layers)]
+        self.v_pools = [np.zeros(n, self.dtype) for _ in range(num_layers)]
         self.tables = np.zeros((max_seqs, table_stride), np.int32)
         self.table_lens = np.zeros(max_seqs, np.int32)
         self.bm = BlockManager(num_blocks)
@@ -203,18 +213,20 @@ class CacheState:
     def free_list(self) -> np.ndarray:
         return self.bm.free_blocks
 
-    def append(self, layer, pos, n_new, k_new, v_new, max_new):
+    def append(self, layer, pos, tok_off, k_new, v_new, max_new):
+        """Ragged append: sequence s takes rows tok_off[s]..tok_off[s+1]-1 of k_new/v_new."""
         pos = np.ascontiguousarray(pos, np.int32)
-        n_new = np.ascontiguousarray(n_new, np.int32)
-        k_new = np.ascontiguousarray(k_new, self.dtype)
-        v_new = np.ascontiguousarray(v_new, self.dtype)
+        tok_off = np.ascontiguousarray(tok_off, np.int32)
+        k_new = np.ascontiguousarray(k_new, self.dtype).reshape(-1, self.kv_stride)
+        v_new = np.ascontiguousarray(v_new, self.dtype).reshape(-1, self.kv_stride)
         batch = pos.size
+        assert tok_off.size == batch + 1
         status = np.zeros(batch, np.int32)
         _L().pkvo_append(BF16 if self.dtype == np.uint16 else F32, self.kv_stride,
                          self.block_size, _p(self.k_pools[layer]), _p(self.v_pools[layer]),
                          _p(self.tables), self.table_stride, _p(self.table_lens),
-                         _p(self.bm.free_list), _p(self.bm.count), _p(pos), _p(n_new), max_new,
-                         _p(k_new), _p(v_new), batch, _p(status))
+                         _p(self.bm.free_list), _p(self.bm.count), _p(pos), _p(tok_off), max_new,
+                         _p(k_new), _p(v_new), k_new.shape[0], batch, _p(status))
         return status
 
     def rollback(self, new_len):

@@ -360,6 +360,8 @@ void pkvo_bm_free(int32_t* free_list, int32_t* free_count, int32_t block_id) {
 }
 
 /* ------------------------------------------------------------- KV append
+ * Sequence s appends n_s = tok_off[s+1] - tok_off[s] tokens whose K / V rows are rows
+ * tok_off[s] .. tok_off[s+1]-1 of k_new / v_new ([total_rows][kv_stride], pool dtype).
  * For each sequence s in index order (the engine serves sequences one after
  * another): for each new token b in order, position p = pos[s] + b grows the
  * table while p // bs >= len(table) (allocate() pops the LIFO back). If a pop
@@ -368,31 +370,33 @@ void pkvo_bm_free(int32_t* free_list, int32_t* free_count, int32_t block_id) {
  * returns before the copy, :1989-1992; verify sets oom_abort before any write,
  * :3017-3026; chunked prefill breaks before the layer pass, :2516-2530).
  * Otherwise the rows row = table[p // bs] * bs + p % bs receive exact copies
- * of k_new / v_new (:1994-2001).
- * pos[s] < 0 or n_new[s] <= 0 skips the sequence (status 0); n_new[s] > max_new is
- * rejected with status -5 (the C ABI's PKV_SEQ_BAD_ARGS).
- * A table that would exceed table_stride entries gives status -2 and no change.
- * k_new/v_new: [batch][max_new][kv_stride] in the pool dtype.               */
+ * of the new rows (:1994-2001).
+ * pos[s] < 0 or n_s <= 0 skips the sequence (status 0). A token range outside
+ * [0, total_rows) or longer than max_new is rejected with status -5 (the C ABI's
+ * PKV_SEQ_BAD_ARGS); a table that would exceed table_stride entries gives status -2
+ * (PKV_SEQ_TABLE_FULL). Neither changes anything.                              */
 void pkvo_append(int dtype, int32_t kv_stride, int32_t block_size, void* k_pool, void* v_pool,
                  int32_t* tables, int32_t table_stride, int32_t* table_lens, int32_t* free_list,
-                 int32_t* free_count, const int32_t* pos, const int32_t* n_new, int32_t max_new,
-                 const void* k_new, const void* v_new, int32_t batch, int32_t* status) {
+                 int32_t* free_count, const int32_t* pos, const int32_t* tok_off, int32_t max_new,
+                 const void* k_new, const void* v_new, int32_t total_rows, int32_t batch,
+                 int32_t* status) {
     size_t elt = dtype == PKVO_BF16 ? 2 : 4;
     for (int32_t s = 0; s < batch; ++s) {
         status[s] = 0;
-        if (pos[s] < 0 || n_new[s] <= 0) continue;
-        if (n_new[s] > max_new) {
+        int32_t r0 = tok_off[s], n = tok_off[s + 1] - tok_off[s];
+        if (pos[s] < 0 || n <= 0) continue;
+        if (n > max_new || r0 < 0 || tok_off[s + 1] > total_rows) {
             status[s] = -5;
             continue;
         }
-        int64_t last = (int64_t)pos[s] + n_new[s] - 1;
+        int64_t last = (int64_t)pos[s] + n - 1;
         if (last / block_size >= table_stride) {
             status[s] = -2;
             continue;
         }
         int32_t* table = tables + (int64_t)s * table_stride;
         int oom = 0;
-        for (int32_t b = 0; b < n_new[s] && !oom; ++b) {
+        for (int32_t b = 0; b < n && !oom; ++b) {
             int64_t p = (int64_t)pos[s] + b;
             while (p / block_size >= table_lens[s]) {
                 int32_t blk = pkvo_bm_allocate(free_list, free_count);
@@ -408,10 +412,10 @@ void pkvo_append(int dtype, int32_t kv_stride, int32_t block_size, void* k_pool,
             status[s] = -1;
             continue;
         }
-        for (int32_t b = 0; b < n_new[s]; ++b) {
+        for (int32_t b = 0; b < n; ++b) {
             int64_t p = (int64_t)pos[s] + b;
             int64_t row = (int64_t)table[p / block_size] * block_size + p % block_size;
-            size_t src = ((size_t)s * max_new + b) * kv_stride * elt;
+            size_t src = ((size_t)r0 + b) * kv_stride * elt;
             memcpy((char*)k_pool + row * kv_stride * elt, (const char*)k_new + src, kv_stride * elt);
             memcpy((char*)v_pool + row * kv_stride * elt, (const char*)v_new + src, kv_stride * elt);
         }

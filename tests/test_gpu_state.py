@@ -39,21 +39,23 @@ def test_random_append_rollback_sequences(gpu, kv_dtype, seed):
     spec, cache, st = _mk(kv_dtype, nseq, bs, num_blocks, stride, layers=2)
     length = np.zeros(nseq, np.int64)
     npdt = np.uint16 if kv_dtype == BF16 else np.float32
-    kd = hip.DeviceArray((nseq, max_new, spec.kv_stride), npdt)
-    vd = hip.DeviceArray((nseq, max_new, spec.kv_stride), npdt)
+    kd = hip.DeviceArray((nseq * max_new, spec.kv_stride), npdt)
+    vd = hip.DeviceArray((nseq * max_new, spec.kv_stride), npdt)
     for step in range(40):
         if rng.random() < 0.7:
             n_new = rng.integers(0, max_new + 1, nseq).astype(np.int32)
             pos = length.astype(np.int32).copy()
             pos[rng.random(nseq) < 0.1] = -1  # inactive slots
-            raw = rng.standard_normal((2, nseq, max_new, spec.kv_stride)).astype(np.float32)
+            off = O.ragged_tok_off(n_new)
+            rows = max(int(off[-1]), 1)
+            raw = rng.standard_normal((2, rows, spec.kv_stride)).astype(np.float32)
             k = O.to_bf16(raw[0]) if kv_dtype == BF16 else raw[0]
             v = O.to_bf16(raw[1]) if kv_dtype == BF16 else raw[1]
-            kd.upload(k)
-            vd.upload(v)
+            kd.upload_at(0, k)
+            vd.upload_at(0, v)
             layer = int(rng.integers(0, 2))
-            ref_status = st.append(layer, pos, n_new, k, v, max_new)
-            status = cache.append(layer, pos, n_new, kd, vd, max_new).numpy()
+            ref_status = st.append(layer, pos, off, k, v, max_new)
+            status = cache.append(layer, pos, off, kd, vd, max_new, rows).numpy()
             np.testing.assert_array_equal(status, ref_status, err_msg=f"step {step}")
             ok = (ref_status == 0) & (pos >= 0)
             length[ok] += n_new[ok]
@@ -73,22 +75,30 @@ def test_out_of_blocks_and_table_full(gpu):
     print("[state] oom / table full", flush=True)
     nseq, bs, num_blocks, stride = 4, 4, 6, 3
     spec, cache, st = _mk(F32, nseq, bs, num_blocks, stride)
-    k = np.arange(nseq * 13 * spec.kv_stride, dtype=np.float32).reshape(nseq, 13, -1)
+    k = np.arange(nseq * 13 * spec.kv_stride, dtype=np.float32).reshape(nseq * 13, -1)
     kd, vd = hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(-k)
     pos = np.array([0, 0, 0, 0], np.int32)
     n_new = np.array([5, 13, 9, 2], np.int32)  # needs 2, 4 (> stride 3: full), 3, 1
-    ref = st.append(0, pos, n_new, k, -k, 13)
-    got = cache.append(0, pos, n_new, kd, vd, 13).numpy()
+    off = O.ragged_tok_off(n_new)
+    ref = st.append(0, pos, off, k, -k, 13)
+    got = cache.append(0, pos, off, kd, vd, 13, nseq * 13).numpy()
     np.testing.assert_array_equal(got, ref)
     assert list(ref) == [lib.PKV_SEQ_OK, lib.PKV_SEQ_TABLE_FULL, lib.PKV_SEQ_OK, lib.PKV_SEQ_OK]
     _compare(cache, st)
     # The pool now has 0 free blocks: a second round runs dry part-way.
     pos2 = np.array([5, -1, 9, 2], np.int32)
-    n2 = np.array([4, 0, 4, 7], np.int32)
-    ref = st.append(0, pos2, n2, k, -k, 13)
-    got = cache.append(0, pos2, n2, kd, vd, 13).numpy()
+    off2 = O.ragged_tok_off([4, 0, 4, 7])
+    ref = st.append(0, pos2, off2, k, -k, 13)
+    got = cache.append(0, pos2, off2, kd, vd, 13, nseq * 13).numpy()
     np.testing.assert_array_equal(got, ref)
     assert lib.PKV_SEQ_OUT_OF_BLOCKS in list(ref)
+    _compare(cache, st)
+    # Token ranges outside the new rows or longer than max_new are rejected unchanged.
+    off3 = np.array([0, 2, 60, 60, 60], np.int32)
+    ref = st.append(0, np.array([1, 0, 3, 3], np.int32), off3, k, -k, 13)
+    got = cache.append(0, np.array([1, 0, 3, 3], np.int32), off3, kd, vd, 13, 52).numpy()
+    np.testing.assert_array_equal(got, ref)
+    assert ref[1] == lib.PKV_SEQ_BAD_ARGS
     _compare(cache, st)
     cache.free()
 
@@ -117,9 +127,9 @@ def test_config1_append_into_new_block(gpu):
     cache.free_count.upload(np.array([free.size], np.int32))
     k = rng.standard_normal((1, 1, spec.kv_stride)).astype(np.float32)
     v = rng.standard_normal((1, 1, spec.kv_stride)).astype(np.float32)
-    st.append(0, [512], [1], k, v, 1)
+    st.append(0, [512], [0, 1], k, v, 1)
     dk, dv = hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(v)
-    cache.append(0, [512], [1], dk, dv, 1)
+    cache.append(0, [512], [0, 1], dk, dv, 1, 1)
     assert st.table_lens[0] == 33 and st.tables[0, 32] == free[-1]
     _compare(cache, st)
     cache.free()

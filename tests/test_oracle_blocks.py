@@ -77,14 +77,15 @@ def test_append_rollback_matches_list_engine(seed):
         if op < 2:  # append a ragged batch
             n_new = rng.integers(0, 6, nseq).astype(np.int32)
             pos = np.array(length, np.int32)
-            k = rng.standard_normal((nseq, 5, kvs)).astype(np.float32)
-            v = rng.standard_normal((nseq, 5, kvs)).astype(np.float32)
-            status = st.append(0, pos, n_new, k, v, 5)
+            off = O.ragged_tok_off(n_new)
+            k = rng.standard_normal((int(off[-1]) + 1, kvs)).astype(np.float32)
+            v = rng.standard_normal((int(off[-1]) + 1, kvs)).astype(np.float32)
+            status = st.append(0, pos, off, k, v, 5)
             for s in range(nseq):
                 if n_new[s] == 0:
                     assert status[s] == 0
                     continue
-                rc = eng.append(s, length[s], [tuple(k[s, b]) for b in range(n_new[s])])
+                rc = eng.append(s, length[s], [tuple(k[off[s] + b]) for b in range(n_new[s])])
                 assert status[s] == rc, (step, s)
                 if rc == 0:
                     length[s] += int(n_new[s])
@@ -113,7 +114,7 @@ def test_decode_append_allocates_on_block_boundary_only():
     st = O.CacheState(1, 4, 16, 8, 1, 8)
     k = np.ones((1, 1, 4), np.float32)
     for p in range(33):
-        st.append(0, [p], [1], k * p, k * -p, 1)
+        st.append(0, [p], [0, 1], k * p, k * -p, 1)
         assert st.table_lens[0] == p // 16 + 1
     # LIFO: first allocation is the last block (max-1), then max-2, ...
     assert list(st.tables[0, :3]) == [7, 6, 5]
@@ -126,8 +127,8 @@ def test_decode_append_allocates_on_block_boundary_only():
 def test_out_of_blocks_keeps_popped_blocks_and_writes_nothing():
     # verify-style multi-token append that runs out mid-way (…batched.mojo:3011-3023)
     st = O.CacheState(1, 4, 4, 3, 2, 8)
-    k = np.arange(2 * 12 * 4, dtype=np.float32).reshape(2, 12, 4)
-    status = st.append(0, [0, 0], [4, 12], k, k, 12)
+    k = np.arange(16 * 4, dtype=np.float32).reshape(16, 4)
+    status = st.append(0, [0, 0], [0, 4, 16], k, k, 12)
     assert list(status) == [0, -1]
     assert list(st.tables[0, :1]) == [2]
     assert list(st.tables[1, :st.table_lens[1]]) == [1, 0]  # popped before the list ran dry
@@ -136,22 +137,27 @@ def test_out_of_blocks_keeps_popped_blocks_and_writes_nothing():
     for blk in (1, 0):
         assert np.all(st.k_pools[0][blk * 16:(blk + 1) * 16] == 0)
     # decode append for seq 0 into its partially filled block still works
-    status = st.append(0, [4, -1], [0, 0], k, k, 12)
+    status = st.append(0, [4, -1], [0, 0, 0], k, k, 12)
     assert list(status) == [0, 0]
+    # a token range beyond the new rows, or longer than max_new, is rejected unchanged
+    status = st.append(0, [3, 0], [0, 1, 17], k, k, 12)
+    assert list(status) == [0, -5]
+    status = st.append(0, [5, 0], [0, 13, 14], k, k, 12)
+    assert list(status) == [-5, 0]  # seq 1 writes into a block it already holds
 
 
 def test_table_full_is_reported_and_changes_nothing():
     st = O.CacheState(1, 4, 4, 16, 1, 2)
-    k = np.ones((1, 9, 4), np.float32)
-    status = st.append(0, [0], [9], k, k, 9)  # needs 3 blocks, table holds 2
+    k = np.ones((9, 4), np.float32)
+    status = st.append(0, [0], [0, 9], k, k, 9)  # needs 3 blocks, table holds 2
     assert list(status) == [-2]
     assert st.table_lens[0] == 0 and st.bm.count[0] == 16
 
 
 def test_rollback_semantics():
     st = O.CacheState(1, 4, 16, 16, 2, 8)
-    k = np.zeros((2, 40, 4), np.float32)
-    st.append(0, [0, 0], [40, 33], k, k, 40)
+    k = np.zeros((73, 4), np.float32)
+    st.append(0, [0, 0], [0, 40, 73], k, k, 40)
     assert list(st.table_lens) == [3, 3]
     t0, t1 = list(st.tables[0, :3]), list(st.tables[1, :3])
     st.rollback([32, 17])  # keep ceil(32/16)=2 and ceil(17/16)=2
@@ -169,16 +175,16 @@ def test_rollback_then_reappend_matches_fresh_run():
     bs = 16
     a = O.CacheState(1, 4, bs, 64, 1, 16)
     b = O.CacheState(1, 4, bs, 64, 1, 16)
-    k = np.zeros((1, 200, 4), np.float32)
-    a.append(0, [0], [30], k, k, 200)
-    b.append(0, [0], [30], k, k, 200)
-    a.append(0, [30], [4], k, k, 200)  # draft crosses into a third block
+    k = np.zeros((200, 4), np.float32)
+    a.append(0, [0], [0, 30], k, k, 200)
+    b.append(0, [0], [0, 30], k, k, 200)
+    a.append(0, [30], [0, 4], k, k, 200)  # draft crosses into a third block
     a.rollback([31])  # accept 1 -> back to 2 blocks
-    b.append(0, [30], [1], k, k, 200)
+    b.append(0, [30], [0, 1], k, k, 200)
     np.testing.assert_array_equal(a.table_lens, b.table_lens)
     np.testing.assert_array_equal(a.tables[0, :a.table_lens[0]], b.tables[0, :b.table_lens[0]])
     np.testing.assert_array_equal(a.free_list[:-1], b.free_list[:-1])
     # a holds the freed block on top of its free list; the next allocation takes it back
-    a.append(0, [31], [10], k, k, 200)
-    b.append(0, [31], [10], k, k, 200)
+    a.append(0, [31], [0, 10], k, k, 200)
+    b.append(0, [31], [0, 10], k, k, 200)
     assert a.table_lens[0] == b.table_lens[0] == 3
