@@ -36,15 +36,16 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, AMD published
 
 def _traffic_from_profiles():
     """HBM bytes per attention launch measured by rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), when committed under profiles/."""
-    path = os.path.join(REPO, "profiles", "attend_decode_cfg2_traffic.json")
-    if not os.path.exists(path):
-        return None
+    WRITE_SIZE, scaled by the copy-kernel calibration), from the committed summary."""
+    path = os.path.join(REPO, "profiles", "attend_decode_cfg2_traffic.md")
     try:
         with open(path) as f:
-            return json.load(f).get("bytes_per_launch")
+            for line in f:
+                if line.startswith("bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
     except (OSError, ValueError):
-        return None
+        pass
+    return None
 
 
 def run_gpu(sched, data, steps, warmup, log):
