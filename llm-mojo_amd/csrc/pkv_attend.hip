@@ -603,6 +603,14 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     const int G = p->num_heads / p->num_kv_heads;
     const int rows = G * q_len;
     if (rows > 16) return fail(PKV_ERR_UNSUPPORTED, "q_len * (num_heads / num_kv_heads) must be <= 16");
+    if (batch > 4096) return fail(PKV_ERR_INVALID, "batch must be <= 4096");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (stream_eligible(p, rows) && workspace_bytes >= stream_layout(p, batch, q_len).total) {
+        rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
+                           q_len, batch, out, workspace, st);
+        if (rc != PKV_OK) return rc;
+        return check_launch("pkv_attend");
+    }
     AttendLayout lay = attend_layout(p, batch, q_len, max_pos);
     if (lay.chunk > kMaxChunk) return fail(PKV_ERR_UNSUPPORTED, "chunk larger than the kernel's LDS bound");
     if (workspace_bytes < lay.total)
@@ -632,7 +640,6 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     a.part_o = ws + lay.o_off;
     a.out = out;
     dim3 grid(lay.max_chunks, p->num_kv_heads, batch);
-    hipStream_t st = static_cast<hipStream_t>(stream);
     const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
     switch (p->head_dim) {
         case 64: rc = bf16 ? dispatch_rows<64, uint16_t>(a, rows, grid, st)

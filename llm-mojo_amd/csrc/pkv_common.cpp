@@ -82,7 +82,9 @@ extern "C" {
 size_t pkv_workspace_size(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos) {
     if (pkv::validate_params(p) != PKV_OK) return 0;
     if (batch <= 0 || q_len <= 0 || max_pos < 0) return 0;
-    return pkv::attend_layout(p, batch, q_len, max_pos).total;
+    const size_t chunked = pkv::attend_layout(p, batch, q_len, max_pos).total;
+    const size_t stream = pkv::stream_layout(p, batch, q_len).total;
+    return chunked > stream ? chunked : stream;
 }
 
 const char* pkv_last_error(void) { return pkv::g_last_error.c_str(); }

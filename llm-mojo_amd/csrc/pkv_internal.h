@@ -38,6 +38,25 @@ struct AttendLayout {
 };
 AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos);
 
+// Stream-K attention (pkv_stream.hip): workspace layout and entry.
+//   plan   int32 [batch + 2]       per, then the key prefix of every sequence
+//   part_ml                        double (m, l) per (slot, row)
+//   part_o                         double [head_dim] per (slot, row)
+// slots = kMaxSlots + batch, rows = num_heads * q_len.
+struct StreamLayout {
+    size_t plan_off;
+    size_t ml_off;
+    size_t o_off;
+    size_t total;
+};
+StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len);
+// True when the stream kernel covers this geometry (head_dim 256, <= 8 rows per kv head).
+bool stream_eligible(const pkv_params* p, int32_t rows);
+int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
+                      const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                      const int32_t* pos, int32_t pos_scalar, int32_t q_len, int32_t batch,
+                      float* out, void* workspace, hipStream_t st);
+
 __host__ __device__ inline int32_t window_start(int32_t pos, int32_t window) {
     if (window <= 0) return 0;
     int32_t s = pos - window + 1;

@@ -1,0 +1,774 @@
+// K2 hot path -- stream-K paged attention over whole pages (decode and verify).
+//
+// Replaces the reference's three-pass CPU loop (attention.mojo:151-294) for head_dim
+// 256 with up to 8 query rows per KV head (decode: G = Hq / Hkv rows; verify: G x q_len).
+//
+// Work split. The keys every sequence attends ([window_start(pos), pos + q_len - 1])
+// are laid end to end, sequence after sequence; workgroup w takes the w-th run of
+// `per` keys of that concatenation (per = ceil(total / P), P workgroups sized to fill
+// the chip once), so every workgroup streams the same number of bytes whatever the mix
+// of context lengths. A workgroup has one wave per KV head (up to 8): the waves walk the
+// same tokens together, so the workgroup reads whole 16-token pages -- 16 rows of
+// Hkv*D*elt contiguous bytes (128 KiB for fp32, 8 heads, D=256) -- instead of 1 KiB
+// slices scattered over the pool. Where a run crosses a sequence boundary the wave
+// finishes one sequence's piece and starts the next. Sequences covered by a single
+// piece write their output directly; the others write (m, l, o) partials, combined by
+// stream_merge_kernel (a second launch, so no device-scope fences are needed).
+// Piece (w, s) of workgroup w and sequence s is stored at slot w + s: the pieces are
+// ordered by both w and s, so w + s is unique and below P + batch.
+//
+// Per wave and batch of U tokens (one token per load instruction: 64 lanes x D/64
+// elements, 16-byte loads for fp32, 8-byte for bf16):
+//   1. the K and V rows of all U tokens are loaded first (addresses are wave-uniform:
+//      page id by readlane from a register holding the piece's page ids, offsets in
+//      scalar registers), so 2U loads are in flight together;
+//   2. partial dots of U tokens x R rows reduced across the 64 lanes by a halving
+//      exchange: permlane32/permlane16 swaps for the two wide levels, DPP inside rows
+//      for the rest (no LDS traffic); afterwards lane l holds dot l / REP;
+//   3. online softmax per row: batch max / sum over the lanes of a row by DPP
+//      rotations and permlane swaps, one exponential per lane, the accumulators
+//      rescaled only when a row's max moves;
+//   4. PV: p broadcast by readlane, accumulated in registers.
+// fp32 pools accumulate in double (scores, exponentials, PV, partials, merge) so the
+// output is the exact attention rounded once to fp32 -- the reference fp32 path carries
+// ~1e-7 absolute error of its own and the parity bound leaves no room for a second
+// error of that size. On CDNA3/4 a non-packed double FMA issues at the fp32 rate.
+// bf16 pools accumulate in fp32.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "pkv_internal.h"
+
+namespace pkv {
+namespace {
+
+#ifndef PKV_STREAM_WAVES
+#define PKV_STREAM_WAVES 8
+#endif
+#ifndef PKV_STREAM_PER_MIN
+#define PKV_STREAM_PER_MIN 64
+#endif
+
+constexpr int kSW = 64;                          // wavefront
+constexpr int kMaxWaves = PKV_STREAM_WAVES;      // KV heads handled by one workgroup
+constexpr int kMergeNT = 256;                    // merge kernel threads
+constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
+
+template <typename KV>
+struct SKV;
+template <>
+struct SKV<float> {
+    using Acc = double;
+    static constexpr int kElt = 4;
+};
+template <>
+struct SKV<uint16_t> {  // bf16 bits
+    using Acc = float;
+    static constexpr int kElt = 2;
+};
+
+// Tokens per batch for R query rows (register budget: 2U loads in flight).
+#ifndef PKV_STREAM_U32
+#define PKV_STREAM_U32 8
+#endif
+#ifndef PKV_STREAM_U16
+#define PKV_STREAM_U16 16
+#endif
+template <typename KV, int R>
+constexpr int batch_tokens() {
+    constexpr int u = sizeof(KV) == 4 ? PKV_STREAM_U32 : PKV_STREAM_U16;  // at R <= 2
+    return R <= 2 ? u : (R == 4 ? u / 2 : u / 4);
+}
+
+// ---- cross-lane primitives (wave64) -------------------------------------------------
+
+template <int CTRL>
+__device__ inline uint32_t dpp32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ inline float dpp(float v) {
+    return __uint_as_float(dpp32<CTRL>(__float_as_uint(v)));
+}
+template <int CTRL>
+__device__ inline double dpp(double v) {
+    const uint32_t lo = dpp32<CTRL>((uint32_t)__double2loint(v));
+    const uint32_t hi = dpp32<CTRL>((uint32_t)__double2hiint(v));
+    return __hiloint2double((int)hi, (int)lo);
+}
+
+// DPP controls (within rows of 16 lanes).
+constexpr int kRor8 = 0x128;        // l -> l ^ 8
+constexpr int kHalfMirror = 0x141;  // l -> l ^ 7 (within 8)
+constexpr int kQuadX2 = 0x4E;       // quad_perm [2,3,0,1]: l -> l ^ 2
+constexpr int kQuadX1 = 0xB1;       // quad_perm [1,0,3,2]: l -> l ^ 1
+template <int O>
+constexpr int ror_ctrl() { return 0x120 + O; }  // row_ror:O
+
+// v_permlane{32,16}_swap: lanes 32-63 (odd 16-lane rows) of `a` swap places with
+// lanes 0-31 (even rows) of `b`. Afterwards a + b holds, in the lower lanes, a summed
+// with its partner lane l ^ O and, in the upper lanes, b summed likewise.
+template <int O>
+__device__ inline void swap_u32(uint32_t& a, uint32_t& b) {
+    if constexpr (O == 32) {
+        auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        a = r[0];
+        b = r[1];
+    } else {
+        static_assert(O == 16, "swap levels are 32 and 16");
+        auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        a = r[0];
+        b = r[1];
+    }
+}
+template <int O>
+__device__ inline void swap_halves(float& a, float& b) {
+    uint32_t x = __float_as_uint(a), y = __float_as_uint(b);
+    swap_u32<O>(x, y);
+    a = __uint_as_float(x);
+    b = __uint_as_float(y);
+}
+template <int O>
+__device__ inline void swap_halves(double& a, double& b) {
+    uint32_t al = (uint32_t)__double2loint(a), ah = (uint32_t)__double2hiint(a);
+    uint32_t bl = (uint32_t)__double2loint(b), bh = (uint32_t)__double2hiint(b);
+    swap_u32<O>(al, bl);
+    swap_u32<O>(ah, bh);
+    a = __hiloint2double((int)ah, (int)al);
+    b = __hiloint2double((int)bh, (int)bl);
+}
+
+// Partner of lane l at level O of the halving exchange (O <= 8). At O = 4 the partner
+// is l ^ 7, which also flips bits 0-1; the exchange stays correct because levels 2 and
+// 1 afterwards sum over those bits completely.
+template <int O, typename T>
+__device__ inline T xpartner(T v) {
+    if constexpr (O == 8) return dpp<kRor8>(v);
+    else if constexpr (O == 4) return dpp<kHalfMirror>(v);
+    else if constexpr (O == 2) return dpp<kQuadX2>(v);
+    else return dpp<kQuadX1>(v);
+}
+
+// Sum of N values per lane over all 64 lanes by halving exchange. On return lane l
+// holds the total of value index l / (64 / N) (N a power of two <= 64).
+template <int N, int O, typename T>
+__device__ inline void xred(T* v, int lane) {
+    if constexpr (O == 0) {
+        return;
+    } else if constexpr (N == 1) {
+        if constexpr (O >= 16) {
+            T a = v[0], b = v[0];
+            swap_halves<O>(a, b);
+            v[0] = a + b;
+        } else {
+            v[0] += xpartner<O>(v[0]);
+        }
+        xred<1, O / 2>(v, lane);
+    } else {
+        constexpr int H = N / 2;
+        if constexpr (O >= 16) {
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                T a = v[i], b = v[i + H];
+                swap_halves<O>(a, b);
+                v[i] = a + b;
+            }
+        } else {
+            const bool upper = (lane & O) != 0;
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const T send = upper ? v[i] : v[i + H];
+                const T keep = upper ? v[i + H] : v[i];
+                v[i] = keep + xpartner<O>(send);
+            }
+        }
+        xred<H, O / 2>(v, lane);
+    }
+}
+
+// All-reduce over lane bits [log2(O0), 6) (the lanes that differ only in those bits):
+// rotations inside 16-lane rows for the bits below 4, then the two swaps.
+struct OpMax {
+    template <typename T>
+    __device__ T operator()(T a, T b) const { return fmax(a, b); }
+};
+struct OpSum {
+    template <typename T>
+    __device__ T operator()(T a, T b) const { return a + b; }
+};
+template <int O, int O0, typename T, typename Op>
+__device__ inline T allreduce_rows(T x, Op op) {
+    if constexpr (O > 8) {
+        return x;
+    } else {
+        if constexpr (O >= O0) x = op(x, dpp<ror_ctrl<O>()>(x));
+        return allreduce_rows<O * 2, O0>(x, op);
+    }
+}
+template <int O0, typename T, typename Op>
+__device__ inline T allreduce_hi(T x, Op op) {
+    static_assert(O0 >= 1 && O0 <= 64, "offset");
+    if constexpr (O0 < 64) {
+        if constexpr (O0 <= 8) x = allreduce_rows<1, O0>(x, op);
+        if constexpr (O0 <= 16) {
+            T a = x, b = x;
+            swap_halves<16>(a, b);
+            x = op(a, b);
+        }
+        T a = x, b = x;
+        swap_halves<32>(a, b);
+        x = op(a, b);
+    }
+    return x;
+}
+
+__device__ inline double bcast(double v, int src) {
+    const int lo = __builtin_amdgcn_readlane(__double2loint(v), src);
+    const int hi = __builtin_amdgcn_readlane(__double2hiint(v), src);
+    return __hiloint2double(hi, lo);
+}
+__device__ inline float bcast(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+__device__ inline int ufirst(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// Global-memory (address space 1) pointers for the device pass; the host pass only
+// parses the kernels and keeps generic pointers.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define PKV_GLOBAL __attribute__((address_space(1)))
+#else
+#define PKV_GLOBAL
+#endif
+typedef const PKV_GLOBAL char gchar;
+// A wave-uniform address held in scalar registers, so a load adds only the 32-bit lane
+// offset (global_load ... v_off, s[base]) instead of a 64-bit vector add per load.
+__device__ inline gchar* uniform_ptr(const char* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<gchar*>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ inline double exp_acc(double x) { return exp(x); }
+__device__ inline float exp_acc(float x) { return expf(x); }
+
+// ---- loads ------------------------------------------------------------------------
+
+// NW 32-bit words per lane from a lane-contiguous run.
+template <int NW>
+__device__ inline void load_words(gchar* p, uint32_t (&w)[NW]) {
+    typedef const PKV_GLOBAL uint4 g4;
+    typedef const PKV_GLOBAL uint2 g2;
+    typedef const PKV_GLOBAL uint32_t g1;
+    if constexpr (NW % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < NW / 4; ++i) {
+            const uint4 v = reinterpret_cast<g4*>(p)[i];
+            w[4 * i + 0] = v.x;
+            w[4 * i + 1] = v.y;
+            w[4 * i + 2] = v.z;
+            w[4 * i + 3] = v.w;
+        }
+    } else if constexpr (NW == 2) {
+        const uint2 v = *reinterpret_cast<g2*>(p);
+        w[0] = v.x;
+        w[1] = v.y;
+    } else {
+        static_assert(NW == 1, "words per lane");
+        w[0] = *reinterpret_cast<g1*>(p);
+    }
+}
+
+template <typename A, int NW>
+__device__ inline void unpack_words(const uint32_t (&w)[NW], A* out, float) {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) out[i] = (A)__uint_as_float(w[i]);
+}
+template <typename A, int NW>
+__device__ inline void unpack_words(const uint32_t (&w)[NW], A* out, uint16_t) {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        out[2 * i] = (A)bf16_lo(w[i]);
+        out[2 * i + 1] = (A)bf16_hi(w[i]);
+    }
+}
+
+// ---- kernels ----------------------------------------------------------------------
+
+struct StreamArgs {
+    const float* q;
+    const char* k_pool;
+    const char* v_pool;
+    const int32_t* tables;
+    int32_t table_stride;
+    const int32_t* pos;  // null -> pos_scalar (single sequence)
+    int32_t pos_scalar;
+    int32_t q_len;
+    int32_t Hq;
+    int32_t Hkv;
+    int32_t G;
+    int32_t bs_shift;
+    int32_t num_blocks;
+    int32_t window;
+    float scale;
+    int32_t batch;
+    int32_t nwg;       // P: workgroups along the keys
+    int32_t rows_seq;  // Hq * q_len
+    int32_t* plan;     // [0] = per, [1 + s] = key prefix of sequence s (s <= batch)
+    void* part_ml;     // Acc (m, l) per (slot, row)
+    void* part_o;      // Acc [D] per (slot, row)
+    float* out;
+};
+
+__device__ inline size_t out_row(const StreamArgs& a, int s, int g, int r) {
+    const int j = r / a.G, h = g * a.G + r % a.G;
+    return ((size_t)s * a.q_len + j) * a.Hq + h;
+}
+
+// Exclusive scan of the key counts in s_pre[0..batch) (in place, one wave), total in
+// s_pre[batch].
+__device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
+    int carry = 0;
+    for (int base = 0; base < batch; base += kSW) {
+        const int i = base + lane;
+        const int v = i < batch ? s_pre[i] : 0;
+        int incl = v;
+#pragma unroll
+        for (int o = 1; o < kSW; o <<= 1) {
+            const int t = __shfl_up(incl, o);
+            if (lane >= o) incl += t;
+        }
+        if (i < batch) s_pre[i] = carry + incl - v;
+        carry += __shfl(incl, kSW - 1);
+    }
+    if (lane == 0) s_pre[batch] = carry;
+}
+
+template <int D, typename KV, int R>
+__global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamArgs a) {
+    using Acc = typename SKV<KV>::Acc;
+    constexpr int kElt = SKV<KV>::kElt;
+    constexpr int EPL = D / kSW;                // elements per lane per token
+    constexpr int NWD = EPL * kElt / 4;         // 32-bit words per lane per token
+    constexpr int U = batch_tokens<KV, R>();    // tokens per batch
+    constexpr int NV = U * R;                   // dots per batch
+    static_assert(NV <= kSW && (NV & (NV - 1)) == 0, "dots per batch: power of two <= 64");
+    constexpr int REP = kSW / NV;               // lanes holding the same reduced dot
+    constexpr int ROWB = R * REP;               // lane offset of the first token bit
+
+    extern __shared__ int smem[];
+    int* s_pre = smem;                  // [batch + 1]
+    int* s_lo = smem + a.batch + 1;     // [batch]: window start, -1 inactive, -2 bad
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kSW - 1);
+    const int wave = ufirst(tid / kSW);
+    const int nthr = blockDim.x;
+    const int w = blockIdx.y;
+    const int B = a.batch;
+
+    for (int i = tid; i < B; i += nthr) {
+        const int p0 = a.pos ? a.pos[i] : a.pos_scalar;
+        int n = 0, lo = -1;
+        if (p0 >= 0) {
+            const int hi = p0 + a.q_len - 1;
+            if ((hi >> a.bs_shift) < a.table_stride) {
+                lo = window_start(p0, a.window);
+                n = hi - lo + 1;
+            } else {
+                lo = -2;
+            }
+        }
+        s_pre[i] = n;
+        s_lo[i] = lo;
+    }
+    __syncthreads();
+    if (wave == 0) wave_scan_counts(s_pre, B, lane);
+    __syncthreads();
+
+    const int total = ufirst(s_pre[B]);
+    const int per = max(kPerMin, (total + a.nwg - 1) / a.nwg);
+    if (w == 0 && blockIdx.x == 0) {
+        // Plan for the merge launch; inactive sequences get zeros, contract violations NaN.
+        if (tid == 0) a.plan[0] = per;
+        for (int i = tid; i <= B; i += nthr) a.plan[1 + i] = s_pre[i];
+        for (int s = 0; s < B; ++s) {
+            const int lo = s_lo[s];
+            if (lo >= 0) continue;
+            const float fill = lo == -1 ? 0.f : __builtin_nanf("");
+            for (int i = tid; i < a.rows_seq * D; i += nthr)
+                a.out[((size_t)s * a.rows_seq + i / D) * D + i % D] = fill;
+        }
+    }
+    const int k0 = w * per;
+    if (k0 >= total) return;
+    const int k1 = min(total, k0 + per);
+    const int g = blockIdx.x * kMaxWaves + wave;  // this wave's KV head
+    if (g >= a.Hkv) return;
+
+    const int rows = a.G * a.q_len;
+    const size_t row_bytes = (size_t)a.Hkv * D * kElt;
+    const char* kbase = a.k_pool + (size_t)g * D * kElt;  // wave-uniform
+    const char* vbase = a.v_pool + (size_t)g * D * kElt;
+    const uint32_t lane_off = (uint32_t)lane * EPL * kElt;
+    const int bs_mask = (1 << a.bs_shift) - 1;
+
+    // lane -> (token u_own, row r_own) of the reduced dot it holds
+    const int idx_own = lane / REP;
+    const int r_own = idx_own % R;
+    const int u_own = idx_own / R;
+    const bool row_live = r_own < rows;
+
+    // first sequence with s_pre[s] <= k0 < s_pre[s + 1]
+    int s = 0;
+    {
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (ufirst(s_pre[mid]) <= k0) lo = mid;
+            else hi = mid - 1;
+        }
+        s = lo;
+    }
+    for (; s < B; ++s) {
+        const int ps = ufirst(s_pre[s]);
+        const int pe = ufirst(s_pre[s + 1]);
+        if (ps >= k1) break;
+        if (pe == ps) continue;
+        const int lo_key = ufirst(s_lo[s]);
+        const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
+        const int tb = lo_key + min(k1, pe) - ps;  // one past the last
+        const bool single = (ps / per) == ((pe - 1) / per);
+        const int pos0 = a.pos ? ufirst(a.pos[s]) : a.pos_scalar;
+
+        // Query rows -> registers (scaled); rows beyond `rows` stay zero.
+        Acc qr[R][EPL];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r < rows) {
+                const float* qp = a.q + out_row(a, s, g, r) * D + lane * EPL;
+#pragma unroll
+                for (int e = 0; e < EPL; e += 2) {
+                    const float2 v = *reinterpret_cast<const float2*>(qp + e);
+                    qr[r][e] = (Acc)v.x * (Acc)a.scale;
+                    qr[r][e + 1] = (Acc)v.y * (Acc)a.scale;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) qr[r][e] = (Acc)0;
+            }
+        }
+        const int pq_own = pos0 + r_own / a.G;  // query position of my row
+        const int ws_own = window_start(pq_own, a.window);
+
+        Acc m_own = (Acc)-INFINITY, l_own = (Acc)0;
+        Acc acc[R][EPL];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[r][e] = (Acc)0;
+
+        const int32_t* trow = a.tables + (size_t)s * a.table_stride;
+        const int last_page = (tb - 1) >> a.bs_shift;
+        int pgbase = -kSW;  // page index held by lane 0 of vpg
+        int vpg = 0;
+        bool bad = false;
+
+        for (int t = ta; t < tb; t += U) {
+            const int tl = min(t + U - 1, tb - 1);
+            if ((tl >> a.bs_shift) - pgbase >= kSW) {  // page ids of the next 64 pages
+                pgbase = t >> a.bs_shift;
+                int b = 0;
+                if (pgbase + lane <= last_page) {
+                    b = trow[pgbase + lane];
+                    if (b < 0 || b >= a.num_blocks) {
+                        bad = true;
+                        b = 0;
+                    }
+                }
+                vpg = b;
+            }
+            // K and V rows of the batch, all in flight together (tokens past the piece
+            // re-read its last row and are masked).
+            uint32_t kw[U][NWD], vw[U][NWD];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int tt = min(t + u, tb - 1);
+                const int page = __builtin_amdgcn_readlane(vpg, (tt >> a.bs_shift) - pgbase);
+                const size_t off = (((size_t)page << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
+                load_words<NWD>(uniform_ptr(kbase + off) + lane_off, kw[u]);
+                load_words<NWD>(uniform_ptr(vbase + off) + lane_off, vw[u]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep all 2U loads ahead of the math
+            // scores
+            Acc dots[NV];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                Acc kf[EPL];
+                unpack_words<Acc, NWD>(kw[u], kf, KV());
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    Acc d = (Acc)0;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) d = fma(qr[r][e], kf[e], d);
+                    dots[u * R + r] = d;
+                }
+            }
+            xred<NV, kSW / 2>(dots, lane);
+            const int t_own = t + u_own;
+            const bool ok = row_live && t_own < tb && t_own <= pq_own && t_own >= ws_own;
+            const Acc sc = ok ? dots[0] : (Acc)-INFINITY;
+            const Acc mb = allreduce_hi<ROWB>(sc, OpMax());
+            const Acc m_new = fmax(m_own, mb);
+            const Acc p_own = ok ? exp_acc(sc - m_new) : (Acc)0;
+            const Acc lb = allreduce_hi<ROWB>(p_own, OpSum());
+            const bool moved = m_new != m_own;
+            Acc scl = (Acc)1;
+            if (moved) scl = exp_acc(m_own - m_new);  // m_own = -inf gives 0
+            l_own = l_own * scl + lb;
+            m_own = m_new;
+            if (__any(moved)) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const Acc f = bcast(scl, r * REP);
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[r][e] *= f;
+                }
+            }
+            // PV
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                Acc vf[EPL];
+                unpack_words<Acc, NWD>(vw[u], vf, KV());
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const Acc p = bcast(p_own, (u * R + r) * REP);
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[r][e] = fma(p, vf[e], acc[r][e]);
+                }
+            }
+        }
+        bad = __any(bad);
+
+        if (single) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (r < rows) {
+                    const Acc inv = (Acc)1 / (bcast(l_own, r * REP) + (Acc)1e-10);
+                    float* op = a.out + out_row(a, s, g, r) * D + lane * EPL;
+#pragma unroll
+                    for (int e = 0; e < EPL; e += 2) {
+                        float2 v;
+                        v.x = bad ? __builtin_nanf("") : (float)(acc[r][e] * inv);
+                        v.y = bad ? __builtin_nanf("") : (float)(acc[r][e + 1] * inv);
+                        *reinterpret_cast<float2*>(op + e) = v;
+                    }
+                }
+            }
+        } else {
+            const size_t slot = (size_t)(w + s) * a.rows_seq;
+            Acc* po = static_cast<Acc*>(a.part_o);
+            Acc* pml = static_cast<Acc*>(a.part_ml);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (r < rows) {
+                    const int row = (r / a.G) * a.Hq + g * a.G + r % a.G;
+                    Acc* dst = po + (slot + row) * D + lane * EPL;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) dst[e] = acc[r][e];
+                    if (lane == r * REP) {
+                        pml[(slot + row) * 2 + 0] = bad ? (Acc)__builtin_nan("") : m_own;
+                        pml[(slot + row) * 2 + 1] = l_own;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Combines the pieces of every sequence that spans more than one workgroup:
+//   out = sum_c o_c e^(m_c - M) / (sum_c l_c e^(m_c - M) + 1e-10),  M = max_c m_c,
+// the reference's softmax(x)_i = e^(x_i - max) / (sum + 1e-10). One workgroup per
+// (row, sequence). A NaN m_c marks a piece that met a table entry outside the pool.
+template <int D, typename Acc>
+__global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
+    constexpr int kMaxPieces = 1024;
+    __shared__ Acc s_w[kMaxPieces];
+    __shared__ Acc s_part[kMergeNT / kSW];
+    __shared__ int s_nan;
+    const int row = blockIdx.x;
+    const int s = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kSW - 1);
+    const int wave = tid / kSW;
+    const int per = a.plan[0];
+    const int ps = a.plan[1 + s], pe = a.plan[2 + s];
+    if (pe == ps) return;
+    const int wf = ps / per, wl = (pe - 1) / per;
+    if (wf == wl) return;
+    const int cnt = wl - wf + 1;  // <= nwg <= kMaxPieces
+    const Acc* pml = static_cast<const Acc*>(a.part_ml);
+    const Acc* po = static_cast<const Acc*>(a.part_o);
+    auto slot_row = [&](int c) -> size_t { return (size_t)(wf + c + s) * a.rows_seq + row; };
+
+    if (tid == 0) s_nan = 0;
+    __syncthreads();
+    Acc M = (Acc)-INFINITY;
+    for (int c = tid; c < cnt; c += kMergeNT) {
+        const Acc m = pml[slot_row(c) * 2];
+        if (m != m) s_nan = 1;
+        M = fmax(M, m);
+        s_w[c] = m;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmax(M, __shfl_xor(M, o));
+    if (lane == 0) s_part[wave] = M;
+    __syncthreads();
+    M = s_part[0];
+#pragma unroll
+    for (int i = 1; i < kMergeNT / kSW; ++i) M = fmax(M, s_part[i]);
+    __syncthreads();
+    Acc L = (Acc)0;
+    for (int c = tid; c < cnt; c += kMergeNT) {
+        const Acc m = s_w[c];
+        const Acc wgt = (m == (Acc)-INFINITY) ? (Acc)0 : exp_acc(m - M);
+        s_w[c] = wgt;
+        L += pml[slot_row(c) * 2 + 1] * wgt;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
+    if (lane == 0) s_part[wave] = L;
+    __syncthreads();
+    L = (Acc)0;
+#pragma unroll
+    for (int i = 0; i < kMergeNT / kSW; ++i) L += s_part[i];
+    const Acc inv = (Acc)1 / (L + (Acc)1e-10);
+    const bool nan = s_nan != 0;
+    for (int d = tid; d < D; d += kMergeNT) {
+        Acc o8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o8[i] = (Acc)0;
+        int c = 0;
+        for (; c + 8 <= cnt; c += 8) {  // eight independent loads in flight
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o8[i] = fma(s_w[c + i], po[slot_row(c + i) * D + d], o8[i]);
+        }
+        for (; c < cnt; ++c) o8[0] = fma(s_w[c], po[slot_row(c) * D + d], o8[0]);
+        const Acc o = ((o8[0] + o8[1]) + (o8[2] + o8[3])) + ((o8[4] + o8[5]) + (o8[6] + o8[7]));
+        a.out[((size_t)s * a.rows_seq + row) * D + d] = nan ? __builtin_nanf("") : (float)(o * inv);
+    }
+}
+
+// ---- host -------------------------------------------------------------------------
+
+constexpr int kMaxSlots = 1024;  // workgroups along the keys, at most (merge LDS bound)
+
+struct Occ {
+    std::mutex mu;
+    std::map<std::pair<const void*, int>, int> blocks;  // (kernel, device) -> P
+};
+Occ& occ() {
+    static Occ o;
+    return o;
+}
+
+// Workgroups that fill the device once (all resident together), capped at kMaxSlots.
+int fill_workgroups(const void* fn, int threads, size_t lds) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    Occ& o = occ();
+    std::lock_guard<std::mutex> lk(o.mu);
+    auto key = std::make_pair(fn, dev);
+    auto it = o.blocks.find(key);
+    if (it != o.blocks.end()) return it->second;
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return -1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess)
+        return -1;
+    int p = cus * (per_cu > 0 ? per_cu : 1);
+    if (p > kMaxSlots) p = kMaxSlots;
+    o.blocks.emplace(key, p);
+    return p;
+}
+
+template <int D, typename KV, int R>
+int32_t launch_r(StreamArgs a, hipStream_t st) {
+    using Acc = typename SKV<KV>::Acc;
+    const int waves = a.Hkv < kMaxWaves ? a.Hkv : kMaxWaves;
+    const int threads = waves * kSW;
+    const size_t lds = (size_t)(2 * a.batch + 1) * sizeof(int);
+    const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R>);
+    const int slots = fill_workgroups(fn, threads, lds);
+    if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
+    // Launch-resident workgroups only: each covers ceil(total / slots) keys.
+    a.nwg = slots;
+    dim3 grid((a.Hkv + kMaxWaves - 1) / kMaxWaves, a.nwg);
+    hipLaunchKernelGGL((stream_attend_kernel<D, KV, R>), grid, dim3(threads), lds, st, a);
+    hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch), dim3(kMergeNT),
+                       0, st, a);
+    return PKV_OK;
+}
+
+}  // namespace
+
+StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len) {
+    StreamLayout L{};
+    auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t rows = (size_t)p->num_heads * q_len;
+    const size_t slots = (size_t)kMaxSlots + batch;
+    L.plan_off = 0;
+    L.ml_off = align((size_t)(batch + 2) * sizeof(int32_t));
+    L.o_off = L.ml_off + align(slots * rows * 2 * sizeof(double));
+    L.total = L.o_off + align(slots * rows * (size_t)p->head_dim * sizeof(double));
+    return L;
+}
+
+bool stream_eligible(const pkv_params* p, int32_t rows) {
+    return p->head_dim == 256 && rows <= 8 && rows >= 1;
+}
+
+int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
+                      const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                      const int32_t* pos, int32_t pos_scalar, int32_t q_len, int32_t batch,
+                      float* out, void* workspace, hipStream_t st) {
+    const int G = p->num_heads / p->num_kv_heads;
+    const int rows = G * q_len;
+    StreamLayout lay = stream_layout(p, batch, q_len);
+    StreamArgs a{};
+    char* ws = static_cast<char*>(workspace);
+    a.q = q;
+    a.k_pool = static_cast<const char*>(k_pool);
+    a.v_pool = static_cast<const char*>(v_pool);
+    a.tables = block_tables;
+    a.table_stride = table_stride;
+    a.pos = pos;
+    a.pos_scalar = pos_scalar;
+    a.q_len = q_len;
+    a.Hq = p->num_heads;
+    a.Hkv = p->num_kv_heads;
+    a.G = G;
+    a.bs_shift = __builtin_ctz((unsigned)p->block_size);
+    a.num_blocks = p->num_blocks;
+    a.window = p->window;
+    a.scale = p->scale;
+    a.batch = batch;
+    a.rows_seq = p->num_heads * q_len;
+    a.plan = reinterpret_cast<int32_t*>(ws + lay.plan_off);
+    a.part_ml = ws + lay.ml_off;
+    a.part_o = ws + lay.o_off;
+    a.out = out;
+    const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
+    if (p->head_dim != 256) return fail(PKV_ERR_UNSUPPORTED, "stream path: head_dim 256 only");
+    if (rows <= 1) return bf16 ? launch_r<256, uint16_t, 1>(a, st) : launch_r<256, float, 1>(a, st);
+    if (rows <= 2) return bf16 ? launch_r<256, uint16_t, 2>(a, st) : launch_r<256, float, 2>(a, st);
+    if (rows <= 4) return bf16 ? launch_r<256, uint16_t, 4>(a, st) : launch_r<256, float, 4>(a, st);
+    if (rows <= 8) return bf16 ? launch_r<256, uint16_t, 8>(a, st) : launch_r<256, float, 8>(a, st);
+    return fail(PKV_ERR_UNSUPPORTED, "stream path: at most 8 query rows per kv head");
+}
+
+}  // namespace pkv
