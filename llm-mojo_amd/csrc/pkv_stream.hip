@@ -705,9 +705,11 @@ int32_t launch_r(StreamArgs a, hipStream_t st) {
     const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R>);
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
-    // Launch-resident workgroups only: each covers ceil(total / slots) keys.
-    a.nwg = slots;
-    dim3 grid((a.Hkv + kMaxWaves - 1) / kMaxWaves, a.nwg);
+    // Resident workgroups only: the head groups share the slots, and each workgroup
+    // covers ceil(total / nwg) keys.
+    const int groups = (a.Hkv + kMaxWaves - 1) / kMaxWaves;
+    a.nwg = slots / groups > 0 ? slots / groups : 1;
+    dim3 grid(groups, a.nwg);
     hipLaunchKernelGGL((stream_attend_kernel<D, KV, R>), grid, dim3(threads), lds, st, a);
     hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch), dim3(kMergeNT),
                        0, st, a);

@@ -46,6 +46,7 @@ def _lib():
             "hipStreamDestroy": [vp],
             "hipStreamSynchronize": [vp],
             "hipEventCreate": [ctypes.POINTER(vp)],
+            "hipEventCreateWithFlags": [ctypes.POINTER(vp), ctypes.c_uint],
             "hipEventDestroy": [vp],
             "hipEventRecord": [vp, vp],
             "hipEventSynchronize": [vp],
@@ -159,10 +160,17 @@ class Stream:
             self.handle = None
 
 
+hipEventDisableSystemFence = 0x20000000  # record without a system-scope release
+
+
 class Event:
-    def __init__(self):
+    def __init__(self, flags: int = 0):
         e = ctypes.c_void_p()
-        check(_lib().hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        if flags:
+            check(_lib().hipEventCreateWithFlags(ctypes.byref(e), flags),
+                  "hipEventCreateWithFlags")
+        else:
+            check(_lib().hipEventCreate(ctypes.byref(e)), "hipEventCreate")
         self.handle = e.value
 
     def record(self, stream: Stream | None = None) -> None:
