@@ -607,7 +607,7 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (stream_eligible(p, rows) && workspace_bytes >= stream_layout(p, batch, q_len).total) {
         rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
-                           q_len, batch, out, workspace, st);
+                           q_len, batch, max_pos, out, workspace, st);
         if (rc != PKV_OK) return rc;
         return check_launch("pkv_attend");
     }

@@ -55,7 +55,7 @@ bool stream_eligible(const pkv_params* p, int32_t rows);
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                       const int32_t* pos, int32_t pos_scalar, int32_t q_len, int32_t batch,
-                      float* out, void* workspace, hipStream_t st);
+                      int32_t max_pos, float* out, void* workspace, hipStream_t st);
 
 __host__ __device__ inline int32_t window_start(int32_t pos, int32_t window) {
     if (window <= 0) return 0;

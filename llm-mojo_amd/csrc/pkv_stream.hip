@@ -315,6 +315,7 @@ struct StreamArgs {
     int32_t num_blocks;
     int32_t window;
     float scale;
+    int32_t max_pos;   // last query position the caller sized for
     int32_t batch;
     int32_t nwg;       // P: workgroups along the keys
     int32_t rows_seq;  // Hq * q_len
@@ -376,7 +377,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         int n = 0, lo = -1;
         if (p0 >= 0) {
             const int hi = p0 + a.q_len - 1;
-            if ((hi >> a.bs_shift) < a.table_stride) {
+            if (hi <= a.max_pos && (hi >> a.bs_shift) < a.table_stride) {
                 lo = window_start(p0, a.window);
                 n = hi - lo + 1;
             } else {
@@ -737,7 +738,7 @@ bool stream_eligible(const pkv_params* p, int32_t rows) {
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                       const int32_t* pos, int32_t pos_scalar, int32_t q_len, int32_t batch,
-                      float* out, void* workspace, hipStream_t st) {
+                      int32_t max_pos, float* out, void* workspace, hipStream_t st) {
     const int G = p->num_heads / p->num_kv_heads;
     const int rows = G * q_len;
     StreamLayout lay = stream_layout(p, batch, q_len);
@@ -758,6 +759,7 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.num_blocks = p->num_blocks;
     a.window = p->window;
     a.scale = p->scale;
+    a.max_pos = max_pos;
     a.batch = batch;
     a.rows_seq = p->num_heads * q_len;
     a.plan = reinterpret_cast<int32_t*>(ws + lay.plan_off);

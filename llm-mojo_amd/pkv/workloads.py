@@ -127,3 +127,198 @@ class DecodeSchedule:
         kv = int(n.sum()) * 2 * self.kv_stride * elt
         qo = 2 * self.B * self.HQ * self.D * 4
         return kv + qo + int(pages.sum()) * 4
+
+
+def _assign_tables(rng, blocks_per_seq, num_blocks: int, table_stride: int):
+    """Seeded random non-overlapping block tables: a permutation of the pool dealt out to
+    the sequences in order; the unassigned ids form the free list in ascending order (a
+    fresh BlockManager's LIFO stack after the assigned ids were taken)."""
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    B = len(blocks_per_seq)
+    tables = np.zeros((B, table_stride), np.int32)
+    lens = np.asarray(blocks_per_seq, np.int32)
+    off = 0
+    for s in range(B):
+        n = int(lens[s])
+        tables[s, :n] = perm[off:off + n]
+        off += n
+    return tables, lens, np.sort(perm[off:]).astype(np.int32)
+
+
+class SingleStep:
+    """Config 1: one sequence, 16 q / 8 kv heads, head_dim 256,
+    block 16, fp32; a 256-block pool; the sequence holds 512 tokens in a seeded random
+    32-block prefix of a permutation of the pool; the step appends the token at position
+    512 (the 33rd block, popped from the back of the free list) and attends 513 keys.
+    K, V, Q ~ N(0, 1); softmax scale 1/sqrt(256)."""
+
+    HQ, HKV, D, BS = 16, 8, 256, 16
+    NUM_BLOCKS = 256
+    CTX = 512
+    SCALE = 0.0625
+    B = 1
+    WINDOW = 0
+
+    def __init__(self, seed: int = 0):
+        rng = np.random.default_rng(seed)
+        self.kv_stride = self.HKV * self.D
+        self.num_blocks = self.NUM_BLOCKS
+        self.table_stride = 64
+        self.tables0, self.lens0, self.free0 = _assign_tables(
+            rng, [self.CTX // self.BS], self.num_blocks, self.table_stride)
+        self.pos = np.array([self.CTX], np.int32)
+        self.max_pos = self.CTX
+        base = int(rng.integers(1, 2**40))
+        self.seed_k, self.seed_v = base, base + 1
+        self.seed_q, self.seed_knew, self.seed_vnew = base + 2, base + 3, base + 4
+
+    def device_data(self, stream=None) -> dict:
+        rows = self.num_blocks * self.BS
+        return {"k": synth.normal((rows, self.kv_stride), self.seed_k, stream=stream),
+                "v": synth.normal((rows, self.kv_stride), self.seed_v, stream=stream),
+                "q": synth.normal((1, 1, self.HQ, self.D), self.seed_q, stream=stream),
+                "k_new": synth.normal((1, self.kv_stride), self.seed_knew, stream=stream),
+                "v_new": synth.normal((1, self.kv_stride), self.seed_vnew, stream=stream)}
+
+    def attend_bytes(self, elt: int = 4) -> int:
+        n = self.CTX + 1
+        return n * 2 * self.kv_stride * elt + 2 * self.HQ * self.D * 4 + (n // self.BS + 1) * 4
+
+
+class LongDecode:
+    """Config 3: batch 8, 16 q / 8 kv heads, head_dim 256,
+    block 16, bf16 K/V pages, fp32 Q. A pool of exactly 16384 blocks dealt out by a seeded
+    permutation, 2048 blocks (32768 slots) per sequence. Each sequence holds 32767 cached
+    tokens; the step appends the token at position 32767 (the last slot of its partially
+    filled 2048th block) and attends all 32768 keys. K, V ~ N(0, 1) rounded to bf16
+    (round-to-nearest-even), Q ~ N(0, 1) fp32, scale 1/sqrt(256)."""
+
+    HQ, HKV, D, BS = 16, 8, 256, 16
+    B = 8
+    CTX = 32768  # keys attended, including the appended token
+    NUM_BLOCKS = 16384
+    SCALE = 0.0625
+    WINDOW = 0
+
+    def __init__(self, seed: int = 0, batch: int | None = None, ctx: int | None = None):
+        rng = np.random.default_rng(seed)
+        if batch is not None:
+            self.B = batch
+        if ctx is not None:
+            self.CTX = ctx
+        self.kv_stride = self.HKV * self.D
+        per_seq = (self.CTX + self.BS - 1) // self.BS
+        self.num_blocks = self.NUM_BLOCKS if (batch, ctx) == (None, None) else self.B * per_seq
+        self.table_stride = per_seq
+        self.tables0, self.lens0, self.free0 = _assign_tables(
+            rng, [per_seq] * self.B, self.num_blocks, self.table_stride)
+        self.pos = np.full(self.B, self.CTX - 1, np.int32)
+        self.max_pos = self.CTX - 1
+        base = int(rng.integers(1, 2**40))
+        self.seed_k, self.seed_v = base, base + 1
+        self.seed_q, self.seed_knew, self.seed_vnew = base + 2, base + 3, base + 4
+
+    def device_data(self, stream=None) -> dict:
+        rows = self.num_blocks * self.BS
+        bf = np.uint16
+        return {"k": synth.normal((rows, self.kv_stride), self.seed_k, bf, stream=stream),
+                "v": synth.normal((rows, self.kv_stride), self.seed_v, bf, stream=stream),
+                "q": synth.normal((self.B, 1, self.HQ, self.D), self.seed_q, stream=stream),
+                "k_new": synth.normal((self.B, self.kv_stride), self.seed_knew, bf,
+                                      stream=stream),
+                "v_new": synth.normal((self.B, self.kv_stride), self.seed_vnew, bf,
+                                      stream=stream)}
+
+    def attend_bytes(self, elt: int = 2) -> int:
+        n = self.CTX
+        return (self.B * n * 2 * self.kv_stride * elt + 2 * self.B * self.HQ * self.D * 4
+                + self.B * ((n - 1) // self.BS + 1) * 4)
+
+
+class VerifySchedule:
+    """Config 5: MTP speculative verify and rollback with shared
+    KV. 16 sequences with contexts seeded uniform on [512, 4096]; two global-attention
+    layers (16 q / 8 kv heads, head_dim 256, fp32, block 16) standing in for the target
+    layers whose pools the MTP assistant reads. Per iteration, with L = each sequence's
+    committed length:
+      1. MTP drafting: DRAFT read-only attention calls on both pools at kv_pos = L - 1,
+         through the target's own tables (mtp_generate_step, …batched.mojo:2955-2990);
+      2. verify: append DRAFT draft tokens' K/V at L .. L + DRAFT - 1 on both layers, then
+         attend DRAFT query tokens against the paged prefix plus the causal-masked draft;
+      3. acceptance: a seeded count a ~ U{0..DRAFT}; rollback to L + a (tail blocks back to
+         the LIFO free list in ascending logical order).
+    32 iterations. The pool holds the blocks the contexts can grow to, plus 10 %."""
+
+    HQ, HKV, D, BS = 16, 8, 256, 16
+    B = 16
+    DRAFT = 4
+    ITERS = 32
+    SCALE = 0.0625
+    WINDOW = 0
+    LAYERS = 2
+
+    def __init__(self, seed: int = 0, batch: int | None = None, iters: int | None = None,
+                 ctx_lo: int = 512, ctx_hi: int = 4096):
+        rng = np.random.default_rng(seed)
+        if batch is not None:
+            self.B = batch
+        if iters is not None:
+            self.ITERS = iters
+        B, bs = self.B, self.BS
+        self.kv_stride = self.HKV * self.D
+        self.ctx0 = rng.integers(ctx_lo, ctx_hi + 1, B).astype(np.int64)
+        grow = self.DRAFT * (self.ITERS + 1)
+        need = int(np.sum((self.ctx0 + grow + bs - 1) // bs))
+        self.num_blocks = int(np.ceil(need * 1.1))
+        self.table_stride = int((ctx_hi + grow + bs - 1) // bs) + 2
+        self.tables0, self.lens0, self.free0 = _assign_tables(
+            rng, (self.ctx0 + bs - 1) // bs, self.num_blocks, self.table_stride)
+        self.accept = rng.integers(0, self.DRAFT + 1, (self.ITERS, B)).astype(np.int32)
+        self.length = np.zeros((self.ITERS + 1, B), np.int64)  # committed length per iter
+        self.length[0] = self.ctx0
+        for it in range(self.ITERS):
+            self.length[it + 1] = self.length[it] + self.accept[it]
+        self.max_pos = int(self.length.max()) + self.DRAFT - 1
+        base = int(rng.integers(1, 2**40))
+        self.seed_pool = [[base + 10 * layer + kv for kv in range(2)] for layer in range(2)]
+        self.seed_q, self.seed_mtp_q = base + 100, base + 101
+        self.seed_knew, self.seed_vnew = base + 102, base + 103
+
+    def device_data(self, stream=None) -> dict:
+        rows = self.num_blocks * self.BS
+        n = self.ITERS * self.LAYERS
+        return {"pools": [[synth.normal((rows, self.kv_stride), self.seed_pool[l][kv],
+                                        stream=stream) for kv in range(2)]
+                          for l in range(self.LAYERS)],
+                "q": synth.normal((n, self.B, self.DRAFT, self.HQ, self.D), self.seed_q,
+                                  stream=stream),
+                "mtp_q": synth.normal((n, self.DRAFT, self.B, 1, self.HQ, self.D),
+                                      self.seed_mtp_q, stream=stream),
+                "k_new": synth.normal((n, self.B * self.DRAFT, self.kv_stride), self.seed_knew,
+                                      stream=stream),
+                "v_new": synth.normal((n, self.B * self.DRAFT, self.kv_stride), self.seed_vnew,
+                                      stream=stream)}
+
+    def pos(self, it: int) -> np.ndarray:
+        return self.length[it].astype(np.int32)
+
+    def new_len(self, it: int) -> np.ndarray:
+        return self.length[it + 1].astype(np.int32)
+
+    def tok_off(self) -> np.ndarray:
+        return (np.arange(self.B + 1) * self.DRAFT).astype(np.int32)
+
+    def verify_bytes(self, it: int, elt: int = 4) -> int:
+        """Algorithmic bytes of one verify attention launch (one layer): each K/V row
+        slice of prefix + draft once, Q in, O out, table entries."""
+        n = self.length[it] + self.DRAFT
+        kv = int(n.sum()) * 2 * self.kv_stride * elt
+        qo = 2 * self.B * self.DRAFT * self.HQ * self.D * 4
+        return kv + qo + int(((n - 1) // self.BS + 1).sum()) * 4
+
+    def verify_flops(self, it: int) -> int:
+        """QK^T and PV multiply-adds x 2 of one verify launch, counting the causal mask:
+        query j attends L + j + 1 keys."""
+        keys = sum(int(self.length[it, s]) * self.DRAFT
+                   + self.DRAFT * (self.DRAFT + 1) // 2 for s in range(self.B))
+        return 4 * self.D * self.HQ * keys

@@ -236,3 +236,10 @@ def test_inactive_sequence_gives_zeros_and_bad_table_gives_nan(gpu):
              dpos2.ptr, 1, B, 127, out.ptr, ws.ptr, ws.nbytes)
     o = out.numpy()
     assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[0])) and np.all(np.isfinite(o[2]))
+    # beyond max_pos but inside the table stride -> NaN as well (the grid is sized by it)
+    stride3 = 16
+    dtab3 = hip.DeviceArray.from_numpy(rng.integers(0, nb, (B, stride3)).astype(np.int32))
+    lib.call("pkv_attend", None, ctypes.byref(p), q.ptr, k.ptr, k.ptr, dtab3.ptr, stride3,
+             dpos2.ptr, 1, B, 127, out.ptr, ws.ptr, ws.nbytes)
+    o = out.numpy()
+    assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[0])) and np.all(np.isfinite(o[2]))
