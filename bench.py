@@ -32,6 +32,7 @@ for _p in (REPO, os.path.join(REPO, "llm-mojo_amd")):
 
 METRIC = "paged decode attn tokens/s + achieved HBM GB/s (% peak) at B=32, 1 GPU"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, AMD published
+PEAK_FP64_VALU_TFLOPS = 78.6  # MI355X vector fp64, AMD published
 
 
 def _traffic_from_profiles():
@@ -218,6 +219,327 @@ def run_cpu(sched, data, seconds, nthreads, log):
     return dict(steps=done, seconds=elapsed, outs=outs)
 
 
+class _Setup:
+    """A PagedKVCache for workload `w` in its initial block-manager state, the pools
+    copied from the workload's device data, and a stream-ordered restore of the state."""
+
+    def __init__(self, w, layers, kv_dtype, q_len, stream):
+        from pkv import LayerSpec, PagedKVCache, hip
+
+        self.hip = hip
+        self.stream = stream
+        specs = [LayerSpec(w.HQ, w.HKV, w.D, window=w.WINDOW, kv_dtype=kv_dtype)
+                 for _ in range(layers)]
+        self.cache = PagedKVCache(specs, block_size=w.BS, num_blocks=w.num_blocks,
+                                  max_seqs=w.B, max_blocks_per_seq=w.table_stride,
+                                  max_q_len=q_len, max_pos=w.max_pos, scale=w.SCALE,
+                                  stream=stream)
+        D = hip.DeviceArray.from_numpy
+        tables = np.zeros((w.B, w.table_stride), np.int32)
+        tables[:, :w.tables0.shape[1]] = w.tables0
+        fl = np.zeros(w.num_blocks, np.int32)
+        fl[:w.free0.size] = w.free0
+        c = self.cache
+        self.pairs = ((c.tables, D(tables)), (c.table_lens, D(np.asarray(w.lens0, np.int32))),
+                      (c.free_list, D(fl)), (c.free_count, D(np.array([w.free0.size], np.int32))))
+        self.restore()
+        hip.synchronize()
+
+    def restore(self):
+        h = self.hip
+        for dst, src in self.pairs:
+            h.check(h._lib().hipMemcpyAsync(dst.ptr, src.ptr, dst.nbytes, h.hipMemcpyDeviceToDevice,
+                                            self.stream.handle), "hipMemcpyAsync")
+
+
+def _timed(hip, stream, steps, body):
+    """Runs body(i) for i < steps between two events on `stream`; returns milliseconds."""
+    t0, t1 = hip.Event(), hip.Event()
+    hip.synchronize()
+    t0.record(stream)
+    for i in range(steps):
+        body(i)
+    t1.record(stream)
+    t1.synchronize()
+    return t0.elapsed_ms(t1)
+
+
+def _event_pairs(hip, n):
+    f = hip.hipEventDisableSystemFence
+    return [(hip.Event(f), hip.Event(f)) for _ in range(n)]
+
+
+def _line(metric, value, unit, steps, warmup, ms_per_step, dtype, workload, roofline, extra):
+    r = {"metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": steps,
+         "warmup": warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+         "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic: seeded "
+         "N(0,1) K/V/Q, seeded random non-overlapping block tables",
+         "config": {"workload": workload}, "roofline": roofline}
+    r.update(extra)
+    return r
+
+
+def _roofline(nbytes, dur_ms, kernel, flops=None):
+    achieved = nbytes / (dur_ms / 1e3) / 1e9
+    r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+         "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernel,
+         "avg_launch_us": round(dur_ms * 1e3, 2), "algorithmic_bytes_per_launch": int(nbytes)}
+    if flops is not None:  # the fp32-pool arithmetic runs in double on the vector ALUs
+        tf = flops / (dur_ms / 1e3) / 1e12
+        r["fp64_vector_tflops"] = round(tf, 2)
+        r["fp64_vector_frac"] = round(tf / PEAK_FP64_VALU_TFLOPS, 4)
+    return r
+
+
+def bench_config1(args, log):
+    """Config 1: one sequence, append at 512 (new block) + attend 513 keys, fp32. A step
+    ends with a rollback to 512 tokens, which returns the block to the back of the free
+    list, so every step starts from the same state."""
+    from pkv import F32, hip
+    from pkv.workloads import SingleStep
+
+    w = SingleStep(seed=args.seed)
+    d = w.device_data()
+    stream = hip.Stream()
+    S = _Setup(w, 1, F32, 1, stream)
+    c = S.cache
+    c.k_pools[0].copy_from(d["k"])
+    c.v_pools[0].copy_from(d["v"])
+    D = hip.DeviceArray.from_numpy
+    dpos, doff, dnl = D(w.pos), D(np.array([0, 1], np.int32)), D(w.pos)
+    out = hip.DeviceArray((1, 1, w.HQ, w.D), np.float32)
+    ev = _event_pairs(hip, args.steps)
+
+    def step(i, events=None):
+        c.append(0, dpos.ptr, doff.ptr, d["k_new"], d["v_new"], 1, 1, batch=1)
+        if events:
+            events[i][0].record(stream)
+        c.attend(0, d["q"], dpos.ptr, 1, out, batch=1)
+        if events:
+            events[i][1].record(stream)
+        c.rollback(dnl.ptr, batch=1)
+
+    for i in range(args.warmup):
+        step(i)
+    ms = _timed(hip, stream, args.steps, step)
+    _timed(hip, stream, args.steps, lambda i: step(i, ev))
+    dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    got = out.numpy()
+    res = _line("config 1 single-sequence decode step (append + attend 513 keys) latency",
+                1e3 / ms * args.steps, "steps/s", args.steps, args.warmup, ms / args.steps,
+                "f32", "BASELINE config 1: 1 sequence, ctx 512 -> append at 512 into a new "
+                "block, attend 513 keys, 16q/8kv/256, block 16, 256-block pool, fp32",
+                _roofline(w.attend_bytes(), dur, "stream_attend_kernel<256, float, 2>"),
+                {"attend_us": round(dur * 1e3, 2)})
+    if args.cpu_seconds > 0:
+        from oracle import oracle as O
+
+        st = O.CacheState(1, w.kv_stride, w.BS, w.num_blocks, 1, w.table_stride,
+                          alloc_pools=False)
+        st.k_pools[0] = d["k"].numpy().reshape(-1).copy()
+        st.v_pools[0] = d["v"].numpy().reshape(-1).copy()
+        kn, vn, q = d["k_new"].numpy(), d["v_new"].numpy(), d["q"].numpy()
+        n, el, ref = 0, 0.0, None
+        while el < args.cpu_seconds and n < 1000:
+            st.tables[:, :w.tables0.shape[1]] = w.tables0
+            st.table_lens[:] = w.lens0
+            st.bm.free_list[:w.free0.size] = w.free0
+            st.bm.count[0] = w.free0.size
+            t = time.perf_counter()
+            st.append(0, w.pos, [0, 1], kn, vn, 1)
+            ref = O.attend(q, st.k_pools[0], st.v_pools[0], st.tables, st.table_lens, w.pos, 1,
+                           w.HQ, w.HKV, w.D, w.BS, 0, scale=w.SCALE, nthreads=args.cpu_threads)
+            el += time.perf_counter() - t
+            n += 1
+        res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "steps/s",
+                               "cores": args.cpu_threads, "kind": "port",
+                               "sample": f"{n} steps (append + paged_attention_layer, "
+                                         f"{args.cpu_threads} head-pair tasks)"}
+        res["parity_sample_max_rel_err"] = float(f"{O.max_rel_err(got, ref):.3g}")
+    return res
+
+
+def bench_config3(args, log):
+    """Config 3: 8 sequences x 32768 keys over bf16 pages; a step appends the token at
+    position 32767 (no allocation: the slot is in the last table block) and attends."""
+    from pkv import BF16, hip
+    from pkv.workloads import LongDecode
+
+    w = LongDecode(seed=args.seed)
+    d = w.device_data()
+    stream = hip.Stream()
+    S = _Setup(w, 1, BF16, 1, stream)
+    c = S.cache
+    c.k_pools[0].copy_from(d["k"])
+    c.v_pools[0].copy_from(d["v"])
+    D = hip.DeviceArray.from_numpy
+    dpos, doff = D(w.pos), D(np.arange(w.B + 1, dtype=np.int32))
+    out = hip.DeviceArray((w.B, 1, w.HQ, w.D), np.float32)
+    ev = _event_pairs(hip, args.steps)
+
+    def step(i, events=None):
+        c.append(0, dpos.ptr, doff.ptr, d["k_new"], d["v_new"], 1, w.B)
+        if events:
+            events[i][0].record(stream)
+        c.attend(0, d["q"], dpos.ptr, 1, out)
+        if events:
+            events[i][1].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    ms = _timed(hip, stream, args.steps, step)
+    _timed(hip, stream, args.steps, lambda i: step(i, ev))
+    dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    got = out.numpy()
+    res = _line("config 3 long-context paged decode tokens/s (B=8, 32K keys, bf16 pages)",
+                w.B * args.steps / (ms / 1e3), "tokens/s", args.steps, args.warmup,
+                ms / args.steps, "bf16",
+                "BASELINE config 3: 8 sequences x 32768 keys, 16q/8kv/256, block 16, "
+                "16384-block pool, bf16 K/V, fp32 Q, append + attend",
+                _roofline(w.attend_bytes(), dur,
+                          "stream_attend_kernel<256, bf16, 2> + stream_merge_kernel<256, float>"),
+                {"attend_us": round(dur * 1e3, 2)})
+    if args.cpu_seconds > 0:
+        from oracle import oracle as O
+
+        k, v, q = d["k"].numpy().reshape(-1), d["v"].numpy().reshape(-1), d["q"].numpy()
+        tables = np.ascontiguousarray(w.tables0)
+        n, el, ref = 0, 0.0, None
+        while el < args.cpu_seconds and n < 100:
+            t = time.perf_counter()
+            ref = O.attend(q, k, v, tables, w.lens0, w.pos, 1, w.HQ, w.HKV, w.D, w.BS, 0,
+                           scale=w.SCALE, nthreads=args.cpu_threads)
+            el += time.perf_counter() - t
+            n += 1
+        res["cpu_baseline"] = {"value": round(w.B * n / el, 3), "unit": "tokens/s",
+                               "cores": args.cpu_threads, "kind": "port",
+                               "sample": f"{n} attention steps (8 sequences in turn, "
+                                         f"{args.cpu_threads} head-pair tasks per call; the "
+                                         f"pre-append pools, so the 32768th key differs)"}
+        log("config 3 cpu sample done")
+    return res
+
+
+def bench_config5(args, log):
+    """Config 5: per iteration, MTP reads (4 draft steps x 2 layers, read-only at pos-1),
+    4-token verify append + causal attention on both layers, rollback to the accepted
+    length; the 32-iteration schedule repeats with the block-manager state restored."""
+    from pkv import F32, hip
+    from pkv.workloads import VerifySchedule
+
+    w = VerifySchedule(seed=args.seed)
+    d = w.device_data()
+    stream = hip.Stream()
+    L, B, DR = w.LAYERS, w.B, w.DRAFT
+    S = _Setup(w, L, F32, DR, stream)
+    c = S.cache
+    for layer in range(L):
+        c.k_pools[layer].copy_from(d["pools"][layer][0])
+        c.v_pools[layer].copy_from(d["pools"][layer][1])
+    pristine = [(c.k_pools[l], d["pools"][l][0]) for l in range(L)] + \
+               [(c.v_pools[l], d["pools"][l][1]) for l in range(L)]
+    D = hip.DeviceArray.from_numpy
+    dpos = [D(w.pos(it)) for it in range(w.ITERS)]
+    dpm1 = [D(w.pos(it) - 1) for it in range(w.ITERS)]
+    dnl = [D(w.new_len(it)) for it in range(w.ITERS)]
+    doff = D(w.tok_off())
+    out_v = hip.DeviceArray((w.ITERS, L, B, DR, w.HQ, w.D), np.float32)
+    out_m = hip.DeviceArray((B, 1, w.HQ, w.D), np.float32)
+    qstep, mstep = B * DR * w.HQ * w.D * 4, B * w.HQ * w.D * 4
+    kvstep = B * DR * w.kv_stride * 4
+    ev = [_event_pairs(hip, L) for _ in range(args.steps)]
+
+    def iteration(i, events=None):
+        it = i % w.ITERS
+        if i > 0 and it == 0:
+            S.restore()
+        for dstep in range(DR):
+            for layer in range(L):
+                c.attend(layer, d["mtp_q"].ptr + ((it * L + layer) * DR + dstep) * mstep,
+                         dpm1[it].ptr, 1, out_m)
+        for layer in range(L):
+            n = it * L + layer
+            c.append(layer, dpos[it].ptr, doff.ptr, d["k_new"].ptr + n * kvstep,
+                     d["v_new"].ptr + n * kvstep, DR, B * DR)
+        for layer in range(L):
+            n = it * L + layer
+            if events:
+                events[i][layer][0].record(stream)
+            c.attend(layer, d["q"].ptr + n * qstep, dpos[it].ptr, DR, out_v.ptr + n * qstep)
+            if events:
+                events[i][layer][1].record(stream)
+        c.rollback(dnl[it].ptr)
+
+    def reset():
+        for pool, src in pristine:
+            pool.copy_from(src)
+        S.restore()
+        hip.synchronize()
+
+    for i in range(args.warmup):
+        iteration(i)
+    reset()
+    ms = _timed(hip, stream, args.steps, iteration)
+    got = out_v.numpy()
+    reset()
+    _timed(hip, stream, args.steps, lambda i: iteration(i, ev))
+    dur = np.array([[a.elapsed_ms(b) for a, b in e] for e in ev])
+    its = [i % w.ITERS for i in range(args.steps)]
+    nbytes = float(np.mean([w.verify_bytes(it) for it in its]))
+    flops = float(np.mean([w.verify_flops(it) for it in its]))
+    res = _line("config 5 MTP verify query tokens/s (16 seq, draft 4, 2 layers, shared KV, "
+                "rollback)", B * DR * args.steps / (ms / 1e3), "tokens/s", args.steps,
+                args.warmup, ms / args.steps, "f32",
+                "BASELINE config 5: 16 sequences, ctx U[512,4096], 2 global layers 16q/8kv/256 "
+                "fp32, block 16; per iteration 4 MTP reads at pos-1 per layer, 4-token verify "
+                "append + causal attention, accept U{0..4}, rollback; 32-iteration schedule",
+                _roofline(nbytes, float(dur.mean()), "stream_attend_kernel<256, float, 8> + "
+                          "stream_merge_kernel<256, double>", flops=flops),
+                {"verify_attend_us": round(float(dur.mean()) * 1e3, 2)})
+    if args.cpu_seconds > 0:
+        from oracle import oracle as O
+
+        st = O.CacheState(L, w.kv_stride, w.BS, w.num_blocks, B, w.table_stride,
+                          alloc_pools=False)
+        for layer in range(L):
+            st.k_pools[layer] = d["pools"][layer][0].numpy().reshape(-1).copy()
+            st.v_pools[layer] = d["pools"][layer][1].numpy().reshape(-1).copy()
+        st.tables[:, :w.tables0.shape[1]] = w.tables0
+        st.table_lens[:] = w.lens0
+        st.bm.free_list[:w.free0.size] = w.free0
+        st.bm.count[0] = w.free0.size
+        qa, ma = d["q"].numpy(), d["mtp_q"].numpy()
+        kn, vn = d["k_new"].numpy(), d["v_new"].numpy()
+        n, el, errs = 0, 0.0, []
+        for it in range(w.ITERS):
+            t = time.perf_counter()
+            pos = w.pos(it)
+            for dstep in range(DR):
+                for layer in range(L):
+                    O.attend(ma[it * L + layer, dstep], st.k_pools[layer], st.v_pools[layer],
+                             st.tables, st.table_lens, pos - 1, 1, w.HQ, w.HKV, w.D, w.BS, 0,
+                             scale=w.SCALE, nthreads=args.cpu_threads)
+            for layer in range(L):
+                st.append(layer, pos, w.tok_off(), kn[it * L + layer], vn[it * L + layer], DR)
+            for layer in range(L):
+                ref = O.attend(qa[it * L + layer], st.k_pools[layer], st.v_pools[layer],
+                               st.tables, st.table_lens, pos, DR, w.HQ, w.HKV, w.D, w.BS, 0,
+                               scale=w.SCALE, nthreads=args.cpu_threads)
+                errs.append(O.max_rel_err(got[it, layer], ref))
+            st.rollback(w.new_len(it))
+            el += time.perf_counter() - t
+            n += 1
+            if el >= args.cpu_seconds:
+                break
+        res["cpu_baseline"] = {"value": round(B * DR * n / el, 2), "unit": "tokens/s",
+                               "cores": args.cpu_threads, "kind": "port",
+                               "sample": f"first {n} iterations of the schedule (MTP reads, "
+                                         f"appends, verify as {DR} sequential "
+                                         f"paged_attention_layer calls per sequence, rollback)"}
+        res["parity_sample_max_rel_err"] = float(f"{max(errs):.3g}")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -229,6 +551,8 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=8,
                     help="threads for the reference CPU path (8 = its Hq/2 head-pair tasks)")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 5],
+                    help="BASELINE.json configuration (2, the default, is the headline)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -247,6 +571,10 @@ def main() -> int:
     if hip.device_count() < 1:
         print("bench.py needs a GPU: no HIP device visible", file=sys.stderr)
         return 1
+    legs = {1: bench_config1, 3: bench_config3, 5: bench_config5}
+    if args.config in legs:
+        print(json.dumps(legs[args.config](args, log)), flush=True)
+        return 0
     t = time.perf_counter()
     sched = DecodeSchedule(seed=args.seed)
     data = sched.device_data()

@@ -51,7 +51,7 @@ namespace {
 #define PKV_STREAM_WAVES 8
 #endif
 #ifndef PKV_STREAM_PER_MIN
-#define PKV_STREAM_PER_MIN 64
+#define PKV_STREAM_PER_MIN 16
 #endif
 
 constexpr int kSW = 64;                          // wavefront
