@@ -124,6 +124,24 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
                    const int32_t* pos, int32_t batch, int32_t max_pos, float* out,
                    void* workspace, size_t workspace_bytes);
 
+/* K3 -- chunked-prefill attention over bf16 pages with bf16 MFMA (fp32 accumulation).
+ * Replaces the engine's per-token prefill loop (append one token, then one
+ * paged_attention_layer call for it: model_speculative_moe_batched.mojo:2600-2637 for
+ * the chunked path, :2767-2833 for the CPU path) once the chunk's K/V rows have been
+ * appended with pkv_append. Queries are ragged: sequence s owns query rows
+ * q_off[s] .. q_off[s+1]-1 of q (bf16 [rows][num_heads][head_dim]) at positions
+ * pos[s], pos[s]+1, ...; query i attends keys [window_start(pos[s]+i), pos[s]+i] of its
+ * own table (prefix plus the causal part of the chunk). out: fp32 [rows][num_heads]
+ * [head_dim]. kv_dtype must be PKV_DTYPE_BF16, head_dim 256, num_heads / num_kv_heads in
+ * {1, 2, 4}. max_q bounds q_off[s+1]-q_off[s] (it sizes the grid) and max_pos bounds
+ * pos[s] + its query count - 1; a sequence violating either, or whose table holds an
+ * entry outside [0, num_blocks), gets NaN outputs; pos[s] < 0 gives zeros. One launch,
+ * no workspace. q_off: int32 [batch + 1] (device). */
+int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void* k_pool,
+                    const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                    const int32_t* pos, const int32_t* q_off, int32_t max_q, int32_t batch,
+                    int32_t max_pos, float* out);
+
 /* K5 -- rollback / retire. No reference counterpart for draft rollback (the engine
  * leaves rejected rows in place and only advances pos, :3295-3368); retire is
  * model_speculative_moe_batched.mojo:3626-3628 and chat reset :2424-2439.

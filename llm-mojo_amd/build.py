@@ -32,7 +32,8 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{os.path.join(REPO, 'include')}",
 ]
-SOURCES = ["pkv_common.cpp", "pkv_state.hip", "pkv_attend.hip", "pkv_stream.hip"]
+SOURCES = ["pkv_common.cpp", "pkv_state.hip", "pkv_attend.hip", "pkv_stream.hip",
+           "pkv_prefill.hip"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -1,0 +1,355 @@
+// K3 -- chunked-prefill attention over paged bf16 K/V with bf16 MFMA (gfx950).
+//
+// Replaces the engine's per-token prefill loop, which appends one token and calls
+// paged_attention_layer for it before the next (model_speculative_moe_batched.mojo
+// :2600-2637 chunked, :2767-2833 CPU), i.e. causal attention of every chunk query over
+// the cached prefix plus the chunk itself. The chunk's K/V rows are appended first
+// (pkv_append); this kernel then attends all chunk queries in one launch.
+//
+// Workgroup = (tile of 128/G queries, kv head g, sequence), four waves; wave w owns 32
+// rows: query block w / G (32 consecutive queries) of q head g*G + w % G. All four waves
+// share the K/V tiles of 64 keys staged in LDS, so every K/V byte is read once per tile
+// of 128 rows. Per key tile:
+//   S^T = K Q^T  (v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q from registers):
+//     the output puts row j of the wave in lanes j and j + 32, each holding 16 of the 32
+//     keys of a sub-tile, so the online softmax needs one cross-lane step (permlane32);
+//   P = exp2(S * scale * log2 e - m), split P = P_hi + P_lo (both bf16; the residual of a
+//     single bf16 rounding would break the 2e-2 output bound near zero);
+//   O^T += V^T P^T (A = V^T from LDS, B = P_hi then P_lo straight from the S^T registers):
+//     the keys of a 16-key step are taken in the order the S^T registers hold them, and
+//     V^T is stored in LDS with the same permutation (bits 2 and 3 of the key index
+//     swapped inside each 16-key group), so each operand is one 16-byte LDS read.
+// Accumulation is fp32 throughout; the output is O / (l + 1e-10) (the reference's
+// softmax denominator, attention.mojo:151-162).
+//
+// MFMA lane layouts (v_mfma_f32_32x32x16_bf16, checked on the device):
+//   A[i][k]: lane i + 32*(k/8), element k%8;   B[k][j]: lane j + 32*(k/8), element k%8;
+//   C[i][j]: lane j + 32*((i/4)%2), register 4*(i/8) + i%4.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "pkv_internal.h"
+
+namespace pkv {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kD = 256;             // head_dim of this kernel
+constexpr int kKT = 64;             // keys per tile
+constexpr int kKStr = kD + 8;       // K tile row stride (bf16): 528 B, rotates the banks
+constexpr int kVStr = kKT + 8;      // V^T row stride (bf16): 144 B
+constexpr int kNT = 256;            // four waves
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct PrefillArgs {
+    const uint16_t* q;  // bf16 [rows][Hq][D]
+    const uint16_t* k_pool;
+    const uint16_t* v_pool;
+    const int32_t* tables;
+    int32_t table_stride;
+    const int32_t* pos;    // [batch]: position of each sequence's first query
+    const int32_t* q_off;  // [batch + 1]: query rows of sequence s
+    int32_t Hq;
+    int32_t Hkv;
+    int32_t bs_shift;
+    int32_t num_blocks;
+    int32_t window;
+    float scale_log2;  // softmax scale * log2(e)
+    int32_t max_q;
+    int32_t max_pos;
+    int32_t qtiles;
+    float* out;  // fp32 [rows][Hq][D]
+};
+
+// Position of key k (0..63) of a tile inside its V^T row: bits 2 and 3 swapped.
+__device__ inline int vperm(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+
+__device__ inline float swap32_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float swap32_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int G>
+__global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
+    constexpr int QB = 128 / G;  // queries per workgroup
+    __shared__ __attribute__((aligned(16))) uint16_t sK[kKT * kKStr];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[kD * kVStr];
+    __shared__ int s_row[kKT];
+    __shared__ int s_bad;
+
+    const int s = blockIdx.z;
+    const int g = blockIdx.y;
+    const int tile = a.qtiles - 1 - (int)blockIdx.x;  // long (late) tiles first
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int half = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row0 = a.q_off[s];
+    const int n_q = a.q_off[s + 1] - row0;
+    const int q0 = tile * QB;
+    const int head = g * G + wave % G;
+    const int qi = q0 + (wave / G) * 32 + (lane & 31);  // this lane's query
+    const bool live = qi < n_q;
+    const int pos0 = a.pos[s];
+    auto out_at = [&](int query, int h) -> float* {
+        return a.out + ((size_t)(row0 + query) * a.Hq + h) * kD;
+    };
+
+    // Contract violations: the rows this workgroup owns get NaN (or zeros when the
+    // sequence is inactive); queries beyond the grid (n_q > max_q) get NaN from tile 0.
+    const int hi_all = pos0 + n_q - 1;
+    const bool inactive = pos0 < 0;
+    const bool bad_seq = !inactive && n_q > 0 &&
+                         (hi_all > a.max_pos || (hi_all >> a.bs_shift) >= a.table_stride ||
+                          n_q > a.max_q);
+    if (tile == 0 && n_q > a.qtiles * QB && !inactive) {
+        for (int i = tid; i < (n_q - a.qtiles * QB) * G * kD; i += kNT) {
+            const int r = i / (G * kD), h = (i / kD) % G, d = i % kD;
+            out_at(a.qtiles * QB + r, g * G + h)[d] = __builtin_nanf("");
+        }
+    }
+    if (q0 >= n_q) return;
+    if (inactive || bad_seq) {
+        const float fill = inactive ? 0.f : __builtin_nanf("");
+        for (int i = tid; i < QB * G * kD; i += kNT) {
+            const int r = i / (G * kD), h = (i / kD) % G, d = i % kD;
+            if (q0 + r < n_q) out_at(q0 + r, g * G + h)[d] = fill;
+        }
+        return;
+    }
+
+    const int q_last = min(n_q, q0 + QB) - 1;
+    const int k_lo = window_start(pos0 + q0, a.window);
+    const int k_hi = pos0 + q_last;
+    const int qpos = pos0 + qi;
+    const int ws_row = window_start(qpos, a.window);
+    // Tiles fully inside every row's [window start, position] need no mask.
+    const int min_qpos = pos0 + q0;
+    const int max_ws = window_start(k_hi, a.window);
+
+    // Q as the B operand of S^T: lane holds Q[row][16c + 8*half .. +7] for c = 0..15.
+    bf16x8 qreg[16];
+    {
+        const uint16_t* qp = a.q + ((size_t)(row0 + (live ? qi : 0)) * a.Hq + head) * kD + 8 * half;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const uint4 v = live ? *reinterpret_cast<const uint4*>(qp + 16 * c) : make_uint4(0, 0, 0, 0);
+            qreg[c] = __builtin_bit_cast(bf16x8, v);
+        }
+    }
+
+    f32x16 o[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
+    float m = -INFINITY;  // running max (log2 domain) of this lane's row
+    float l = 0.f;        // this lane's share of the running sum (keys of its half)
+    if (tid == 0) s_bad = 0;
+
+    const int32_t* trow = a.tables + (size_t)s * a.table_stride;
+    const size_t head_off = (size_t)g * kD;
+    const size_t row_elems = (size_t)a.Hkv * kD;
+    const int bs_mask = (1 << a.bs_shift) - 1;
+
+    for (int kb = k_lo & ~(kKT - 1); kb <= k_hi; kb += kKT) {
+        __syncthreads();  // the previous tile's LDS reads are done
+        if (tid < kKT) {
+            const int kpos = min(max(kb + tid, k_lo), k_hi);
+            int b = trow[kpos >> a.bs_shift];
+            if (b < 0 || b >= a.num_blocks) {
+                s_bad = 1;
+                b = 0;
+            }
+            s_row[tid] = (b << a.bs_shift) | (kpos & bs_mask);
+        }
+        __syncthreads();
+        // K tile: 64 keys x 32 chunks of 8 elements, row-major with a padded stride.
+#pragma unroll
+        for (int i = 0; i < (kKT * kD / 8) / kNT; ++i) {
+            const int u = tid + i * kNT;
+            const int key = u >> 5, dc = u & 31;
+            const uint4 v = *reinterpret_cast<const uint4*>(
+                a.k_pool + (size_t)s_row[key] * row_elems + head_off + 8 * dc);
+            *reinterpret_cast<uint4*>(&sK[key * kKStr + 8 * dc]) = v;
+        }
+        // V tile transposed: unit = 4 consecutive keys x 8 dims; each dim's 4 keys go to
+        // one 8-byte run at the permuted key position.
+#pragma unroll
+        for (int i = 0; i < (kKT / 4) * (kD / 8) / kNT; ++i) {
+            const int u = tid + i * kNT;
+            const int kg = u >> 5, dc = u & 31;
+            uint4 r[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                r[j] = *reinterpret_cast<const uint4*>(
+                    a.v_pool + (size_t)s_row[4 * kg + j] * row_elems + head_off + 8 * dc);
+            const int kp = vperm(4 * kg);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int w = e >> 1, sh = (e & 1) * 16;
+                auto el = [&](int j) -> uint32_t {
+                    const uint32_t x = w == 0 ? r[j].x : w == 1 ? r[j].y : w == 2 ? r[j].z : r[j].w;
+                    return (x >> sh) & 0xffffu;
+                };
+                uint2 pk;
+                pk.x = el(0) | (el(1) << 16);
+                pk.y = el(2) | (el(3) << 16);
+                *reinterpret_cast<uint2*>(&sV[(8 * dc + e) * kVStr + kp]) = pk;
+            }
+        }
+        __syncthreads();
+
+        // S^T = K Q^T for the two 32-key sub-tiles.
+        f32x16 st[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) st[t][v] = 0.f;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const uint4 kv = *reinterpret_cast<const uint4*>(
+                    &sK[(t * 32 + (lane & 31)) * kKStr + 16 * c + 8 * half]);
+                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8, kv), qreg[c], st[t], 0, 0, 0);
+            }
+        }
+        // Scale, mask, row max. Lane holds keys kb + 32t + 8(v/4) + 4*half + v%4 of its row.
+        const bool full = kb >= max_ws && kb + kKT - 1 <= min_qpos;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                float x = st[t][v] * a.scale_log2;
+                if (!full) {
+                    const int kpos = kb + 32 * t + 8 * (v >> 2) + 4 * half + (v & 3);
+                    if (!live || kpos > qpos || kpos < ws_row) x = -INFINITY;
+                }
+                st[t][v] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = swap32_max(mx);
+        const float m_new = fmaxf(m, mx);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = m == m_new ? 1.f : exp2f(m - m_new);
+        float ls = 0.f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float p = exp2f(st[t][v] - m_use);  // exp2(-inf) = 0
+                st[t][v] = p;
+                ls += p;
+            }
+        l = l * alpha + ls;
+        m = m_new;
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
+        }
+        // O^T += V^T P^T, 16 keys per step: step ks uses registers 8*(ks%2) .. +7 of
+        // sub-tile ks/2 (keys 16ks + {4h..4h+3, 8+4h..8+4h+3} for lane half h).
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8 ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float p = st[ks >> 1][8 * (ks & 1) + e];
+                const __bf16 h = (__bf16)p;
+                ph[e] = h;
+                pl[e] = (__bf16)(p - (float)h);
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const uint4 vv = *reinterpret_cast<const uint4*>(
+                    &sV[(32 * t + (lane & 31)) * kVStr + 16 * ks + 8 * half]);
+                const bf16x8 av = __builtin_bit_cast(bf16x8, vv);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, ph, o[t], 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pl, o[t], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();
+    const bool bad = s_bad != 0;
+    const float l_row = swap32_sum(l);
+    const float inv = 1.f / (l_row + 1e-10f);
+    if (live) {
+        float* op = out_at(qi, head);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int mq = 0; mq < 4; ++mq) {
+                float4 v;
+                v.x = bad ? __builtin_nanf("") : o[t][4 * mq + 0] * inv;
+                v.y = bad ? __builtin_nanf("") : o[t][4 * mq + 1] * inv;
+                v.z = bad ? __builtin_nanf("") : o[t][4 * mq + 2] * inv;
+                v.w = bad ? __builtin_nanf("") : o[t][4 * mq + 3] * inv;
+                *reinterpret_cast<float4*>(op + 32 * t + 8 * mq + 4 * half) = v;
+            }
+    }
+}
+
+}  // namespace
+}  // namespace pkv
+
+extern "C" {
+
+int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void* k_pool,
+                    const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                    const int32_t* pos, const int32_t* q_off, int32_t max_q, int32_t batch,
+                    int32_t max_pos, float* out) {
+    using namespace pkv;
+    clear_error();
+    int32_t rc = validate_params(p);
+    if (rc != PKV_OK) return rc;
+    if (p->kv_dtype != PKV_DTYPE_BF16)
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: the MFMA path needs bf16 pools");
+    if (p->head_dim != kD) return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: head_dim 256 only");
+    const int G = p->num_heads / p->num_kv_heads;
+    if (G != 1 && G != 2 && G != 4)
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: num_heads / num_kv_heads must be 1, 2 or 4");
+    if (batch <= 0 || batch > 65535 || max_q <= 0 || table_stride <= 0 || max_pos < 0 ||
+        p->num_kv_heads > 65535)
+        return fail(PKV_ERR_INVALID, "pkv_prefill: batch, max_q, table_stride must be positive");
+    if (!q || !k_pool || !v_pool || !block_tables || !pos || !q_off || !out)
+        return fail(PKV_ERR_INVALID, "pkv_prefill: null device pointer");
+    if ((int64_t)p->num_blocks << __builtin_ctz((unsigned)p->block_size) > INT32_MAX)
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: pool rows must fit in int32");
+    PrefillArgs a{};
+    a.q = static_cast<const uint16_t*>(q);
+    a.k_pool = static_cast<const uint16_t*>(k_pool);
+    a.v_pool = static_cast<const uint16_t*>(v_pool);
+    a.tables = block_tables;
+    a.table_stride = table_stride;
+    a.pos = pos;
+    a.q_off = q_off;
+    a.Hq = p->num_heads;
+    a.Hkv = p->num_kv_heads;
+    a.bs_shift = __builtin_ctz((unsigned)p->block_size);
+    a.num_blocks = p->num_blocks;
+    a.window = p->window;
+    a.scale_log2 = p->scale * kLog2e;
+    a.max_q = max_q;
+    a.max_pos = max_pos;
+    a.out = out;
+    const int qb = 128 / G;
+    a.qtiles = (max_q + qb - 1) / qb;
+    dim3 grid(a.qtiles, p->num_kv_heads, batch);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (G == 1) hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kNT), 0, st, a);
+    else if (G == 2) hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kNT), 0, st, a);
+    else hipLaunchKernelGGL(prefill_kernel<4>, grid, dim3(kNT), 0, st, a);
+    return check_launch("pkv_prefill");
+}
+
+}  // extern "C"

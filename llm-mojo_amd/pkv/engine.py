@@ -167,6 +167,19 @@ class PagedKVCache:
                  self.max_pos if max_pos is None else max_pos, _ptr(out), self.workspace.ptr,
                  self.workspace.nbytes)
 
+    def prefill(self, layer: int, q, pos, q_off, max_q: int, out, batch: int | None = None,
+                max_pos: int | None = None):
+        """Chunked-prefill attention (K3, bf16 pools): q bf16 [rows][Hq][D] (device),
+        out fp32 [rows][Hq][D]; sequence s owns rows q_off[s] .. q_off[s+1]-1 at positions
+        pos[s], pos[s] + 1, ... and attends causally over its prefix and the chunk."""
+        b = batch or self.max_seqs
+        p = self.params[layer]
+        lib.call("pkv_prefill", self._stream(), ctypes.byref(p), _ptr(q),
+                 self.k_pools[layer].ptr, self.v_pools[layer].ptr, self.tables.ptr,
+                 self.table_stride, self._ints(pos, self._i32_a, b),
+                 self._ints(q_off, self._i32_b, b + 1), max_q, b,
+                 self.max_pos if max_pos is None else max_pos, _ptr(out))
+
     def rollback(self, new_len, batch: int | None = None, status=None):
         """Truncate tables to ceil(new_len / block_size) blocks, freeing the tail in
         ascending logical order (K5). new_len[s] < 0 leaves slot s alone; 0 retires it."""

@@ -53,6 +53,7 @@ PROTOTYPES = {
                           _sz]),
     "pkv_decode": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _sz]),
     "pkv_rollback": (_i32, [_vp, _PP, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp]),
+    "pkv_prefill": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "pkv_paged_attention_layer": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                                          _i32, _vp, _i32, _i32, _i32, _i32, _vp, _sz]),
     "pkv_last_error": (ctypes.c_char_p, []),

@@ -322,3 +322,79 @@ class VerifySchedule:
         keys = sum(int(self.length[it, s]) * self.DRAFT
                    + self.DRAFT * (self.DRAFT + 1) // 2 for s in range(self.B))
         return 4 * self.D * self.HQ * keys
+
+
+class PrefillChunk:
+    """Config 4: chunked prefill into the paged cache, bf16,
+    MFMA path. 4 sequences, 16 q / 8 kv heads, head_dim 256, block 16. Each sequence
+    already holds a prefix of seeded length in [0, 6144] (seeded random block tables);
+    a 2048-token chunk of Q/K/V ~ N(0, 1) bf16 is appended (the chunk fills the prefix's
+    partial last block, then freshly allocated blocks popped from the LIFO free list) and
+    every chunk query attends causally over prefix plus chunk, fp32 accumulation. The pool
+    holds the blocks prefix + chunk need, plus 10 %."""
+
+    HQ, HKV, D, BS = 16, 8, 256, 16
+    B = 4
+    CHUNK = 2048
+    PREFIX_MAX = 6144
+    SCALE = 0.0625
+    WINDOW = 0
+
+    def __init__(self, seed: int = 0, batch: int | None = None, chunk: int | None = None,
+                 prefix_max: int | None = None, hq: int | None = None, hkv: int | None = None,
+                 window: int | None = None, prefix=None):
+        rng = np.random.default_rng(seed)
+        for name, v in (("B", batch), ("CHUNK", chunk), ("PREFIX_MAX", prefix_max),
+                        ("HQ", hq), ("HKV", hkv), ("WINDOW", window)):
+            if v is not None:
+                setattr(self, name, v)
+        B, bs = self.B, self.BS
+        self.kv_stride = self.HKV * self.D
+        self.prefix = rng.integers(0, self.PREFIX_MAX + 1, B).astype(np.int64)
+        if prefix is not None:
+            self.prefix = np.asarray(prefix, np.int64)
+        need = int(np.sum((self.prefix + self.CHUNK + bs - 1) // bs))
+        self.num_blocks = int(np.ceil(need * 1.1))
+        self.table_stride = int((self.PREFIX_MAX + self.CHUNK + bs - 1) // bs) + 2
+        self.tables0, self.lens0, self.free0 = _assign_tables(
+            rng, (self.prefix + bs - 1) // bs, self.num_blocks, self.table_stride)
+        self.pos = self.prefix.astype(np.int32)
+        self.max_pos = int(self.prefix.max()) + self.CHUNK - 1
+        base = int(rng.integers(1, 2**40))
+        self.seed_k, self.seed_v = base, base + 1
+        self.seed_q, self.seed_knew, self.seed_vnew = base + 2, base + 3, base + 4
+
+    @property
+    def rows(self) -> int:
+        return self.B * self.CHUNK
+
+    def tok_off(self) -> np.ndarray:
+        return (np.arange(self.B + 1) * self.CHUNK).astype(np.int32)
+
+    def device_data(self, stream=None) -> dict:
+        bf = np.uint16
+        prow = self.num_blocks * self.BS
+        return {"k": synth.normal((prow, self.kv_stride), self.seed_k, bf, stream=stream),
+                "v": synth.normal((prow, self.kv_stride), self.seed_v, bf, stream=stream),
+                "q": synth.normal((self.rows, self.HQ, self.D), self.seed_q, bf, stream=stream),
+                "k_new": synth.normal((self.rows, self.kv_stride), self.seed_knew, bf,
+                                      stream=stream),
+                "v_new": synth.normal((self.rows, self.kv_stride), self.seed_vnew, bf,
+                                      stream=stream)}
+
+    def keys_attended(self) -> int:
+        """Sum over all queries of the keys each attends (causal, window 0 or W)."""
+        tot = 0
+        for s in range(self.B):
+            p = np.arange(self.CHUNK, dtype=np.int64) + int(self.prefix[s])
+            lo = np.maximum(p - self.WINDOW + 1, 0) if self.WINDOW > 0 else np.zeros_like(p)
+            tot += int((p - lo + 1).sum())
+        return tot
+
+    def flops(self) -> int:
+        """QK^T and PV: 2 multiply-adds per (query, head, key, dim) -> 4 flops."""
+        return 4 * self.D * self.HQ * self.keys_attended()
+
+    def kv_bytes(self, elt: int = 2) -> int:
+        """K and V of every sequence's prefix + chunk read once per kv head."""
+        return int((self.prefix + self.CHUNK).sum()) * 2 * self.kv_stride * elt

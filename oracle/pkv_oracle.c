@@ -450,7 +450,9 @@ void pkvo_rollback(int32_t block_size, int32_t* tables, int32_t table_stride, in
  * q_scale multiplies q before the call (1.0 = the reference; a power of two is
  * exact, so a softmax scale of 2^-k is emulated without rounding).
  * par: 0 = serial over sequences, head-pair tasks on `nthreads` threads
- *      (reference-faithful); 1 = sequences spread over `nthreads` threads.   */
+ *      (reference-faithful); 1 = sequences spread over `nthreads` threads;
+ *      2 = (sequence, query) pairs spread over `nthreads` threads (the calls are
+ *      independent once the keys are in the pool; used for long prefill chunks). */
 int pkvo_attend(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                 int32_t block_size, int32_t window, float q_scale, const float* q,
                 const void* k_pool, const void* v_pool, const int32_t* tables,
@@ -463,8 +465,11 @@ int pkvo_attend(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head
     }
     int64_t hd = (int64_t)num_heads * head_dim;
     int err = 0;
-    int outer = (par == 1 && nthreads > 1) ? nthreads : 1;
-    int inner = (par == 1) ? 1 : nthreads;
+    int outer = (par >= 1 && nthreads > 1) ? nthreads : 1;
+    int inner = (par >= 1) ? 1 : nthreads;
+    /* par 2: one work item per (sequence, query); otherwise one per sequence. */
+    int64_t items = par == 2 ? (int64_t)batch * q_len : batch;
+    int32_t per_item = par == 2 ? 1 : q_len;
 #pragma omp parallel num_threads(outer) if (outer > 1)
     {
         float* scores = (float*)malloc(sizeof(float) * (size_t)(num_heads * (max_n + 1)));
@@ -472,9 +477,11 @@ int pkvo_attend(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head
         int64_t* tab = (int64_t*)malloc(sizeof(int64_t) * (size_t)(table_stride > 0 ? table_stride : 1));
         float* qs = (float*)malloc(sizeof(float) * (size_t)hd);
 #pragma omp for schedule(dynamic, 1)
-        for (int32_t s = 0; s < batch; ++s) {
+        for (int64_t it = 0; it < items; ++it) {
+            const int32_t s = (int32_t)(par == 2 ? it / q_len : it);
+            const int32_t j0 = (int32_t)(par == 2 ? it % q_len : 0);
             for (int32_t i = 0; i < table_stride; ++i) tab[i] = tables[(int64_t)s * table_stride + i];
-            for (int32_t j = 0; j < q_len; ++j) {
+            for (int32_t j = j0; j < j0 + per_item; ++j) {
                 const float* qj = q + ((int64_t)s * q_len + j) * hd;
                 float* oj = out + ((int64_t)s * q_len + j) * hd;
                 if (pos[s] < 0) {
