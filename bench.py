@@ -33,6 +33,7 @@ for _p in (REPO, os.path.join(REPO, "llm-mojo_amd")):
 METRIC = "paged decode attn tokens/s + achieved HBM GB/s (% peak) at B=32, 1 GPU"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, AMD published
 PEAK_FP64_VALU_TFLOPS = 78.6  # MI355X vector fp64, AMD published
+PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, AMD published
 
 
 def _traffic_from_profiles():
@@ -420,6 +421,91 @@ def bench_config3(args, log):
     return res
 
 
+def bench_config4(args, log):
+    """Config 4: chunked prefill. A step appends the 4 x 2048-token chunks into fresh
+    blocks and runs the MFMA prefill attention; a rollback to the prefix lengths returns
+    the chunk's blocks so every step starts from the same state."""
+    from pkv import BF16, hip
+    from pkv.workloads import PrefillChunk
+
+    w = PrefillChunk(seed=args.seed)
+    d = w.device_data()
+    stream = hip.Stream()
+    S = _Setup(w, 1, BF16, 1, stream)
+    c = S.cache
+    c.k_pools[0].copy_from(d["k"])
+    c.v_pools[0].copy_from(d["v"])
+    D = hip.DeviceArray.from_numpy
+    dpos, doff = D(w.pos), D(w.tok_off())
+    dnl = D(w.prefix.astype(np.int32))
+    out = hip.DeviceArray((w.rows, w.HQ, w.D), np.float32)
+    ev = _event_pairs(hip, args.steps)
+
+    def step(i, events=None):
+        c.append(0, dpos.ptr, doff.ptr, d["k_new"], d["v_new"], w.CHUNK, w.rows)
+        if events:
+            events[i][0].record(stream)
+        c.prefill(0, d["q"], dpos.ptr, doff.ptr, w.CHUNK, out)
+        if events:
+            events[i][1].record(stream)
+        c.rollback(dnl.ptr)
+
+    for i in range(args.warmup):
+        step(i)
+    ms = _timed(hip, stream, args.steps, step)
+    _timed(hip, stream, args.steps, lambda i: step(i, ev))
+    dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    got = out.numpy()
+    flops = w.flops()
+    tf = flops / (dur / 1e3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_MFMA_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_MFMA_TFLOPS, 4), "traffic": None,
+            "kernel": "prefill_kernel<2>", "avg_launch_us": round(dur * 1e3, 2),
+            "algorithmic_flops_per_launch": int(flops),
+            "note": "algorithmic flops (QK^T + PV, causal); the kernel issues 1.5x that on "
+                    "MFMA (PV runs twice, P split into bf16 hi + lo)"}
+    res = _line("config 4 chunked prefill query tokens/s (4 x 2048-token chunks, bf16, MFMA)",
+                w.rows * args.steps / (ms / 1e3), "tokens/s", args.steps, args.warmup,
+                ms / args.steps, "bf16",
+                "BASELINE config 4: 4 sequences, prefix U[0,6144], 2048-token chunk appended "
+                "into fresh blocks, causal attention over prefix + chunk, 16q/8kv/256, block "
+                "16, bf16 Q/K/V, fp32 accumulation", roof,
+                {"prefill_us": round(dur * 1e3, 2), "prefixes": w.prefix.tolist()})
+    if args.cpu_seconds > 0:
+        from oracle import oracle as O
+
+        k, v = d["k"].numpy().reshape(-1), d["v"].numpy().reshape(-1)
+        kn = d["k_new"].numpy().reshape(-1, w.kv_stride)
+        vn = d["v_new"].numpy().reshape(-1, w.kv_stride)
+        q32 = O.bf16_to_f32(d["q"].numpy().reshape(w.rows, w.HQ, w.D))
+        st = O.CacheState(1, w.kv_stride, w.BS, w.num_blocks, w.B, w.table_stride,
+                          dtype=np.uint16, alloc_pools=False)
+        st.k_pools[0], st.v_pools[0] = k, v
+        st.tables[:, :w.tables0.shape[1]] = w.tables0
+        st.table_lens[:] = w.lens0
+        st.bm.free_list[:w.free0.size] = w.free0
+        st.bm.count[0] = w.free0.size
+        st.append(0, w.pos, w.tok_off(), kn, vn, w.CHUNK)
+        # The reference prefills token by token; sample the first n queries of sequence 0
+        # (each one paged_attention_layer call on the head-pair threads) within the bound.
+        n, el, errs = 0, 0.0, []
+        while el < args.cpu_seconds and n < w.CHUNK:
+            t = time.perf_counter()
+            ref = O.attend(q32[n:n + 1].reshape(1, 1, w.HQ, w.D), st.k_pools[0], st.v_pools[0],
+                           st.tables[:1], st.table_lens[:1], w.pos[:1] + n, 1, w.HQ, w.HKV,
+                           w.D, w.BS, 0, scale=w.SCALE, nthreads=args.cpu_threads)
+            el += time.perf_counter() - t
+            errs.append(O.max_rel_err(got[n], ref[0, 0]))
+            n += 1
+        res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s",
+                               "cores": args.cpu_threads, "kind": "port",
+                               "sample": f"first {n} chunk queries of sequence 0 (prefix "
+                                         f"{int(w.prefix[0])}), one paged_attention_layer call "
+                                         f"each, {args.cpu_threads} head-pair tasks"}
+        res["parity_sample_max_rel_err"] = float(f"{max(errs):.3g}")
+    return res
+
+
 def bench_config5(args, log):
     """Config 5: per iteration, MTP reads (4 draft steps x 2 layers, read-only at pos-1),
     4-token verify append + causal attention on both layers, rollback to the accepted
@@ -551,7 +637,7 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=8,
                     help="threads for the reference CPU path (8 = its Hq/2 head-pair tasks)")
     ap.add_argument("--quiet", action="store_true")
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 5],
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="BASELINE.json configuration (2, the default, is the headline)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -571,7 +657,7 @@ def main() -> int:
     if hip.device_count() < 1:
         print("bench.py needs a GPU: no HIP device visible", file=sys.stderr)
         return 1
-    legs = {1: bench_config1, 3: bench_config3, 5: bench_config5}
+    legs = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}
     if args.config in legs:
         print(json.dumps(legs[args.config](args, log)), flush=True)
         return 0

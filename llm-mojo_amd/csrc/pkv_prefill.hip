@@ -39,10 +39,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kD = 256;             // head_dim of this kernel
 constexpr int kKT = 64;             // keys per tile
-constexpr int kKStr = kD + 8;       // K tile row stride (bf16): 528 B, rotates the banks
-constexpr int kVStr = kKT + 8;      // V^T row stride (bf16): 144 B
 constexpr int kNT = 256;            // four waves
 constexpr float kLog2e = 1.4426950408889634f;
+// LDS tiles, double-buffered (bf16 elements). K: [key][256] rows of 512 B whose 16-byte
+// chunk c sits at chunk c ^ (key & 7). V^T: [dim][64 keys] rows of 128 B; keys are
+// permuted inside 16-key groups (bits 2 and 3 swapped) and chunk c of row d sits at
+// chunk c ^ (((d >> 3) ^ d) & 7). Both swizzles keep every group of eight lanes of an
+// operand read or a staging write on distinct banks.
+constexpr int kKTile = kKT * kD;    // elements per K buffer (32 KiB)
+constexpr int kVTile = kD * kKT;    // elements per V^T buffer (32 KiB)
 
 struct PrefillArgs {
     const uint16_t* q;  // bf16 [rows][Hq][D]
@@ -66,6 +71,7 @@ struct PrefillArgs {
 
 // Position of key k (0..63) of a tile inside its V^T row: bits 2 and 3 swapped.
 __device__ inline int vperm(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+__device__ inline int vswz(int d) { return ((d >> 3) ^ d) & 7; }
 
 __device__ inline float swap32_max(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -76,13 +82,16 @@ __device__ inline float swap32_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
 template <int G>
 __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     constexpr int QB = 128 / G;  // queries per workgroup
-    __shared__ __attribute__((aligned(16))) uint16_t sK[kKT * kKStr];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[kD * kVStr];
-    __shared__ int s_row[kKT];
-    __shared__ int s_bad;
+    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    uint16_t* sK = smem;                    // [2][kKTile]
+    uint16_t* sV = smem + 2 * kKTile;       // [2][kVTile]
+    int* s_row = reinterpret_cast<int*>(smem + 2 * kKTile + 2 * kVTile);  // [2][kKT]
+    int* s_bad = s_row + 2 * kKT;
 
     const int s = blockIdx.z;
     const int g = blockIdx.y;
@@ -90,12 +99,13 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int half = lane >> 5;
+    const int l32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = a.q_off[s];
     const int n_q = a.q_off[s + 1] - row0;
     const int q0 = tile * QB;
     const int head = g * G + wave % G;
-    const int qi = q0 + (wave / G) * 32 + (lane & 31);  // this lane's query
+    const int qi = q0 + (wave / G) * 32 + l32;  // this lane's query
     const bool live = qi < n_q;
     const int pos0 = a.pos[s];
     auto out_at = [&](int query, int h) -> float* {
@@ -130,9 +140,81 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     const int k_hi = pos0 + q_last;
     const int qpos = pos0 + qi;
     const int ws_row = window_start(qpos, a.window);
-    // Tiles fully inside every row's [window start, position] need no mask.
-    const int min_qpos = pos0 + q0;
-    const int max_ws = window_start(k_hi, a.window);
+    const int min_qpos = pos0 + q0;                 // tiles inside every row's range
+    const int max_ws = window_start(k_hi, a.window);  // need no mask
+    const int kb0 = k_lo & ~(kKT - 1);
+    const int ntiles = (k_hi - kb0) / kKT + 1;
+
+    const int32_t* trow = a.tables + (size_t)s * a.table_stride;
+    const size_t head_off = (size_t)g * kD;
+    const size_t row_elems = (size_t)a.Hkv * kD;
+    const int bs_mask = (1 << a.bs_shift) - 1;
+
+    // Pool rows of the keys of tile t -> s_row[t % 2] (threads 0..63).
+    auto stage_rows = [&](int t) {
+        if (tid < kKT && t < ntiles) {
+            const int kpos = min(max(kb0 + t * kKT + tid, k_lo), k_hi);
+            int b = trow[kpos >> a.bs_shift];
+            if (b < 0 || b >= a.num_blocks) {
+                *s_bad = 1;
+                b = 0;
+            }
+            s_row[(t & 1) * kKT + tid] = (b << a.bs_shift) | (kpos & bs_mask);
+        }
+    };
+    // K tile t -> sK[t % 2] straight from global memory into LDS: each wave instruction
+    // fills two key rows (1 KiB); lane i loads the global chunk that belongs at chunk
+    // i % 32 of its row under the swizzle.
+    auto issue_k = [&](int t) {
+        uint16_t* dst = sK + (t & 1) * kKTile;
+        const int* rows = s_row + (t & 1) * kKT;
+#pragma unroll
+        for (int j = 0; j < kKT / 8; ++j) {  // 8 instructions per wave, 2 rows each
+            const int key = wave * (kKT / 4) + 2 * j + half;
+            const int c = l32 ^ (key & 7);
+            const uint16_t* src = a.k_pool + (size_t)rows[key] * row_elems + head_off + 8 * c;
+            __builtin_amdgcn_global_load_lds(
+                src, (lds_void*)(dst + (wave * (kKT / 4) + 2 * j) * kD), 16, 0, 0);
+        }
+    };
+    // V tile t: unit = 4 consecutive keys x 8 dims (two units per thread).
+    uint4 vreg[2][4];
+    auto load_v = [&](int t) {
+        const int* rows = s_row + (t & 1) * kKT;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int u = tid + i * kNT;
+            const int kg = u >> 5, dc = u & 31;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                vreg[i][j] = *reinterpret_cast<const uint4*>(
+                    a.v_pool + (size_t)rows[4 * kg + j] * row_elems + head_off + 8 * dc);
+        }
+    };
+    auto store_v = [&](int t) {
+        uint16_t* dst = sV + (t & 1) * kVTile;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int u = tid + i * kNT;
+            const int kg = u >> 5, dc = u & 31;
+            const int kp = vperm(4 * kg);  // 4-aligned: the 4 keys stay contiguous
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int d = 8 * dc + e;
+                const int w = e >> 1, sh = (e & 1) * 16;
+                auto el = [&](int j) -> uint32_t {
+                    const uint4& r = vreg[i][j];
+                    const uint32_t x = w == 0 ? r.x : w == 1 ? r.y : w == 2 ? r.z : r.w;
+                    return (x >> sh) & 0xffffu;
+                };
+                uint2 pk;
+                pk.x = el(0) | (el(1) << 16);
+                pk.y = el(2) | (el(3) << 16);
+                const int col = (((kp >> 3) ^ vswz(d)) << 3) | (kp & 7);
+                *reinterpret_cast<uint2*>(&dst[d * kKT + col]) = pk;
+            }
+        }
+    };
 
     // Q as the B operand of S^T: lane holds Q[row][16c + 8*half .. +7] for c = 0..15.
     bf16x8 qreg[16];
@@ -152,88 +234,64 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
     float m = -INFINITY;  // running max (log2 domain) of this lane's row
     float l = 0.f;        // this lane's share of the running sum (keys of its half)
-    if (tid == 0) s_bad = 0;
 
-    const int32_t* trow = a.tables + (size_t)s * a.table_stride;
-    const size_t head_off = (size_t)g * kD;
-    const size_t row_elems = (size_t)a.Hkv * kD;
-    const int bs_mask = (1 << a.bs_shift) - 1;
+    // prologue: tile 0 staged, tile 1's rows known
+    if (tid == 0) *s_bad = 0;
+    stage_rows(0);
+    __syncthreads();
+    issue_k(0);
+    load_v(0);
+    store_v(0);
+    stage_rows(1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 
-    for (int kb = k_lo & ~(kKT - 1); kb <= k_hi; kb += kKT) {
-        __syncthreads();  // the previous tile's LDS reads are done
-        if (tid < kKT) {
-            const int kpos = min(max(kb + tid, k_lo), k_hi);
-            int b = trow[kpos >> a.bs_shift];
-            if (b < 0 || b >= a.num_blocks) {
-                s_bad = 1;
-                b = 0;
-            }
-            s_row[tid] = (b << a.bs_shift) | (kpos & bs_mask);
+    for (int t = 0; t < ntiles; ++t) {
+        const int kb = kb0 + t * kKT;
+        const bool more = t + 1 < ntiles;
+        if (more) {
+            issue_k(t + 1);
+            load_v(t + 1);
         }
-        __syncthreads();
-        // K tile: 64 keys x 32 chunks of 8 elements, row-major with a padded stride.
-#pragma unroll
-        for (int i = 0; i < (kKT * kD / 8) / kNT; ++i) {
-            const int u = tid + i * kNT;
-            const int key = u >> 5, dc = u & 31;
-            const uint4 v = *reinterpret_cast<const uint4*>(
-                a.k_pool + (size_t)s_row[key] * row_elems + head_off + 8 * dc);
-            *reinterpret_cast<uint4*>(&sK[key * kKStr + 8 * dc]) = v;
-        }
-        // V tile transposed: unit = 4 consecutive keys x 8 dims; each dim's 4 keys go to
-        // one 8-byte run at the permuted key position.
-#pragma unroll
-        for (int i = 0; i < (kKT / 4) * (kD / 8) / kNT; ++i) {
-            const int u = tid + i * kNT;
-            const int kg = u >> 5, dc = u & 31;
-            uint4 r[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                r[j] = *reinterpret_cast<const uint4*>(
-                    a.v_pool + (size_t)s_row[4 * kg + j] * row_elems + head_off + 8 * dc);
-            const int kp = vperm(4 * kg);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int w = e >> 1, sh = (e & 1) * 16;
-                auto el = [&](int j) -> uint32_t {
-                    const uint32_t x = w == 0 ? r[j].x : w == 1 ? r[j].y : w == 2 ? r[j].z : r[j].w;
-                    return (x >> sh) & 0xffffu;
-                };
-                uint2 pk;
-                pk.x = el(0) | (el(1) << 16);
-                pk.y = el(2) | (el(3) << 16);
-                *reinterpret_cast<uint2*>(&sV[(8 * dc + e) * kVStr + kp]) = pk;
-            }
-        }
-        __syncthreads();
+        const uint16_t* cK = sK + (t & 1) * kKTile;
+        const uint16_t* cV = sV + (t & 1) * kVTile;
 
-        // S^T = K Q^T for the two 32-key sub-tiles.
+        // S^T = K Q^T for the two 32-key sub-tiles, operands read two steps ahead.
         f32x16 st[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int v = 0; v < 16; ++v) st[0][v] = st[1][v] = 0.f;
+        auto kop = [&](int sub, int c) -> bf16x8 {
+            const int key = sub * 32 + l32;
+            const int ch = (2 * c + half) ^ (key & 7);
+            return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cK[key * kD + 8 * ch]));
+        };
+        bf16x8 ka[3][2];
+        ka[0][0] = kop(0, 0);
+        ka[0][1] = kop(1, 0);
+        ka[1][0] = kop(0, 1);
+        ka[1][1] = kop(1, 1);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) st[t][v] = 0.f;
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const uint4 kv = *reinterpret_cast<const uint4*>(
-                    &sK[(t * 32 + (lane & 31)) * kKStr + 16 * c + 8 * half]);
-                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    __builtin_bit_cast(bf16x8, kv), qreg[c], st[t], 0, 0, 0);
+        for (int c = 0; c < 16; ++c) {
+            if (c + 2 < 16) {
+                ka[(c + 2) % 3][0] = kop(0, c + 2);
+                ka[(c + 2) % 3][1] = kop(1, c + 2);
             }
+            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c % 3][0], qreg[c], st[0], 0, 0, 0);
+            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c % 3][1], qreg[c], st[1], 0, 0, 0);
         }
         // Scale, mask, row max. Lane holds keys kb + 32t + 8(v/4) + 4*half + v%4 of its row.
         const bool full = kb >= max_ws && kb + kKT - 1 <= min_qpos;
         float mx = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                float x = st[t][v] * a.scale_log2;
+                float x = st[u][v] * a.scale_log2;
                 if (!full) {
-                    const int kpos = kb + 32 * t + 8 * (v >> 2) + 4 * half + (v & 3);
+                    const int kpos = kb + 32 * u + 8 * (v >> 2) + 4 * half + (v & 3);
                     if (!live || kpos > qpos || kpos < ws_row) x = -INFINITY;
                 }
-                st[t][v] = x;
+                st[u][v] = x;
                 mx = fmaxf(mx, x);
             }
         mx = swap32_max(mx);
@@ -242,25 +300,38 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         const float alpha = m == m_new ? 1.f : exp2f(m - m_new);
         float ls = 0.f;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const float p = exp2f(st[t][v] - m_use);  // exp2(-inf) = 0
-                st[t][v] = p;
+                const float p = exp2f(st[u][v] - m_use);  // exp2(-inf) = 0
+                st[u][v] = p;
                 ls += p;
             }
         l = l * alpha + ls;
         m = m_new;
         if (__any(alpha != 1.f)) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
+            for (int u = 0; u < 8; ++u)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
+                for (int v = 0; v < 16; ++v) o[u][v] *= alpha;
         }
         // O^T += V^T P^T, 16 keys per step: step ks uses registers 8*(ks%2) .. +7 of
-        // sub-tile ks/2 (keys 16ks + {4h..4h+3, 8+4h..8+4h+3} for lane half h).
+        // sub-tile ks/2 (keys 16ks + {4h..4h+3, 8+4h..8+4h+3} for lane half h), which
+        // sit at V^T positions 16ks + 8h .. +7 (the vperm order).
+        auto vop = [&](int ks, int u) -> bf16x8 {
+            const int d = 32 * u + l32;
+            const int ch = (2 * ks + half) ^ vswz(d);
+            return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cV[d * kKT + 8 * ch]));
+        };
+        bf16x8 va[2][8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) va[0][u] = vop(0, u);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
+            if (ks + 1 < 4) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) va[(ks + 1) & 1][u] = vop(ks + 1, u);
+            }
             bf16x8 ph, pl;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -270,34 +341,40 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
                 pl[e] = (__bf16)(p - (float)h);
             }
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const uint4 vv = *reinterpret_cast<const uint4*>(
-                    &sV[(32 * t + (lane & 31)) * kVStr + 16 * ks + 8 * half]);
-                const bf16x8 av = __builtin_bit_cast(bf16x8, vv);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, ph, o[t], 0, 0, 0);
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pl, o[t], 0, 0, 0);
-            }
+            for (int u = 0; u < 8; ++u)
+                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[ks & 1][u], ph, o[u], 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[ks & 1][u], pl, o[u], 0, 0, 0);
         }
+        if (more) {
+            store_v(t + 1);
+            stage_rows(t + 2);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // tile t+1's direct-to-LDS K loads have landed
+        __syncthreads();
     }
-    __syncthreads();
-    const bool bad = s_bad != 0;
+    const bool bad = *s_bad != 0;
     const float l_row = swap32_sum(l);
     const float inv = 1.f / (l_row + 1e-10f);
     if (live) {
         float* op = out_at(qi, head);
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+        for (int u = 0; u < 8; ++u)
 #pragma unroll
             for (int mq = 0; mq < 4; ++mq) {
                 float4 v;
-                v.x = bad ? __builtin_nanf("") : o[t][4 * mq + 0] * inv;
-                v.y = bad ? __builtin_nanf("") : o[t][4 * mq + 1] * inv;
-                v.z = bad ? __builtin_nanf("") : o[t][4 * mq + 2] * inv;
-                v.w = bad ? __builtin_nanf("") : o[t][4 * mq + 3] * inv;
-                *reinterpret_cast<float4*>(op + 32 * t + 8 * mq + 4 * half) = v;
+                v.x = bad ? __builtin_nanf("") : o[u][4 * mq + 0] * inv;
+                v.y = bad ? __builtin_nanf("") : o[u][4 * mq + 1] * inv;
+                v.z = bad ? __builtin_nanf("") : o[u][4 * mq + 2] * inv;
+                v.w = bad ? __builtin_nanf("") : o[u][4 * mq + 3] * inv;
+                *reinterpret_cast<float4*>(op + 32 * u + 8 * mq + 4 * half) = v;
             }
     }
 }
+
+// Dynamic LDS of prefill_kernel: two K and two V^T tiles, two row tables, a flag.
+constexpr size_t kPrefillLds = (size_t)(2 * kKTile + 2 * kVTile) * 2 + (2 * kKT + 4) * 4;
 
 }  // namespace
 }  // namespace pkv
@@ -346,9 +423,17 @@ int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void
     a.qtiles = (max_q + qb - 1) / qb;
     dim3 grid(a.qtiles, p->num_kv_heads, batch);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (G == 1) hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kNT), 0, st, a);
-    else if (G == 2) hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kNT), 0, st, a);
-    else hipLaunchKernelGGL(prefill_kernel<4>, grid, dim3(kNT), 0, st, a);
+    const void* fn = G == 1 ? reinterpret_cast<const void*>(&prefill_kernel<1>)
+                   : G == 2 ? reinterpret_cast<const void*>(&prefill_kernel<2>)
+                            : reinterpret_cast<const void*>(&prefill_kernel<4>);
+    // Above 64 KiB of dynamic LDS the kernel must opt in (once per kernel and device).
+    static_assert(kPrefillLds <= 160 * 1024, "LDS budget of one CU");
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrefillLds) !=
+        hipSuccess)
+        return fail(PKV_ERR_HIP, "pkv_prefill: could not reserve the kernel's LDS");
+    if (G == 1) hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kNT), kPrefillLds, st, a);
+    else if (G == 2) hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kNT), kPrefillLds, st, a);
+    else hipLaunchKernelGGL(prefill_kernel<4>, grid, dim3(kNT), kPrefillLds, st, a);
     return check_launch("pkv_prefill");
 }
 
