@@ -90,8 +90,9 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
     uint16_t* sK = smem;                    // [2][kKTile]
     uint16_t* sV = smem + 2 * kKTile;       // [2][kVTile]
-    int* s_row = reinterpret_cast<int*>(smem + 2 * kKTile + 2 * kVTile);  // [2][kKT]
-    int* s_bad = s_row + 2 * kKT;
+    // element offset of each key's head slice in the pools, per staged tile
+    int64_t* s_off = reinterpret_cast<int64_t*>(smem + 2 * kKTile + 2 * kVTile);  // [2][kKT]
+    int* s_bad = reinterpret_cast<int*>(s_off + 2 * kKT);
 
     const int s = blockIdx.z;
     const int g = blockIdx.y;
@@ -150,7 +151,8 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     const size_t row_elems = (size_t)a.Hkv * kD;
     const int bs_mask = (1 << a.bs_shift) - 1;
 
-    // Pool rows of the keys of tile t -> s_row[t % 2] (threads 0..63).
+    // Pool offsets of the keys of tile t -> s_off[t % 2] (threads 0..63). Keys outside
+    // [k_lo, k_hi] re-read a valid row and are masked.
     auto stage_rows = [&](int t) {
         if (tid < kKT && t < ntiles) {
             const int kpos = min(max(kb0 + t * kKT + tid, k_lo), k_hi);
@@ -159,7 +161,8 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
                 *s_bad = 1;
                 b = 0;
             }
-            s_row[(t & 1) * kKT + tid] = (b << a.bs_shift) | (kpos & bs_mask);
+            const int row = (b << a.bs_shift) | (kpos & bs_mask);
+            s_off[(t & 1) * kKT + tid] = (int64_t)row * (int64_t)row_elems + (int64_t)head_off;
         }
     };
     // K tile t -> sK[t % 2] straight from global memory into LDS: each wave instruction
@@ -167,49 +170,44 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     // i % 32 of its row under the swizzle.
     auto issue_k = [&](int t) {
         uint16_t* dst = sK + (t & 1) * kKTile;
-        const int* rows = s_row + (t & 1) * kKT;
+        const int64_t* offs = s_off + (t & 1) * kKT;
 #pragma unroll
         for (int j = 0; j < kKT / 8; ++j) {  // 8 instructions per wave, 2 rows each
             const int key = wave * (kKT / 4) + 2 * j + half;
             const int c = l32 ^ (key & 7);
-            const uint16_t* src = a.k_pool + (size_t)rows[key] * row_elems + head_off + 8 * c;
+            const uint16_t* src = a.k_pool + offs[key] + 8 * c;
             __builtin_amdgcn_global_load_lds(
                 src, (lds_void*)(dst + (wave * (kKT / 4) + 2 * j) * kD), 16, 0, 0);
         }
     };
     // V tile t: unit = 4 consecutive keys x 8 dims (two units per thread).
-    uint4 vreg[2][4];
-    auto load_v = [&](int t) {
-        const int* rows = s_row + (t & 1) * kKT;
+    uint4 vreg[4];
+    auto load_v = [&](int t, int i) {  // unit i of this thread: keys 4kg..4kg+3, dims 8dc..+7
+        const int64_t* offs = s_off + (t & 1) * kKT;
+        const int u = tid + i * kNT;
+        const int kg = u >> 5, dc = u & 31;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int u = tid + i * kNT;
-            const int kg = u >> 5, dc = u & 31;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                vreg[i][j] = *reinterpret_cast<const uint4*>(
-                    a.v_pool + (size_t)rows[4 * kg + j] * row_elems + head_off + 8 * dc);
-        }
+        for (int j = 0; j < 4; ++j)
+            vreg[j] = *reinterpret_cast<const uint4*>(a.v_pool + offs[4 * kg + j] + 8 * dc);
     };
-    auto store_v = [&](int t) {
+    auto store_v = [&](int t, int i) {
         uint16_t* dst = sV + (t & 1) * kVTile;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        {
             const int u = tid + i * kNT;
             const int kg = u >> 5, dc = u & 31;
             const int kp = vperm(4 * kg);  // 4-aligned: the 4 keys stay contiguous
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int d = 8 * dc + e;
-                const int w = e >> 1, sh = (e & 1) * 16;
-                auto el = [&](int j) -> uint32_t {
-                    const uint4& r = vreg[i][j];
-                    const uint32_t x = w == 0 ? r.x : w == 1 ? r.y : w == 2 ? r.z : r.w;
-                    return (x >> sh) & 0xffffu;
+                // dim e of keys j = 0..3: 16-bit half (e & 1) of word e / 2 of vreg[i][j]
+                auto word = [&](int j) -> uint32_t {
+                    const uint4& r = vreg[j];
+                    return (e >> 1) == 0 ? r.x : (e >> 1) == 1 ? r.y : (e >> 1) == 2 ? r.z : r.w;
                 };
+                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
                 uint2 pk;
-                pk.x = el(0) | (el(1) << 16);
-                pk.y = el(2) | (el(3) << 16);
+                pk.x = __builtin_amdgcn_perm(word(1), word(0), sel);
+                pk.y = __builtin_amdgcn_perm(word(3), word(2), sel);
                 const int col = (((kp >> 3) ^ vswz(d)) << 3) | (kp & 7);
                 *reinterpret_cast<uint2*>(&dst[d * kKT + col]) = pk;
             }
@@ -240,8 +238,10 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     stage_rows(0);
     __syncthreads();
     issue_k(0);
-    load_v(0);
-    store_v(0);
+    load_v(0, 0);
+    store_v(0, 0);
+    load_v(0, 1);
+    store_v(0, 1);
     stage_rows(1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         const bool more = t + 1 < ntiles;
         if (more) {
             issue_k(t + 1);
-            load_v(t + 1);
+            load_v(t + 1, 0);
         }
         const uint16_t* cK = sK + (t & 1) * kKTile;
         const uint16_t* cV = sV + (t & 1) * kVTile;
@@ -265,51 +265,65 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
             const int ch = (2 * c + half) ^ (key & 7);
             return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cK[key * kD + 8 * ch]));
         };
-        bf16x8 ka[3][2];
+        bf16x8 ka[2][2];
         ka[0][0] = kop(0, 0);
         ka[0][1] = kop(1, 0);
-        ka[1][0] = kop(0, 1);
-        ka[1][1] = kop(1, 1);
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            if (c + 2 < 16) {
-                ka[(c + 2) % 3][0] = kop(0, c + 2);
-                ka[(c + 2) % 3][1] = kop(1, c + 2);
+            if (c + 1 < 16) {
+                ka[(c + 1) & 1][0] = kop(0, c + 1);
+                ka[(c + 1) & 1][1] = kop(1, c + 1);
             }
-            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c % 3][0], qreg[c], st[0], 0, 0, 0);
-            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c % 3][1], qreg[c], st[1], 0, 0, 0);
+            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c & 1][0], qreg[c], st[0], 0, 0, 0);
+            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c & 1][1], qreg[c], st[1], 0, 0, 0);
         }
-        // Scale, mask, row max. Lane holds keys kb + 32t + 8(v/4) + 4*half + v%4 of its row.
-        const bool full = kb >= max_ws && kb + kKT - 1 <= min_qpos;
+        if (more) {
+            store_v(t + 1, 0);
+            load_v(t + 1, 1);
+        }
+        // Mask and row max of the raw scores (scale > 0, so the max commutes with it).
+        // Lane holds keys kb + 32u + 8(v/4) + 4*half + v%4 of its row. Tiles inside every
+        // row's [window start, position] skip the mask.
         float mx = -INFINITY;
+        if (kb >= max_ws && kb + kKT - 1 <= min_qpos) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                float x = st[u][v] * a.scale_log2;
-                if (!full) {
+                for (int v = 0; v < 16; ++v) mx = fmaxf(mx, st[u][v]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
                     const int kpos = kb + 32 * u + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (!live || kpos > qpos || kpos < ws_row) x = -INFINITY;
+                    const bool ok = live && kpos <= qpos && kpos >= ws_row;
+                    st[u][v] = ok ? st[u][v] : -INFINITY;
+                    mx = fmaxf(mx, st[u][v]);
                 }
-                st[u][v] = x;
-                mx = fmaxf(mx, x);
-            }
-        mx = swap32_max(mx);
-        const float m_new = fmaxf(m, mx);
+        }
+        mx = swap32_max(mx) * a.scale_log2;
+        // The reference max m moves only when the tile max exceeds it by more than 8
+        // (log2 units): p = exp2(s - m) <= 256 stays exact enough in fp32, the result is
+        // unchanged (softmax does not depend on the reference), and the 128 accumulators
+        // are rescaled only on the rare tiles that move it.
+        const bool move = mx > m + 8.f;
+        const float m_new = move ? mx : m;
+        const float alpha = move ? __builtin_amdgcn_exp2f(m - m_new) : 1.f;  // m = -inf: 0
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = m == m_new ? 1.f : exp2f(m - m_new);
-        float ls = 0.f;
+        // v_exp_f32 directly: results below 2^-126 flush to zero, which is immaterial next
+        // to the row sum (>= 1 for the key that sets the max).
+        float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const float p = exp2f(st[u][v] - m_use);  // exp2(-inf) = 0
+                const float p = __builtin_amdgcn_exp2f(fmaf(st[u][v], a.scale_log2, -m_use));
                 st[u][v] = p;
-                ls += p;
+                lsum[v & 3] += p;
             }
-        l = l * alpha + ls;
+        l = l * alpha + ((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
         m = m_new;
-        if (__any(alpha != 1.f)) {
+        if (__any(move)) {
 #pragma unroll
             for (int u = 0; u < 8; ++u)
 #pragma unroll
@@ -323,15 +337,11 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
             const int ch = (2 * ks + half) ^ vswz(d);
             return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cV[d * kKT + 8 * ch]));
         };
-        bf16x8 va[2][8];
+        bf16x8 va[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) va[0][u] = vop(0, u);
+        for (int u = 0; u < 8; ++u) va[u] = vop(0, u);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            if (ks + 1 < 4) {
-#pragma unroll
-                for (int u = 0; u < 8; ++u) va[(ks + 1) & 1][u] = vop(ks + 1, u);
-            }
             bf16x8 ph, pl;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -342,13 +352,15 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[ks & 1][u], ph, o[u], 0, 0, 0);
+                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u], ph, o[u], 0, 0, 0);
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[ks & 1][u], pl, o[u], 0, 0, 0);
+            for (int u = 0; u < 8; ++u) {
+                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u], pl, o[u], 0, 0, 0);
+                if (ks + 1 < 4) va[u] = vop(ks + 1, u);  // next step's operand, 8 MFMAs ahead
+            }
         }
         if (more) {
-            store_v(t + 1);
+            store_v(t + 1, 1);
             stage_rows(t + 2);
         }
         __builtin_amdgcn_s_waitcnt(0);  // tile t+1's direct-to-LDS K loads have landed
@@ -373,8 +385,8 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     }
 }
 
-// Dynamic LDS of prefill_kernel: two K and two V^T tiles, two row tables, a flag.
-constexpr size_t kPrefillLds = (size_t)(2 * kKTile + 2 * kVTile) * 2 + (2 * kKT + 4) * 4;
+// Dynamic LDS of prefill_kernel: two K and two V^T tiles, two key-offset tables, a flag.
+constexpr size_t kPrefillLds = (size_t)(2 * kKTile + 2 * kVTile) * 2 + 2 * kKT * 8 + 16;
 
 }  // namespace
 }  // namespace pkv
@@ -395,6 +407,8 @@ int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void
     const int G = p->num_heads / p->num_kv_heads;
     if (G != 1 && G != 2 && G != 4)
         return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: num_heads / num_kv_heads must be 1, 2 or 4");
+    if (!(p->scale > 0.f) || !(p->scale < INFINITY))
+        return fail(PKV_ERR_INVALID, "pkv_prefill: scale must be positive and finite");
     if (batch <= 0 || batch > 65535 || max_q <= 0 || table_stride <= 0 || max_pos < 0 ||
         p->num_kv_heads > 65535)
         return fail(PKV_ERR_INVALID, "pkv_prefill: batch, max_q, table_stride must be positive");
