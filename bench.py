@@ -36,10 +36,10 @@ PEAK_FP64_VALU_TFLOPS = 78.6  # MI355X vector fp64, AMD published
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, AMD published
 
 
-def _traffic_from_profiles():
+def _traffic_from_profiles(name="stream_attend_decode_cfg2_traffic.md"):
     """HBM bytes per attention launch measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by the copy-kernel calibration), from the committed summary."""
-    path = os.path.join(REPO, "profiles", "attend_decode_cfg2_traffic.md")
+    path = os.path.join(REPO, "profiles", name)
     try:
         with open(path) as f:
             for line in f:
@@ -400,6 +400,7 @@ def bench_config3(args, log):
                 _roofline(w.attend_bytes(), dur,
                           "stream_attend_kernel<256, bf16, 2> + stream_merge_kernel<256, float>"),
                 {"attend_us": round(dur * 1e3, 2)})
+    res["roofline"]["traffic"] = _traffic_from_profiles("stream_attend_bf16_cfg3_profile.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
 
