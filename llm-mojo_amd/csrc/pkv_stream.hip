@@ -349,7 +349,9 @@ __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
     if (lane == 0) s_pre[batch] = carry;
 }
 
-template <int D, typename KV, int R>
+// R query rows per wave; WPH waves per KV head split the head's rows (WPH = 2 gives two
+// waves of R rows each, reading the same K/V: the second read of a row slice hits the cache).
+template <int D, typename KV, int R, int WPH>
 __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamArgs a) {
     using Acc = typename SKV<KV>::Acc;
     constexpr int kElt = SKV<KV>::kElt;
@@ -408,7 +410,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     const int k0 = w * per;
     if (k0 >= total) return;
     const int k1 = min(total, k0 + per);
-    const int g = blockIdx.x * kMaxWaves + wave;  // this wave's KV head
+    const int g = blockIdx.x * (kMaxWaves / WPH) + wave / WPH;  // this wave's KV head
+    const int rb = (wave % WPH) * R;  // first of this wave's rows of the head
     if (g >= a.Hkv) return;
 
     const int rows = a.G * a.q_len;
@@ -422,7 +425,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     const int idx_own = lane / REP;
     const int r_own = idx_own % R;
     const int u_own = idx_own / R;
-    const bool row_live = r_own < rows;
+    const bool row_live = rb + r_own < rows;
 
     // first sequence with s_pre[s] <= k0 < s_pre[s + 1]
     int s = 0;
@@ -450,8 +453,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         Acc qr[R][EPL];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (r < rows) {
-                const float* qp = a.q + out_row(a, s, g, r) * D + lane * EPL;
+            if (rb + r < rows) {
+                const float* qp = a.q + out_row(a, s, g, rb + r) * D + lane * EPL;
 #pragma unroll
                 for (int e = 0; e < EPL; e += 2) {
                     const float2 v = *reinterpret_cast<const float2*>(qp + e);
@@ -463,7 +466,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
                 for (int e = 0; e < EPL; ++e) qr[r][e] = (Acc)0;
             }
         }
-        const int pq_own = pos0 + r_own / a.G;  // query position of my row
+        const int pq_own = pos0 + (rb + r_own) / a.G;  // query position of my row
         const int ws_own = window_start(pq_own, a.window);
 
         Acc m_own = (Acc)-INFINITY, l_own = (Acc)0;
@@ -558,9 +561,9 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         if (single) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (r < rows) {
+                if (rb + r < rows) {
                     const Acc inv = (Acc)1 / (bcast(l_own, r * REP) + (Acc)1e-10);
-                    float* op = a.out + out_row(a, s, g, r) * D + lane * EPL;
+                    float* op = a.out + out_row(a, s, g, rb + r) * D + lane * EPL;
 #pragma unroll
                     for (int e = 0; e < EPL; e += 2) {
                         float2 v;
@@ -576,8 +579,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             Acc* pml = static_cast<Acc*>(a.part_ml);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (r < rows) {
-                    const int row = (r / a.G) * a.Hq + g * a.G + r % a.G;
+                if (rb + r < rows) {
+                    const int row = ((rb + r) / a.G) * a.Hq + g * a.G + (rb + r) % a.G;
                     Acc* dst = po + (slot + row) * D + lane * EPL;
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) dst[e] = acc[r][e];
@@ -697,21 +700,21 @@ int fill_workgroups(const void* fn, int threads, size_t lds) {
     return p;
 }
 
-template <int D, typename KV, int R>
+template <int D, typename KV, int R, int WPH = 1>
 int32_t launch_r(StreamArgs a, hipStream_t st) {
     using Acc = typename SKV<KV>::Acc;
-    const int waves = a.Hkv < kMaxWaves ? a.Hkv : kMaxWaves;
+    const int waves = a.Hkv * WPH < kMaxWaves ? a.Hkv * WPH : kMaxWaves;
     const int threads = waves * kSW;
     const size_t lds = (size_t)(2 * a.batch + 1) * sizeof(int);
-    const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R>);
+    const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH>);
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
     // Resident workgroups only: the head groups share the slots, and each workgroup
     // covers ceil(total / nwg) keys.
-    const int groups = (a.Hkv + kMaxWaves - 1) / kMaxWaves;
+    const int groups = (a.Hkv * WPH + kMaxWaves - 1) / kMaxWaves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     dim3 grid(groups, a.nwg);
-    hipLaunchKernelGGL((stream_attend_kernel<D, KV, R>), grid, dim3(threads), lds, st, a);
+    hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH>), grid, dim3(threads), lds, st, a);
     hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch), dim3(kMergeNT),
                        0, st, a);
     return PKV_OK;
@@ -771,7 +774,8 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     if (rows <= 1) return bf16 ? launch_r<256, uint16_t, 1>(a, st) : launch_r<256, float, 1>(a, st);
     if (rows <= 2) return bf16 ? launch_r<256, uint16_t, 2>(a, st) : launch_r<256, float, 2>(a, st);
     if (rows <= 4) return bf16 ? launch_r<256, uint16_t, 4>(a, st) : launch_r<256, float, 4>(a, st);
-    if (rows <= 8) return bf16 ? launch_r<256, uint16_t, 8>(a, st) : launch_r<256, float, 8>(a, st);
+    // 5..8 rows (verify): two waves of 4 rows per kv head
+    if (rows <= 8) return bf16 ? launch_r<256, uint16_t, 4, 2>(a, st) : launch_r<256, float, 4, 2>(a, st);
     return fail(PKV_ERR_UNSUPPORTED, "stream path: at most 8 query rows per kv head");
 }
 
