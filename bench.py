@@ -191,7 +191,7 @@ def run_cpu(sched, data, seconds, nthreads, log):
     st.bm.free_list[:sched.free0.size] = sched.free0
     st.bm.count[0] = sched.free0.size
     log("cpu baseline inputs downloaded")
-    outs = []
+    outs, exact = [], []
     elapsed = 0.0
     done = 0
     dec_off = sched.decode_tok_off()
@@ -212,12 +212,18 @@ def run_cpu(sched, data, seconds, nthreads, log):
                          nthreads=nthreads, par=0)
             step_out.append(o)
         elapsed += time.perf_counter() - t0
+        if j < 2:  # float64 attention of the same inputs (outside the timed sample)
+            for layer in range(2):
+                exact.append((j, layer, O.attend_f64(
+                    qh[j, layer], st.k_pools[layer], st.v_pools[layer], st.tables,
+                    sched.pos[j], 1, sched.HQ, sched.HKV, sched.D, sched.BS,
+                    sched.WINDOW if layer == 0 else 0, scale=sched.SCALE)))
         outs.append(step_out)
         done += 1
         if elapsed >= seconds:
             break
     log(f"cpu baseline: {done} steps in {elapsed:.1f}s on {nthreads} threads")
-    return dict(steps=done, seconds=elapsed, outs=outs)
+    return dict(steps=done, seconds=elapsed, outs=outs, exact=exact)
 
 
 class _Setup:
@@ -580,7 +586,7 @@ def bench_config5(args, log):
                 "BASELINE config 5: 16 sequences, ctx U[512,4096], 2 global layers 16q/8kv/256 "
                 "fp32, block 16; per iteration 4 MTP reads at pos-1 per layer, 4-token verify "
                 "append + causal attention, accept U{0..4}, rollback; 32-iteration schedule",
-                _roofline(nbytes, float(dur.mean()), "stream_attend_kernel<256, float, 8> + "
+                _roofline(nbytes, float(dur.mean()), "stream_attend_kernel<256, float, 4> (2 waves per kv head) + "
                           "stream_merge_kernel<256, double>", flops=flops),
                 {"verify_attend_us": round(float(dur.mean()) * 1e3, 2)})
     if args.cpu_seconds > 0:
@@ -597,7 +603,7 @@ def bench_config5(args, log):
         st.bm.count[0] = w.free0.size
         qa, ma = d["q"].numpy(), d["mtp_q"].numpy()
         kn, vn = d["k_new"].numpy(), d["v_new"].numpy()
-        n, el, errs = 0, 0.0, []
+        n, el, errs, e64, own = 0, 0.0, [], [], []
         for it in range(w.ITERS):
             t = time.perf_counter()
             pos = w.pos(it)
@@ -608,11 +614,22 @@ def bench_config5(args, log):
                              scale=w.SCALE, nthreads=args.cpu_threads)
             for layer in range(L):
                 st.append(layer, pos, w.tok_off(), kn[it * L + layer], vn[it * L + layer], DR)
+            refs = []
             for layer in range(L):
                 ref = O.attend(qa[it * L + layer], st.k_pools[layer], st.v_pools[layer],
                                st.tables, st.table_lens, pos, DR, w.HQ, w.HKV, w.D, w.BS, 0,
                                scale=w.SCALE, nthreads=args.cpu_threads)
                 errs.append(O.max_rel_err(got[it, layer], ref))
+                refs.append(ref)
+            el += time.perf_counter() - t
+            if it == 0:  # float64 attention of iteration 0 (outside the timed sample)
+                for layer in range(L):
+                    ex = O.attend_f64(qa[layer], st.k_pools[layer], st.v_pools[layer],
+                                      st.tables, pos, DR, w.HQ, w.HKV, w.D, w.BS, 0,
+                                      scale=w.SCALE)
+                    e64.append(O.max_rel_err(got[0, layer], ex))
+                    own.append(O.max_rel_err(refs[layer], ex))
+            t = time.perf_counter()
             st.rollback(w.new_len(it))
             el += time.perf_counter() - t
             n += 1
@@ -624,6 +641,10 @@ def bench_config5(args, log):
                                          f"appends, verify as {DR} sequential "
                                          f"paged_attention_layer calls per sequence, rollback)"}
         res["parity_sample_max_rel_err"] = float(f"{max(errs):.3g}")
+        res["parity_sample"] = {"iterations": n, "max_rel_err_vs_cpu_fp32": float(f"{max(errs):.3g}"),
+                                "max_rel_err_vs_float64": float(f"{max(e64):.3g}"),
+                                "cpu_fp32_vs_float64": float(f"{max(own):.3g}"),
+                                "float64_iterations": 1}
     return res
 
 
@@ -718,6 +739,17 @@ def main() -> int:
                       f"{args.cpu_threads} head-pair tasks per call"}
         if errs:
             result["parity_sample_max_rel_err"] = float(f"{max(errs):.3g}")
+            # The fp32 reference path is itself an approximation: on these long contexts it
+            # sits ~1e-4 from the exact (float64) attention. The GPU accumulates in double
+            # and is held to 1e-5 of float64 (tests/parity.py).
+            e64 = [O.max_rel_err(g["outs"][j, layer], ex) for j, layer, ex in c["exact"]]
+            own = [O.max_rel_err(c["outs"][j][layer], ex) for j, layer, ex in c["exact"]]
+            result["parity_sample"] = {
+                "steps": min(c["steps"], steps), "max_rel_err_vs_cpu_fp32": float(f"{max(errs):.3g}"),
+                "max_rel_err_vs_float64": float(f"{max(e64):.3g}"),
+                "cpu_fp32_vs_float64": float(f"{max(own):.3g}"),
+                "float64_steps": len(c["exact"]) // 2,
+                "metric": "max |x-ref|/(|ref|+1e-3)"}
     print(json.dumps(result), flush=True)
     return 0
 

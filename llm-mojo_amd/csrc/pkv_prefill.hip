@@ -91,8 +91,8 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     uint16_t* sK = smem;                    // [2][kKTile]
     uint16_t* sV = smem + 2 * kKTile;       // [2][kVTile]
     // element offset of each key's head slice in the pools, per staged tile
-    int64_t* s_off = reinterpret_cast<int64_t*>(smem + 2 * kKTile + 2 * kVTile);  // [2][kKT]
-    int* s_bad = reinterpret_cast<int*>(s_off + 2 * kKT);
+    int64_t* s_off = reinterpret_cast<int64_t*>(smem + 2 * kKTile + 2 * kVTile);  // [4][kKT]
+    int* s_bad = reinterpret_cast<int*>(s_off + 4 * kKT);
 
     const int s = blockIdx.z;
     const int g = blockIdx.y;
@@ -141,17 +141,16 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     const int k_hi = pos0 + q_last;
     const int qpos = pos0 + qi;
     const int ws_row = window_start(qpos, a.window);
-    const int min_qpos = pos0 + q0;                 // tiles inside every row's range
+    const int min_qpos = pos0 + q0;                   // tiles inside every row's range
     const int max_ws = window_start(k_hi, a.window);  // need no mask
     const int kb0 = k_lo & ~(kKT - 1);
     const int ntiles = (k_hi - kb0) / kKT + 1;
-
     const int32_t* trow = a.tables + (size_t)s * a.table_stride;
     const size_t head_off = (size_t)g * kD;
     const size_t row_elems = (size_t)a.Hkv * kD;
     const int bs_mask = (1 << a.bs_shift) - 1;
 
-    // Pool offsets of the keys of tile t -> s_off[t % 2] (threads 0..63). Keys outside
+    // Pool offsets of the keys of tile t -> s_off[t % 4] (threads 0..63). Keys outside
     // [k_lo, k_hi] re-read a valid row and are masked.
     auto stage_rows = [&](int t) {
         if (tid < kKT && t < ntiles) {
@@ -162,7 +161,7 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
                 b = 0;
             }
             const int row = (b << a.bs_shift) | (kpos & bs_mask);
-            s_off[(t & 1) * kKT + tid] = (int64_t)row * (int64_t)row_elems + (int64_t)head_off;
+            s_off[(t & 3) * kKT + tid] = (int64_t)row * (int64_t)row_elems + (int64_t)head_off;
         }
     };
     // K tile t -> sK[t % 2] straight from global memory into LDS: each wave instruction
@@ -170,20 +169,21 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     // i % 32 of its row under the swizzle.
     auto issue_k = [&](int t) {
         uint16_t* dst = sK + (t & 1) * kKTile;
-        const int64_t* offs = s_off + (t & 1) * kKT;
+        const int64_t* offs = s_off + (t & 3) * kKT;
 #pragma unroll
         for (int j = 0; j < kKT / 8; ++j) {  // 8 instructions per wave, 2 rows each
             const int key = wave * (kKT / 4) + 2 * j + half;
             const int c = l32 ^ (key & 7);
-            const uint16_t* src = a.k_pool + offs[key] + 8 * c;
             __builtin_amdgcn_global_load_lds(
-                src, (lds_void*)(dst + (wave * (kKT / 4) + 2 * j) * kD), 16, 0, 0);
+                a.k_pool + offs[key] + 8 * c, (lds_void*)(dst + (wave * (kKT / 4) + 2 * j) * kD),
+                16, 0, 0);
         }
     };
-    // V tile t: unit = 4 consecutive keys x 8 dims (two units per thread).
+    // V tile t: unit i of this thread = 4 consecutive keys x 8 dims, staged through
+    // registers and written transposed.
     uint4 vreg[4];
-    auto load_v = [&](int t, int i) {  // unit i of this thread: keys 4kg..4kg+3, dims 8dc..+7
-        const int64_t* offs = s_off + (t & 1) * kKT;
+    auto load_v = [&](int t, int i) {
+        const int64_t* offs = s_off + (t & 3) * kKT;
         const int u = tid + i * kNT;
         const int kg = u >> 5, dc = u & 31;
 #pragma unroll
@@ -192,25 +192,23 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     };
     auto store_v = [&](int t, int i) {
         uint16_t* dst = sV + (t & 1) * kVTile;
-        {
-            const int u = tid + i * kNT;
-            const int kg = u >> 5, dc = u & 31;
-            const int kp = vperm(4 * kg);  // 4-aligned: the 4 keys stay contiguous
+        const int u = tid + i * kNT;
+        const int kg = u >> 5, dc = u & 31;
+        const int kp = vperm(4 * kg);  // 4-aligned: the 4 keys stay contiguous
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int d = 8 * dc + e;
-                // dim e of keys j = 0..3: 16-bit half (e & 1) of word e / 2 of vreg[i][j]
-                auto word = [&](int j) -> uint32_t {
-                    const uint4& r = vreg[j];
-                    return (e >> 1) == 0 ? r.x : (e >> 1) == 1 ? r.y : (e >> 1) == 2 ? r.z : r.w;
-                };
-                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-                uint2 pk;
-                pk.x = __builtin_amdgcn_perm(word(1), word(0), sel);
-                pk.y = __builtin_amdgcn_perm(word(3), word(2), sel);
-                const int col = (((kp >> 3) ^ vswz(d)) << 3) | (kp & 7);
-                *reinterpret_cast<uint2*>(&dst[d * kKT + col]) = pk;
-            }
+        for (int e = 0; e < 8; ++e) {
+            const int d = 8 * dc + e;
+            // dim e of keys j = 0..3: 16-bit half (e & 1) of word e / 2 of vreg[j]
+            auto word = [&](int j) -> uint32_t {
+                const uint4& r = vreg[j];
+                return (e >> 1) == 0 ? r.x : (e >> 1) == 1 ? r.y : (e >> 1) == 2 ? r.z : r.w;
+            };
+            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+            uint2 pk;
+            pk.x = __builtin_amdgcn_perm(word(1), word(0), sel);
+            pk.y = __builtin_amdgcn_perm(word(3), word(2), sel);
+            const int col = (((kp >> 3) ^ vswz(d)) << 3) | (kp & 7);
+            *reinterpret_cast<uint2*>(&dst[d * kKT + col]) = pk;
         }
     };
 
@@ -225,83 +223,89 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         }
     }
 
-    f32x16 o[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
-    float m = -INFINITY;  // running max (log2 domain) of this lane's row
-    float l = 0.f;        // this lane's share of the running sum (keys of its half)
-
-    // prologue: tile 0 staged, tile 1's rows known
-    if (tid == 0) *s_bad = 0;
-    stage_rows(0);
-    __syncthreads();
-    issue_k(0);
-    load_v(0, 0);
-    store_v(0, 0);
-    load_v(0, 1);
-    store_v(0, 1);
-    stage_rows(1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    for (int t = 0; t < ntiles; ++t) {
-        const int kb = kb0 + t * kKT;
-        const bool more = t + 1 < ntiles;
-        if (more) {
-            issue_k(t + 1);
-            load_v(t + 1, 0);
-        }
+    // S^T = K Q^T of tile t (two 32-key sub-tiles), K operands read one step ahead.
+    auto qk = [&](int t, f32x16 (&st)[2]) {
         const uint16_t* cK = sK + (t & 1) * kKTile;
-        const uint16_t* cV = sV + (t & 1) * kVTile;
-
-        // S^T = K Q^T for the two 32-key sub-tiles, operands read two steps ahead.
-        f32x16 st[2];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) st[0][v] = st[1][v] = 0.f;
         auto kop = [&](int sub, int c) -> bf16x8 {
             const int key = sub * 32 + l32;
             const int ch = (2 * c + half) ^ (key & 7);
             return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cK[key * kD + 8 * ch]));
         };
-        bf16x8 ka[2][2];
-        ka[0][0] = kop(0, 0);
-        ka[0][1] = kop(1, 0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) st[0][v] = st[1][v] = 0.f;
+        bf16x8 ka[4][2];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) { ka[c][0] = kop(0, c); ka[c][1] = kop(1, c); }
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            if (c + 1 < 16) {
-                ka[(c + 1) & 1][0] = kop(0, c + 1);
-                ka[(c + 1) & 1][1] = kop(1, c + 1);
+            if (c + 3 < 16) {
+                ka[(c + 3) & 3][0] = kop(0, c + 3);
+                ka[(c + 3) & 3][1] = kop(1, c + 3);
             }
-            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c & 1][0], qreg[c], st[0], 0, 0, 0);
-            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c & 1][1], qreg[c], st[1], 0, 0, 0);
+            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c & 3][0], qreg[c], st[0], 0, 0, 0);
+            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c & 3][1], qreg[c], st[1], 0, 0, 0);
         }
-        if (more) {
-            store_v(t + 1, 0);
-            load_v(t + 1, 1);
-        }
-        // Mask and row max of the raw scores (scale > 0, so the max commutes with it).
-        // Lane holds keys kb + 32u + 8(v/4) + 4*half + v%4 of its row. Tiles inside every
-        // row's [window start, position] skip the mask.
+    };
+    // Tiles that straddle a row's causal edge or window start get -inf outside
+    // [window_start(qpos), qpos]; lane holds keys kb + 32u + 8(v/4) + 4*half + v%4.
+    // Rows past the chunk are never written, so they need no mask.
+    auto needs_mask = [&](int t) {
+        const int kb = kb0 + t * kKT;
+        return !(kb >= max_ws && kb + kKT - 1 <= min_qpos);
+    };
+    auto mask = [&](int t, f32x16 (&st)[2]) {
+        const int kb = kb0 + t * kKT;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int kpos = kb + 32 * u + 8 * (v >> 2) + 4 * half + (v & 3);
+                st[u][v] = (kpos <= qpos && kpos >= ws_row) ? st[u][v] : -INFINITY;
+            }
+    };
+
+    f32x16 o[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[u][v] = 0.f;
+    float m = -INFINITY;  // reference max (log2 domain) of this lane's row
+    float l = 0.f;        // this lane's share of the running sum (keys of its half)
+
+    // prologue: tiles 0 and 1 of K and tile 0 of V staged, S^T of tile 0 computed
+    if (tid == 0) *s_bad = 0;
+    stage_rows(0);
+    stage_rows(1);
+    stage_rows(2);
+    __syncthreads();
+    issue_k(0);
+    if (ntiles > 1) issue_k(1);  // tile 1's offsets exist only if the tile does
+    load_v(0, 0);
+    store_v(0, 0);
+    load_v(0, 1);
+    store_v(0, 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    f32x16 st_cur[2];
+    qk(0, st_cur);
+    if (needs_mask(0)) mask(0, st_cur);
+    __syncthreads();  // every wave has read K tile 0 before tile 2 overwrites it
+
+    for (int t = 0; t < ntiles; ++t) {
+        const bool more = t + 1 < ntiles;
+        if (t + 2 < ntiles) issue_k(t + 2);
+        if (more) load_v(t + 1, 0);
+
+        // Block A: S^T of tile t + 1 on the matrix cores while the vector ALUs run the
+        // softmax of tile t (past the last tile the MFMAs read stale LDS; unused).
+        f32x16 st_nxt[2];
+        qk(t + 1, st_nxt);
         float mx = -INFINITY;
-        if (kb >= max_ws && kb + kKT - 1 <= min_qpos) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) mx = fmaxf(mx, st[u][v]);
-        } else {
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int kpos = kb + 32 * u + 8 * (v >> 2) + 4 * half + (v & 3);
-                    const bool ok = live && kpos <= qpos && kpos >= ws_row;
-                    st[u][v] = ok ? st[u][v] : -INFINITY;
-                    mx = fmaxf(mx, st[u][v]);
-                }
-        }
-        mx = swap32_max(mx) * a.scale_log2;
+            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, st_cur[u][v]);
+        mx = swap32_max(mx) * a.scale_log2;  // scale > 0: the max commutes with it
         // The reference max m moves only when the tile max exceeds it by more than 8
         // (log2 units): p = exp2(s - m) <= 256 stays exact enough in fp32, the result is
         // unchanged (softmax does not depend on the reference), and the 128 accumulators
@@ -310,16 +314,20 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         const float m_new = move ? mx : m;
         const float alpha = move ? __builtin_amdgcn_exp2f(m - m_new) : 1.f;  // m = -inf: 0
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        // v_exp_f32 directly: results below 2^-126 flush to zero, which is immaterial next
-        // to the row sum (>= 1 for the key that sets the max).
+        // v_exp_f32 directly: results below 2^-126 flush to zero, immaterial next to the
+        // row sum (>= 1 for the key that set the reference). P = P_hi + P_lo, both bf16.
         float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+        bf16x8 ph[4], pl[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(st[u][v], a.scale_log2, -m_use));
-                st[u][v] = p;
-                lsum[v & 3] += p;
+            for (int e = 0; e < 8; ++e) {
+                const float x = st_cur[ks >> 1][8 * (ks & 1) + e];
+                const float p = __builtin_amdgcn_exp2f(fmaf(x, a.scale_log2, -m_use));
+                lsum[e & 3] += p;
+                const __bf16 h = (__bf16)p;
+                ph[ks][e] = h;
+                pl[ks][e] = (__bf16)(p - (float)h);
             }
         l = l * alpha + ((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
         m = m_new;
@@ -329,9 +337,15 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) o[u][v] *= alpha;
         }
-        // O^T += V^T P^T, 16 keys per step: step ks uses registers 8*(ks%2) .. +7 of
-        // sub-tile ks/2 (keys 16ks + {4h..4h+3, 8+4h..8+4h+3} for lane half h), which
-        // sit at V^T positions 16ks + 8h .. +7 (the vperm order).
+
+        // Block B: O^T += V^T P^T of tile t, 16 keys per step (the register order of the
+        // S^T output, matched by the V^T permutation); V operands read a step ahead;
+        // tile t + 1's V staged into the other buffer in between.
+        if (more) {
+            store_v(t + 1, 0);
+            load_v(t + 1, 1);
+        }
+        const uint16_t* cV = sV + (t & 1) * kVTile;
         auto vop = [&](int ks, int u) -> bf16x8 {
             const int d = 32 * u + l32;
             const int ch = (2 * ks + half) ^ vswz(d);
@@ -342,29 +356,22 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         for (int u = 0; u < 8; ++u) va[u] = vop(0, u);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            bf16x8 ph, pl;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float p = st[ks >> 1][8 * (ks & 1) + e];
-                const __bf16 h = (__bf16)p;
-                ph[e] = h;
-                pl[e] = (__bf16)(p - (float)h);
-            }
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u], ph, o[u], 0, 0, 0);
+                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u], ph[ks], o[u], 0, 0, 0);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u], pl, o[u], 0, 0, 0);
-                if (ks + 1 < 4) va[u] = vop(ks + 1, u);  // next step's operand, 8 MFMAs ahead
+                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u], pl[ks], o[u], 0, 0, 0);
+                if (ks + 1 < 4) va[u] = vop(ks + 1, u);
             }
         }
-        if (more) {
-            store_v(t + 1, 1);
-            stage_rows(t + 2);
-        }
-        __builtin_amdgcn_s_waitcnt(0);  // tile t+1's direct-to-LDS K loads have landed
+        if (more) store_v(t + 1, 1);
+        stage_rows(t + 3);
+        __builtin_amdgcn_s_waitcnt(0);  // tile t+2's direct-to-LDS K loads have landed
         __syncthreads();
+        if (more && needs_mask(t + 1)) mask(t + 1, st_nxt);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) st_cur[u] = st_nxt[u];
     }
     const bool bad = *s_bad != 0;
     const float l_row = swap32_sum(l);
@@ -385,8 +392,8 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     }
 }
 
-// Dynamic LDS of prefill_kernel: two K and two V^T tiles, two key-offset tables, a flag.
-constexpr size_t kPrefillLds = (size_t)(2 * kKTile + 2 * kVTile) * 2 + 2 * kKT * 8 + 16;
+// Dynamic LDS of prefill_kernel: two K and two V^T tiles, four key-offset tables, a flag.
+constexpr size_t kPrefillLds = (size_t)(2 * kKTile + 2 * kVTile) * 2 + 4 * kKT * 8 + 16;
 
 }  // namespace
 }  // namespace pkv
