@@ -6,25 +6,24 @@
 // the cached prefix plus the chunk itself. The chunk's K/V rows are appended first
 // (pkv_append); this kernel then attends all chunk queries in one launch.
 //
-// Workgroup = (tile of 128/G queries, kv head g, sequence), four waves; wave w owns 32
-// rows: query block w / G (32 consecutive queries) of q head g*G + w % G. All four waves
-// share the K/V tiles of 64 keys staged in LDS, so every K/V byte is read once per tile
-// of 128 rows. Per key tile:
-//   S^T = K Q^T  (v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q from registers):
-//     the output puts row j of the wave in lanes j and j + 32, each holding 16 of the 32
-//     keys of a sub-tile, so the online softmax needs one cross-lane step (permlane32);
+// Workgroup = (tile of 128/G queries, kv head g, sequence), eight waves (two per SIMD, so
+// one wave's softmax overlaps the other's matrix work); wave w owns 16 rows: query block
+// w / G (16 consecutive queries) of q head g*G + w % G. All waves share the K/V tiles of
+// 64 keys staged in LDS. Per key tile (v_mfma_f32_16x16x32_bf16 throughout):
+//   S^T = K Q^T (A = K rows from LDS, B = Q from registers): row j of the wave lands in
+//     lanes j, j+16, j+32, j+48, each holding 4 of every 16 keys, so the online softmax
+//     needs two cross-lane steps (permlane16 / permlane32 swaps);
 //   P = exp2(S * scale * log2 e - m), split P = P_hi + P_lo (both bf16; the residual of a
 //     single bf16 rounding would break the 2e-2 output bound near zero);
 //   O^T += V^T P^T (A = V^T from LDS, B = P_hi then P_lo straight from the S^T registers):
-//     the keys of a 16-key step are taken in the order the S^T registers hold them, and
-//     V^T is stored in LDS with the same permutation (bits 2 and 3 of the key index
-//     swapped inside each 16-key group), so each operand is one 16-byte LDS read.
+//     the keys of a 32-key step are taken in the order the S^T registers hold them, and
+//     V^T is stored in LDS with the same permutation, so each operand is one 16-byte read.
 // Accumulation is fp32 throughout; the output is O / (l + 1e-10) (the reference's
 // softmax denominator, attention.mojo:151-162).
 //
-// MFMA lane layouts (v_mfma_f32_32x32x16_bf16, checked on the device):
-//   A[i][k]: lane i + 32*(k/8), element k%8;   B[k][j]: lane j + 32*(k/8), element k%8;
-//   C[i][j]: lane j + 32*((i/4)%2), register 4*(i/8) + i%4.
+// MFMA lane layouts (v_mfma_f32_16x16x32_bf16, checked on the device):
+//   A[i][k]: lane i + 16*(k/8), element k%8;   B[k][j]: lane j + 16*(k/8), element k%8;
+//   C[i][j]: lane j + 16*(i/4), register i%4.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -35,17 +34,17 @@ namespace pkv {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 256;             // head_dim of this kernel
 constexpr int kKT = 64;             // keys per tile
-constexpr int kNT = 256;            // four waves
+constexpr int kNT = 512;            // eight waves
 constexpr float kLog2e = 1.4426950408889634f;
 // LDS tiles, double-buffered (bf16 elements). K: [key][256] rows of 512 B whose 16-byte
 // chunk c sits at chunk c ^ (key & 7). V^T: [dim][64 keys] rows of 128 B; keys are
-// permuted inside 16-key groups (bits 2 and 3 swapped) and chunk c of row d sits at
-// chunk c ^ (((d >> 3) ^ d) & 7). Both swizzles keep every group of eight lanes of an
-// operand read or a staging write on distinct banks.
+// permuted inside 32-key groups (vperm) and chunk c of row d sits at chunk
+// c ^ (((d >> 3) ^ d) & 7). Both swizzles keep every group of eight lanes of an operand
+// read or a staging write on distinct banks.
 constexpr int kKTile = kKT * kD;    // elements per K buffer (32 KiB)
 constexpr int kVTile = kD * kKT;    // elements per V^T buffer (32 KiB)
 
@@ -69,8 +68,12 @@ struct PrefillArgs {
     float* out;  // fp32 [rows][Hq][D]
 };
 
-// Position of key k (0..63) of a tile inside its V^T row: bits 2 and 3 swapped.
-__device__ inline int vperm(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+// Position of key k (0..63) of a tile inside its V^T row. Within a 32-key step, lane
+// group grp of the S^T output holds keys 16b + 4grp + r (b = 0, 1; r = 0..3); they sit at
+// positions 8grp + 4b + r, i.e. key bits [4 | 3:2 | 1:0] -> position bits [2 | 4:3 | 1:0].
+__device__ inline int vperm(int k) {
+    return (k & ~31) | (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
+}
 __device__ inline int vswz(int d) { return ((d >> 3) ^ d) & 7; }
 
 __device__ inline float swap32_max(float x) {
@@ -79,6 +82,14 @@ __device__ inline float swap32_max(float x) {
 }
 __device__ inline float swap32_sum(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float swap16_max(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float swap16_sum(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
@@ -99,14 +110,14 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     const int tile = a.qtiles - 1 - (int)blockIdx.x;  // long (late) tiles first
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int half = lane >> 5;
-    const int l32 = lane & 31;
+    const int grp = lane >> 4;  // 16-lane group
+    const int l16 = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = a.q_off[s];
     const int n_q = a.q_off[s + 1] - row0;
     const int q0 = tile * QB;
     const int head = g * G + wave % G;
-    const int qi = q0 + (wave / G) * 32 + l32;  // this lane's query
+    const int qi = q0 + (wave / G) * 16 + l16;  // this lane's query
     const bool live = qi < n_q;
     const int pos0 = a.pos[s];
     auto out_at = [&](int query, int h) -> float* {
@@ -166,38 +177,34 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     };
     // K tile t -> sK[t % 2] straight from global memory into LDS: each wave instruction
     // fills two key rows (1 KiB); lane i loads the global chunk that belongs at chunk
-    // i % 32 of its row under the swizzle.
+    // i % 32 of its row under the swizzle. Eight waves x 4 instructions = 64 rows.
     auto issue_k = [&](int t) {
         uint16_t* dst = sK + (t & 1) * kKTile;
         const int64_t* offs = s_off + (t & 3) * kKT;
 #pragma unroll
-        for (int j = 0; j < kKT / 8; ++j) {  // 8 instructions per wave, 2 rows each
-            const int key = wave * (kKT / 4) + 2 * j + half;
-            const int c = l32 ^ (key & 7);
-            __builtin_amdgcn_global_load_lds(
-                a.k_pool + offs[key] + 8 * c, (lds_void*)(dst + (wave * (kKT / 4) + 2 * j) * kD),
-                16, 0, 0);
+        for (int j = 0; j < 4; ++j) {
+            const int key = wave * 8 + 2 * j + (lane >> 5);
+            const int c = (lane & 31) ^ (key & 7);
+            __builtin_amdgcn_global_load_lds(a.k_pool + offs[key] + 8 * c,
+                                             (lds_void*)(dst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
         }
     };
-    // V tile t: unit i of this thread = 4 consecutive keys x 8 dims, staged through
+    // V tile t: this thread's unit = 4 consecutive keys x 8 dims, staged through
     // registers and written transposed.
     uint4 vreg[4];
-    auto load_v = [&](int t, int i) {
+    const int v_kg = tid >> 5, v_dc = tid & 31;
+    auto load_v = [&](int t) {
         const int64_t* offs = s_off + (t & 3) * kKT;
-        const int u = tid + i * kNT;
-        const int kg = u >> 5, dc = u & 31;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            vreg[j] = *reinterpret_cast<const uint4*>(a.v_pool + offs[4 * kg + j] + 8 * dc);
+            vreg[j] = *reinterpret_cast<const uint4*>(a.v_pool + offs[4 * v_kg + j] + 8 * v_dc);
     };
-    auto store_v = [&](int t, int i) {
+    auto store_v = [&](int t) {
         uint16_t* dst = sV + (t & 1) * kVTile;
-        const int u = tid + i * kNT;
-        const int kg = u >> 5, dc = u & 31;
-        const int kp = vperm(4 * kg);  // 4-aligned: the 4 keys stay contiguous
+        const int kp = vperm(4 * v_kg);  // 4-aligned: the 4 keys stay contiguous
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int d = 8 * dc + e;
+            const int d = 8 * v_dc + e;
             // dim e of keys j = 0..3: 16-bit half (e & 1) of word e / 2 of vreg[j]
             auto word = [&](int j) -> uint32_t {
                 const uint4& r = vreg[j];
@@ -212,183 +219,155 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         }
     };
 
-    // Q as the B operand of S^T: lane holds Q[row][16c + 8*half .. +7] for c = 0..15.
-    bf16x8 qreg[16];
+    // Q as the B operand of S^T: lane holds Q[row][32c + 8*grp .. +7] for c = 0..7.
+    bf16x8 qreg[8];
     {
-        const uint16_t* qp = a.q + ((size_t)(row0 + (live ? qi : 0)) * a.Hq + head) * kD + 8 * half;
+        const uint16_t* qp = a.q + ((size_t)(row0 + (live ? qi : 0)) * a.Hq + head) * kD + 8 * grp;
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            const uint4 v = live ? *reinterpret_cast<const uint4*>(qp + 16 * c) : make_uint4(0, 0, 0, 0);
+        for (int c = 0; c < 8; ++c) {
+            const uint4 v = live ? *reinterpret_cast<const uint4*>(qp + 32 * c) : make_uint4(0, 0, 0, 0);
             qreg[c] = __builtin_bit_cast(bf16x8, v);
         }
     }
 
-    // S^T = K Q^T of tile t (two 32-key sub-tiles), K operands read one step ahead.
-    auto qk = [&](int t, f32x16 (&st)[2]) {
-        const uint16_t* cK = sK + (t & 1) * kKTile;
-        auto kop = [&](int sub, int c) -> bf16x8 {
-            const int key = sub * 32 + l32;
-            const int ch = (2 * c + half) ^ (key & 7);
-            return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cK[key * kD + 8 * ch]));
-        };
+    f32x4 o[16];  // O^T: d-tile u holds dims 16u + 4grp + r of this lane's row
 #pragma unroll
-        for (int v = 0; v < 16; ++v) st[0][v] = st[1][v] = 0.f;
-        bf16x8 ka[4][2];
-#pragma unroll
-        for (int c = 0; c < 3; ++c) { ka[c][0] = kop(0, c); ka[c][1] = kop(1, c); }
-#pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            if (c + 3 < 16) {
-                ka[(c + 3) & 3][0] = kop(0, c + 3);
-                ka[(c + 3) & 3][1] = kop(1, c + 3);
-            }
-            st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c & 3][0], qreg[c], st[0], 0, 0, 0);
-            st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c & 3][1], qreg[c], st[1], 0, 0, 0);
-        }
-    };
-    // Tiles that straddle a row's causal edge or window start get -inf outside
-    // [window_start(qpos), qpos]; lane holds keys kb + 32u + 8(v/4) + 4*half + v%4.
-    // Rows past the chunk are never written, so they need no mask.
-    auto needs_mask = [&](int t) {
-        const int kb = kb0 + t * kKT;
-        return !(kb >= max_ws && kb + kKT - 1 <= min_qpos);
-    };
-    auto mask = [&](int t, f32x16 (&st)[2]) {
-        const int kb = kb0 + t * kKT;
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int kpos = kb + 32 * u + 8 * (v >> 2) + 4 * half + (v & 3);
-                st[u][v] = (kpos <= qpos && kpos >= ws_row) ? st[u][v] : -INFINITY;
-            }
-    };
-
-    f32x16 o[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[u][v] = 0.f;
+    for (int u = 0; u < 16; ++u) o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY;  // reference max (log2 domain) of this lane's row
-    float l = 0.f;        // this lane's share of the running sum (keys of its half)
+    float l = 0.f;        // this lane's share of the running sum (its 16 of every 64 keys)
 
-    // prologue: tiles 0 and 1 of K and tile 0 of V staged, S^T of tile 0 computed
+    // prologue: tile 0 staged, tile 1's and 2's offsets known
     if (tid == 0) *s_bad = 0;
     stage_rows(0);
     stage_rows(1);
     stage_rows(2);
     __syncthreads();
     issue_k(0);
-    if (ntiles > 1) issue_k(1);  // tile 1's offsets exist only if the tile does
-    load_v(0, 0);
-    store_v(0, 0);
-    load_v(0, 1);
-    store_v(0, 1);
+    load_v(0);
+    store_v(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    f32x16 st_cur[2];
-    qk(0, st_cur);
-    if (needs_mask(0)) mask(0, st_cur);
-    __syncthreads();  // every wave has read K tile 0 before tile 2 overwrites it
 
     for (int t = 0; t < ntiles; ++t) {
+        const int kb = kb0 + t * kKT;
         const bool more = t + 1 < ntiles;
-        if (t + 2 < ntiles) issue_k(t + 2);
-        if (more) load_v(t + 1, 0);
+        if (more) {
+            issue_k(t + 1);
+            load_v(t + 1);
+        }
+        const uint16_t* cK = sK + (t & 1) * kKTile;
+        const uint16_t* cV = sV + (t & 1) * kVTile;
 
-        // Block A: S^T of tile t + 1 on the matrix cores while the vector ALUs run the
-        // softmax of tile t (past the last tile the MFMAs read stale LDS; unused).
-        f32x16 st_nxt[2];
-        qk(t + 1, st_nxt);
+        // S^T = K Q^T: four 16-key sub-tiles (independent accumulators), K operands read
+        // one step ahead.
+        f32x4 st[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) st[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto kop = [&](int u, int c) -> bf16x8 {
+            const int key = 16 * u + l16;
+            const int ch = (4 * c + grp) ^ (key & 7);
+            return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cK[key * kD + 8 * ch]));
+        };
+        bf16x8 ka[2][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ka[0][u] = kop(u, 0);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            if (c + 1 < 8) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) ka[(c + 1) & 1][u] = kop(u, c + 1);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[c & 1][u], qreg[c], st[u], 0, 0, 0);
+        }
+        // Tiles that straddle a row's causal edge or window start get -inf outside
+        // [window_start(qpos), qpos]; st[u][r] is key kb + 16u + 4grp + r. Rows past the
+        // chunk are never written, so they need no mask.
+        if (!(kb >= max_ws && kb + kKT - 1 <= min_qpos)) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kpos = kb + 16 * u + 4 * grp + r;
+                    st[u][r] = (kpos <= qpos && kpos >= ws_row) ? st[u][r] : -INFINITY;
+                }
+        }
         float mx = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, st_cur[u][v]);
-        mx = swap32_max(mx) * a.scale_log2;  // scale > 0: the max commutes with it
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[u][r]);
+        mx = swap32_max(swap16_max(mx)) * a.scale_log2;  // scale > 0: the max commutes
         // The reference max m moves only when the tile max exceeds it by more than 8
         // (log2 units): p = exp2(s - m) <= 256 stays exact enough in fp32, the result is
-        // unchanged (softmax does not depend on the reference), and the 128 accumulators
-        // are rescaled only on the rare tiles that move it.
+        // unchanged (softmax does not depend on the reference), and the accumulators are
+        // rescaled only on the rare tiles that move it.
         const bool move = mx > m + 8.f;
         const float m_new = move ? mx : m;
         const float alpha = move ? __builtin_amdgcn_exp2f(m - m_new) : 1.f;  // m = -inf: 0
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
         // v_exp_f32 directly: results below 2^-126 flush to zero, immaterial next to the
-        // row sum (>= 1 for the key that set the reference). P = P_hi + P_lo, both bf16.
-        float lsum[4] = {0.f, 0.f, 0.f, 0.f};
-        bf16x8 ph[4], pl[4];
+        // row sum. P = P_hi + P_lo, both bf16, packed as the B operand of each 32-key step:
+        // element e of step ks is sub-tile 2ks + e/4, register e % 4.
+        float lsum[2] = {0.f, 0.f};
+        bf16x8 ph[2], pl[2];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float x = st_cur[ks >> 1][8 * (ks & 1) + e];
+                const float x = st[2 * ks + (e >> 2)][e & 3];
                 const float p = __builtin_amdgcn_exp2f(fmaf(x, a.scale_log2, -m_use));
-                lsum[e & 3] += p;
+                lsum[e & 1] += p;
                 const __bf16 h = (__bf16)p;
                 ph[ks][e] = h;
                 pl[ks][e] = (__bf16)(p - (float)h);
             }
-        l = l * alpha + ((lsum[0] + lsum[1]) + (lsum[2] + lsum[3]));
+        l = l * alpha + (lsum[0] + lsum[1]);
         m = m_new;
         if (__any(move)) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) o[u][v] *= alpha;
+            for (int u = 0; u < 16; ++u) o[u] *= alpha;
         }
-
-        // Block B: O^T += V^T P^T of tile t, 16 keys per step (the register order of the
-        // S^T output, matched by the V^T permutation); V operands read a step ahead;
-        // tile t + 1's V staged into the other buffer in between.
-        if (more) {
-            store_v(t + 1, 0);
-            load_v(t + 1, 1);
-        }
-        const uint16_t* cV = sV + (t & 1) * kVTile;
+        // O^T += V^T P^T: 16 d-tiles x 2 steps of 32 keys, hi then lo; the V operand of
+        // (step ks, d-tile u) is dims 16u + l16 at positions 32ks + 8grp .. +7.
         auto vop = [&](int ks, int u) -> bf16x8 {
-            const int d = 32 * u + l32;
-            const int ch = (2 * ks + half) ^ vswz(d);
+            const int d = 16 * u + l16;
+            const int ch = (4 * ks + grp) ^ vswz(d);
             return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cV[d * kKT + 8 * ch]));
         };
-        bf16x8 va[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) va[u] = vop(0, u);
+        for (int ks = 0; ks < 2; ++ks) {
+            bf16x8 va[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+            for (int u = 0; u < 4; ++u) va[u] = vop(ks, u);
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u], ph[ks], o[u], 0, 0, 0);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                o[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[u], pl[ks], o[u], 0, 0, 0);
-                if (ks + 1 < 4) va[u] = vop(ks + 1, u);
+            for (int u = 0; u < 16; ++u) {
+                const bf16x8 cur = va[u & 3];
+                if (u + 4 < 16) va[u & 3] = vop(ks, u + 4);
+                o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, ph[ks], o[u], 0, 0, 0);
+                o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, pl[ks], o[u], 0, 0, 0);
             }
         }
-        if (more) store_v(t + 1, 1);
+        if (more) store_v(t + 1);
         stage_rows(t + 3);
-        __builtin_amdgcn_s_waitcnt(0);  // tile t+2's direct-to-LDS K loads have landed
+        __builtin_amdgcn_s_waitcnt(0);  // tile t+1's direct-to-LDS K loads have landed
         __syncthreads();
-        if (more && needs_mask(t + 1)) mask(t + 1, st_nxt);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) st_cur[u] = st_nxt[u];
     }
     const bool bad = *s_bad != 0;
-    const float l_row = swap32_sum(l);
+    const float l_row = swap32_sum(swap16_sum(l));
     const float inv = 1.f / (l_row + 1e-10f);
     if (live) {
-        float* op = out_at(qi, head);
+        float* op = out_at(qi, head) + 4 * grp;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-#pragma unroll
-            for (int mq = 0; mq < 4; ++mq) {
-                float4 v;
-                v.x = bad ? __builtin_nanf("") : o[u][4 * mq + 0] * inv;
-                v.y = bad ? __builtin_nanf("") : o[u][4 * mq + 1] * inv;
-                v.z = bad ? __builtin_nanf("") : o[u][4 * mq + 2] * inv;
-                v.w = bad ? __builtin_nanf("") : o[u][4 * mq + 3] * inv;
-                *reinterpret_cast<float4*>(op + 32 * u + 8 * mq + 4 * half) = v;
-            }
+        for (int u = 0; u < 16; ++u) {
+            float4 v;
+            v.x = bad ? __builtin_nanf("") : o[u][0] * inv;
+            v.y = bad ? __builtin_nanf("") : o[u][1] * inv;
+            v.z = bad ? __builtin_nanf("") : o[u][2] * inv;
+            v.w = bad ? __builtin_nanf("") : o[u][3] * inv;
+            *reinterpret_cast<float4*>(op + 16 * u) = v;
+        }
     }
 }
 
