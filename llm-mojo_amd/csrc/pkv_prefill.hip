@@ -41,10 +41,13 @@ constexpr int kKT = 64;             // keys per tile
 constexpr int kNT = 512;            // eight waves
 constexpr float kLog2e = 1.4426950408889634f;
 // LDS tiles, double-buffered (bf16 elements). K: [key][256] rows of 512 B whose 16-byte
-// chunk c sits at chunk c ^ (key & 7). V^T: [dim][64 keys] rows of 128 B; keys are
-// permuted inside 32-key groups (vperm) and chunk c of row d sits at chunk
-// c ^ (((d >> 3) ^ d) & 7). Both swizzles keep every group of eight lanes of an operand
-// read or a staging write on distinct banks.
+// chunk c sits at chunk c ^ (key & 15): the 16 keys of an operand read land on distinct
+// banks whether the LDS serves 8 lanes over 32 banks or 16 lanes over 64 per cycle.
+// V^T: [dim][64 keys] rows of 128 B; keys are permuted inside 32-key groups (vperm) and
+// chunk c of row d sits at chunk c ^ (((d >> 3) ^ d) & 7), which keeps the operand reads
+// conflict-free; the transposed staging writes (8 bytes per lane) conflict 2-way. A
+// conflict-free staging order (pairing lanes with permlane32 so each writes 16-byte
+// chunks) measured slower: its extra permutes cost more than the conflicts.
 constexpr int kKTile = kKT * kD;    // elements per K buffer (32 KiB)
 constexpr int kVTile = kD * kKT;    // elements per V^T buffer (32 KiB)
 
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int key = wave * 8 + 2 * j + (lane >> 5);
-            const int c = (lane & 31) ^ (key & 7);
+            const int c = (lane & 31) ^ (key & 15);
             __builtin_amdgcn_global_load_lds(a.k_pool + offs[key] + 8 * c,
                                              (lds_void*)(dst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
         }
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         for (int u = 0; u < 4; ++u) st[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         auto kop = [&](int u, int c) -> bf16x8 {
             const int key = 16 * u + l16;
-            const int ch = (4 * c + grp) ^ (key & 7);
+            const int ch = (4 * c + grp) ^ (key & 15);
             return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cK[key * kD + 8 * ch]));
         };
         bf16x8 ka[2][4];
