@@ -26,6 +26,13 @@
  *     and *free_count = num_blocks to start from the reference's fresh state.
  *   - Concurrent calls that touch the same tables / free list / workspace race; order
  *     them on one stream.
+ *   - Ring pools (pkv_params.ring_size > 0; the engine's default for sliding layers,
+ *     model_speculative_moe_batched.mojo:1301-1304, :1440-1442): a layer pool holds
+ *     num_blocks rings of ring_size rows, and token t of a sequence whose ring slot is
+ *     `slot` lives in row slot * ring_size + t % ring_size (ring_row,
+ *     attention.mojo:144-148). In this mode block_tables[s * table_stride] is sequence
+ *     s's ring slot (Sequence.kv_slot, :819) -- an int32 [batch] array with
+ *     table_stride 1 -- and no block is allocated or freed.
  */
 #ifndef PKV_H
 #define PKV_H
@@ -59,7 +66,7 @@ extern "C" {
 typedef struct pkv_params {
     int32_t num_heads;    /* query heads Hq                                            */
     int32_t num_kv_heads; /* KV heads Hkv; Hq % Hkv == 0                               */
-    int32_t head_dim;     /* D: 64, 128, 256 or 512                                    */
+    int32_t head_dim;     /* D: 64, 256 or 512                                         */
     int32_t block_size;   /* tokens per block, a power of two (the engine uses 16)     */
     int32_t num_blocks;   /* physical blocks in each pool (bounds every table entry)   */
     int32_t window;       /* > 0: keys t >= pos - window + 1 (attention.mojo:135-141);
@@ -67,7 +74,8 @@ typedef struct pkv_params {
     float scale;          /* multiplies q.k before the softmax. 1.0f reproduces the
                              reference exactly (Gemma-4 has no softmax scale)          */
     int32_t kv_dtype;     /* PKV_DTYPE_F32 or PKV_DTYPE_BF16 (pool element type)       */
-    int32_t ring_size;    /* must be 0 (paged addressing); ring mode is not built      */
+    int32_t ring_size;    /* 0: paged pools; > 0: ring pools of ring_size rows per slot
+                             (num_blocks then counts ring slots)                      */
     int32_t reserved;     /* must be 0                                                 */
 } pkv_params;
 
@@ -93,7 +101,13 @@ size_t pkv_workspace_size(const pkv_params* p, int32_t batch, int32_t q_len, int
  * longer than max_new (which sizes the grid) changes nothing for s and gives
  * PKV_SEQ_BAD_ARGS. tok_off: int32 [batch + 1] (device).
  * status: int32 [batch] (device), written for every sequence. batch <= 4096.
- * Two launches on `stream`: the allocation (one workgroup) and the row scatter. */
+ * Two launches on `stream`: the allocation (one workgroup) and the row scatter.
+ * Ring pools (ring_size > 0): one launch, the scatter; token p of sequence s goes to
+ * row slot * ring_size + p % ring_size of its ring (the write sites :1996, :2625,
+ * :3111); table_lens, free_list and free_count are not used and may be NULL. Of more
+ * than ring_size new tokens only the last ring_size are written (the rows a serial
+ * pass leaves). A slot outside [0, num_blocks) gives PKV_SEQ_BAD_BLOCK and writes
+ * nothing. Two sequences sharing a slot in one call race. */
 int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
                    int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
                    int32_t* free_list, int32_t* free_count, const int32_t* pos,
@@ -112,7 +126,13 @@ int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool
  * q, out: fp32 [batch][q_len][num_heads][head_dim].
  * max_pos: an upper bound on pos[s] + q_len - 1 over the batch (sizes the grid); a
  * sequence that exceeds it, or whose table holds an entry outside [0, num_blocks),
- * gets NaN outputs. q_len * (num_heads / num_kv_heads) must be <= 16. */
+ * gets NaN outputs. q_len * (num_heads / num_kv_heads) must be <= 16.
+ * Ring pools (ring_size > 0): keys are read from sequence s's ring (execute_attention_
+ * for_token's ring_base = ring_row(kv_slot, ring_size, 0), :648). Every key of the call,
+ * [window_start(pos[s]), pos[s] + q_len - 1], must still be in the ring: a sequence
+ * spanning more than ring_size keys, or whose slot lies outside [0, num_blocks), gets
+ * NaN outputs (the reference aborts, attention.mojo:265-266). With the engine's
+ * ring_size = window + 8 a verify of up to 9 queries fits. */
 int32_t pkv_attend(void* stream, const pkv_params* p, const float* q, const void* k_pool,
                    const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                    const int32_t* pos, int32_t q_len, int32_t batch, int32_t max_pos,
@@ -136,7 +156,10 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
  * {1, 2, 4}. max_q bounds q_off[s+1]-q_off[s] (it sizes the grid) and max_pos bounds
  * pos[s] + its query count - 1; a sequence violating either, or whose table holds an
  * entry outside [0, num_blocks), gets NaN outputs; pos[s] < 0 gives zeros. One launch,
- * no workspace. q_off: int32 [batch + 1] (device). */
+ * no workspace. q_off: int32 [batch + 1] (device). Paged pools only: ring_size > 0
+ * gives PKV_ERR_UNSUPPORTED (a whole chunk appended into a ring would overwrite keys its
+ * own earlier queries attend; ring layers prefill through pkv_attend in chunks of at
+ * most ring_size - window + 1 queries, as the engine's per-token loop does). */
 int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void* k_pool,
                     const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                     const int32_t* pos, const int32_t* q_off, int32_t max_q, int32_t batch,
@@ -152,7 +175,9 @@ int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void
  * modified. status (optional, int32 [batch]) receives PKV_SEQ_* per sequence. If any
  * length or freed entry is out of range, or the pushes would overflow the free list,
  * the call changes nothing and the offending sequences get PKV_SEQ_BAD_BLOCK /
- * PKV_SEQ_FREE_OVERFLOW. batch <= 4096. */
+ * PKV_SEQ_FREE_OVERFLOW. batch <= 4096. Block tables only: ring params (ring_size > 0)
+ * give PKV_ERR_INVALID -- a ring layer keeps rejected draft rows in place, as the
+ * engine does, and they are overwritten by the next appends at those positions. */
 int32_t pkv_rollback(void* stream, const pkv_params* p, int32_t* block_tables,
                      int32_t table_stride, int32_t* table_lens, int32_t* free_list,
                      int32_t* free_count, const int32_t* new_len, int32_t batch,
@@ -163,8 +188,11 @@ int32_t pkv_rollback(void* stream, const pkv_params* p, int32_t* block_tables,
  * pos / block_size + 1 entries), block_size, pos, num_heads, num_kv_heads, head_dim,
  * window, attn_out. The reference's `scores` / `rows` scratch is replaced by
  * `workspace` (pkv_workspace_size(p, 1, 1, pos) bytes); the pool size and element
- * type the GPU needs for bounds checks come in num_blocks / kv_dtype. ring_size must
- * be 0. Softmax scale 1 (the reference has none). */
+ * type the GPU needs for bounds checks come in num_blocks / kv_dtype. ring_size > 0
+ * reads the ring starting at row ring_base (block_table is not read and may be NULL;
+ * num_blocks counts rings): ring_base < 0, a ring ending past num_blocks * ring_size,
+ * or more attended keys than ring_size give PKV_ERR_INVALID (the reference aborts,
+ * attention.mojo:265-266). Softmax scale 1 (the reference has none). */
 int32_t pkv_paged_attention_layer(void* stream, const float* q, const void* k_pool,
                                   const void* v_pool, const int32_t* block_table,
                                   int32_t block_size, int32_t pos, int32_t num_heads,

@@ -158,12 +158,30 @@ struct AttendArgs {
     int32_t num_blocks;
     int32_t window;
     float scale;
+    int32_t ring_size;  // > 0: ring pools (tables hold one ring slot per sequence)
+    int64_t ring_base;  // ring mode, pos == null: first row of the sequence's ring
     int32_t chunk;
     int32_t max_chunks;
     void* part_ml;  // Acc pairs (m, l) per (row, chunk)
     void* part_o;   // Acc [D] per (row, chunk)
     float* out;
 };
+
+// Whether sequence s's keys [lo, hi] can be addressed: within its block table, or in
+// ring mode within the ring (the reference aborts otherwise, attention.mojo:265-266)
+// with a ring slot inside the pool. `rbase` receives the first row of the ring.
+__device__ inline bool keys_addressable(const AttendArgs& a, int s, int lo, int hi,
+                                        int64_t* rbase) {
+    if (a.ring_size <= 0) return hi / a.bs < a.table_stride;
+    if (hi - lo + 1 > a.ring_size) return false;
+    if (!a.pos) {
+        *rbase = a.ring_base;
+        return true;
+    }
+    const int slot = a.tables[(size_t)s * a.table_stride];
+    *rbase = (int64_t)slot * a.ring_size;
+    return slot >= 0 && slot < a.num_blocks;
+}
 
 // Output row r of this workgroup: query j = r / G, head h = g * G + r % G.
 __device__ inline size_t out_index(const AttendArgs& a, int s, int g, int r, int d, int D) {
@@ -228,7 +246,8 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     const int C = a.chunk;
     const int c_lo = lo / C;
     const int nch = hi / C - c_lo + 1;
-    if (hi / a.bs >= a.table_stride || nch > a.max_chunks) {  // contract violated
+    int64_t rbase = 0;
+    if (!keys_addressable(a, s, lo, hi, &rbase) || nch > a.max_chunks) {  // contract violated
         if (c == 0)
             for (int i = tid; i < rows * D; i += kNT)
                 a.out[out_index(a, s, g, i / D, i % D, D)] = __builtin_nanf("");
@@ -241,7 +260,8 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
 
     // Pages of this chunk -> LDS (bounds-checked against the pool).
     const int pg0 = t0 / a.bs;
-    const int npg = t1 / a.bs - pg0 + 1;
+    const int npg = a.ring_size > 0 ? 0 : t1 / a.bs - pg0 + 1;
+    const int r_t0 = a.ring_size > 0 ? t0 % a.ring_size : 0;  // ring row of key t0
     if (tid == 0) s_flag = 0;
     __syncthreads();
     for (int i = tid; i < npg; i += kNT) {
@@ -284,8 +304,13 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     const int bs_mask = a.bs - 1;
     auto row_off = [&](int tok) -> size_t {  // byte offset of token `tok`'s head slice
         const int t = t0 + tok;
-        const int page = s_page[(t >> bs_shift) - pg0];
-        const size_t row = ((size_t)page << bs_shift) + (size_t)(t & bs_mask);
+        size_t row;
+        if (a.ring_size > 0) {
+            row = (size_t)ring_key_row(rbase, r_t0, tok, a.ring_size);
+        } else {
+            const int page = s_page[(t >> bs_shift) - pg0];
+            row = ((size_t)page << bs_shift) + (size_t)(t & bs_mask);
+        }
         return (row * row_elems + head_off) * sizeof(KV);
     };
 
@@ -495,7 +520,8 @@ __global__ __launch_bounds__(kNT) void attend_merge_kernel(AttendArgs a) {
     const int lo = window_start(pos0, a.window);
     const int c_lo = lo / a.chunk;
     const int nch = hi / a.chunk - c_lo + 1;
-    if (hi / a.bs >= a.table_stride || nch > a.max_chunks || nch == 1) return;
+    int64_t rbase = 0;
+    if (!keys_addressable(a, s, lo, hi, &rbase) || nch > a.max_chunks || nch == 1) return;
 
     const Acc* part_o = static_cast<const Acc*>(a.part_o);
     const Acc* part_ml = static_cast<const Acc*>(a.part_ml);
@@ -590,15 +616,19 @@ int32_t dispatch_rows(const AttendArgs& a, int rows, dim3 grid, hipStream_t st) 
     return PKV_OK;
 }
 
+// pos == NULL: one sequence at pos_scalar (whose ring, in ring mode, starts at row
+// ring_base; block_tables is then not read and may be NULL).
 int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const void* k_pool,
                     const void* v_pool, const int32_t* block_tables, int32_t table_stride,
-                    const int32_t* pos, int32_t pos_scalar, int32_t q_len, int32_t batch,
-                    int32_t max_pos, float* out, void* workspace, size_t workspace_bytes) {
+                    const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
+                    int32_t batch, int32_t max_pos, float* out, void* workspace,
+                    size_t workspace_bytes) {
     int32_t rc = validate_params(p);
     if (rc != PKV_OK) return rc;
     if (batch <= 0 || q_len <= 0 || table_stride <= 0 || max_pos < 0)
         return fail(PKV_ERR_INVALID, "batch, q_len, table_stride must be positive, max_pos >= 0");
-    if (!q || !k_pool || !v_pool || !block_tables || !out || !workspace)
+    const bool tables_read = !(p->ring_size > 0 && !pos);
+    if (!q || !k_pool || !v_pool || (tables_read && !block_tables) || !out || !workspace)
         return fail(PKV_ERR_INVALID, "null device pointer");
     const int G = p->num_heads / p->num_kv_heads;
     const int rows = G * q_len;
@@ -607,7 +637,7 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (stream_eligible(p, rows) && workspace_bytes >= stream_layout(p, batch, q_len).total) {
         rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
-                           q_len, batch, max_pos, out, workspace, st);
+                           ring_base, q_len, batch, max_pos, out, workspace, st);
         if (rc != PKV_OK) return rc;
         return check_launch("pkv_attend");
     }
@@ -634,6 +664,8 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     a.num_blocks = p->num_blocks;
     a.window = p->window;
     a.scale = p->scale;
+    a.ring_size = p->ring_size;
+    a.ring_base = ring_base;
     a.chunk = lay.chunk;
     a.max_chunks = lay.max_chunks;
     a.part_ml = ws + lay.ml_off;
@@ -665,7 +697,7 @@ int32_t pkv_attend(void* stream, const pkv_params* p, const float* q, const void
                    float* out, void* workspace, size_t workspace_bytes) {
     pkv::clear_error();
     if (!pos) return pkv::fail(PKV_ERR_INVALID, "pos is NULL");
-    return pkv::attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0,
+    return pkv::attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0, 0,
                             q_len, batch, max_pos, out, workspace, workspace_bytes);
 }
 
@@ -685,7 +717,6 @@ int32_t pkv_paged_attention_layer(void* stream, const float* q, const void* k_po
                                   int32_t num_blocks, int32_t kv_dtype, void* workspace,
                                   size_t workspace_bytes) {
     pkv::clear_error();
-    (void)ring_base;
     pkv_params p{};
     p.num_heads = num_heads;
     p.num_kv_heads = num_kv_heads;
@@ -697,11 +728,24 @@ int32_t pkv_paged_attention_layer(void* stream, const float* q, const void* k_po
     p.kv_dtype = kv_dtype;
     p.ring_size = ring_size;
     if (pos < 0) pos = -1;
+    if (ring_size > 0) {
+        // Ring rows ring_base .. ring_base + ring_size - 1 must lie in the pool of
+        // num_blocks rings, and the attended keys must fit the ring (the reference aborts
+        // otherwise, attention.mojo:265-266). block_table is not read.
+        const int64_t n = pos < 0 ? 0 : (int64_t)pos + 1 - pkv::window_start(pos, window);
+        if (ring_base < 0 || (int64_t)ring_base + ring_size > (int64_t)num_blocks * ring_size)
+            return pkv::fail(PKV_ERR_INVALID, "ring_base outside the pool of num_blocks rings");
+        if (n > ring_size)
+            return pkv::fail(PKV_ERR_INVALID, "ring_size smaller than the attended window");
+        return pkv::attend_impl(stream, &p, q, k_pool, v_pool, nullptr, 1, nullptr, pos,
+                                ring_base, 1, 1, pos < 0 ? 0 : pos, attn_out, workspace,
+                                workspace_bytes);
+    }
     // The table must cover pos (attention.mojo:271); the kernel checks against the
     // stride, so the stride is exactly the entries needed.
     int32_t stride = (pos < 0 ? 0 : pos / (block_size > 0 ? block_size : 1)) + 1;
-    return pkv::attend_impl(stream, &p, q, k_pool, v_pool, block_table, stride, nullptr, pos, 1,
-                            1, pos < 0 ? 0 : pos, attn_out, workspace, workspace_bytes);
+    return pkv::attend_impl(stream, &p, q, k_pool, v_pool, block_table, stride, nullptr, pos, 0,
+                            1, 1, pos < 0 ? 0 : pos, attn_out, workspace, workspace_bytes);
 }
 
 }  // extern "C"

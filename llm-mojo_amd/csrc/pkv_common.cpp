@@ -38,8 +38,7 @@ int32_t validate_params(const pkv_params* p) {
     if (p->num_blocks <= 0) return fail(PKV_ERR_INVALID, "num_blocks must be positive");
     if (p->kv_dtype != PKV_DTYPE_F32 && p->kv_dtype != PKV_DTYPE_BF16)
         return fail(PKV_ERR_INVALID, "kv_dtype must be PKV_DTYPE_F32 or PKV_DTYPE_BF16");
-    if (p->ring_size != 0)
-        return fail(PKV_ERR_UNSUPPORTED, "ring-buffer addressing (ring_size > 0) is not built");
+    if (p->ring_size < 0) return fail(PKV_ERR_INVALID, "ring_size must be >= 0");
     if (p->reserved != 0) return fail(PKV_ERR_INVALID, "reserved must be 0");
     // Row offsets are computed in 64-bit; the element index of a pool must still fit
     // the int64 range comfortably, which any real pool does.
@@ -61,6 +60,10 @@ AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, in
         int64_t span = (int64_t)p->window + q_len - 1;  // keys touched by the queries
         int64_t win = (span + chunk - 1) / chunk + 1;
         if (win < mc) mc = win;
+    }
+    if (p->ring_size > 0) {  // a ring call never spans more than ring_size keys
+        int64_t ring = ((int64_t)p->ring_size + chunk - 1) / chunk + 1;
+        if (ring < mc) mc = ring;
     }
     if (mc < 1) mc = 1;
     L.max_chunks = (int32_t)mc;

@@ -52,15 +52,30 @@ struct StreamLayout {
 StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len);
 // True when the stream kernel covers this geometry (head_dim 256, <= 8 rows per kv head).
 bool stream_eligible(const pkv_params* p, int32_t rows);
+// pos == NULL: one sequence at pos_scalar; in ring mode its ring starts at row
+// ring_base (otherwise ring slot block_tables[s * table_stride] starts at row
+// slot * ring_size).
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
-                      const int32_t* pos, int32_t pos_scalar, int32_t q_len, int32_t batch,
-                      int32_t max_pos, float* out, void* workspace, hipStream_t st);
+                      const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
+                      int32_t batch, int32_t max_pos, float* out, void* workspace,
+                      hipStream_t st);
 
 __host__ __device__ inline int32_t window_start(int32_t pos, int32_t window) {
     if (window <= 0) return 0;
     int32_t s = pos - window + 1;
     return s > 0 ? s : 0;
+}
+
+// Ring mode (ring_size > 0, attention.mojo:144-148, :264-269): key t of a sequence whose
+// ring starts at row `base` lives at row base + t % ring_size. The keys of one call span
+// at most ring_size positions, so from the row r0 = t0 % ring_size of the first key t0
+// every later key t is one subtraction away.
+__host__ __device__ inline int64_t ring_key_row(int64_t base, int32_t r0, int32_t t_minus_t0,
+                                                int32_t ring_size) {
+    int32_t r = r0 + t_minus_t0;
+    if (r >= ring_size) r -= ring_size;
+    return base + r;
 }
 
 // bf16 (stored as uint16) -> fp32, exact.

@@ -392,6 +392,11 @@ int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void
     if (rc != PKV_OK) return rc;
     if (p->kv_dtype != PKV_DTYPE_BF16)
         return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: the MFMA path needs bf16 pools");
+    // A chunk appended whole into a ring would overwrite keys its own earlier queries
+    // attend; ring layers prefill through pkv_attend in chunks of at most
+    // ring_size - window + 1 queries.
+    if (p->ring_size > 0)
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: paged pools only (ring_size 0)");
     if (p->head_dim != kD) return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: head_dim 256 only");
     const int G = p->num_heads / p->num_kv_heads;
     if (G != 1 && G != 2 && G != 4)

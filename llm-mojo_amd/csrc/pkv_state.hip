@@ -16,6 +16,11 @@
 //                                 status is OK.
 // The launch boundary orders the table writes before the scatter's reads, so neither
 // kernel needs a device-scope fence.
+//
+// Ring pools (ring_size > 0) take no blocks: the scatter alone writes token p of a
+// sequence with ring slot `slot` to row slot * ring_size + p % ring_size
+// (ring_row, attention.mojo:144-148, as at the engine's write sites
+// model_speculative_moe_batched.mojo:1996, :2625, :3111).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -90,10 +95,23 @@ struct AppendArgs {
     int32_t batch;
     int32_t* status;
     int32_t bs;
-    int32_t num_blocks;
+    int32_t num_blocks;  // ring mode: ring slots in the pool
+    int32_t ring_size;   // > 0: ring pools; tables[s * table_stride] is s's ring slot
     int32_t row_bytes;  // num_kv_heads * head_dim * element size (multiple of 16)
     int32_t tok_per_wg;
 };
+
+// Ring mode: PKV_SEQ_OK or the reason sequence s writes nothing.
+__device__ inline int ring_append_status(const AppendArgs& a, int s) {
+    const int p = a.pos[s];
+    const int r0 = a.tok_off[s], r1 = a.tok_off[s + 1];
+    const int n = r1 - r0;
+    if (p < 0 || n <= 0) return PKV_SEQ_OK;
+    if (n > a.max_new || r0 < 0 || r1 > a.total_rows) return PKV_SEQ_BAD_ARGS;
+    const int slot = a.tables[(size_t)s * a.table_stride];
+    if (slot < 0 || slot >= a.num_blocks) return PKV_SEQ_BAD_BLOCK;
+    return PKV_SEQ_OK;
+}
 
 // Blocks sequence s needs (>= 0), or a negative PKV_SEQ_* code.
 __device__ inline int append_need(const AppendArgs& a, int s, int len) {
@@ -150,26 +168,43 @@ __global__ __launch_bounds__(kNT) void alloc_kernel(AppendArgs a) {
 
 // grid = (ceil(max_new / tok_per_wg), batch). Copies this workgroup's tokens of one
 // sequence; a table entry outside the pool is skipped and reported as BAD_BLOCK.
+// Ring mode: every workgroup of sequence s derives its status itself (the one with
+// blockIdx.x == 0 stores it), and of n > ring_size new tokens only the last ring_size
+// are written -- the rows a serial pass leaves behind, since each earlier token's row
+// is overwritten within the same call.
 __global__ __launch_bounds__(kNT) void scatter_kernel(AppendArgs a) {
     const int s = blockIdx.y;
     const int tid = threadIdx.x;
-    if (a.status[s] != PKV_SEQ_OK) return;
+    const bool ring = a.ring_size > 0;
+    if (ring) {
+        const int st = ring_append_status(a, s);
+        if (blockIdx.x == 0 && tid == 0) a.status[s] = st;
+        if (st != PKV_SEQ_OK) return;
+    } else if (a.status[s] != PKV_SEQ_OK) {
+        return;
+    }
     const int p0 = a.pos[s];
     const int row0 = a.tok_off[s];
     const int n = a.tok_off[s + 1] - row0;
     if (p0 < 0 || n <= 0) return;
-    const int tok_begin = blockIdx.x * a.tok_per_wg;
-    const int tok_end = min(n, tok_begin + a.tok_per_wg);
+    const int tok_first = ring && n > a.ring_size ? n - a.ring_size : 0;
+    const int tok_begin = max(tok_first, (int)blockIdx.x * a.tok_per_wg);
+    const int tok_end = min(n, (int)blockIdx.x * a.tok_per_wg + a.tok_per_wg);
     const int vec_per_row = a.row_bytes / 16;
     const int32_t* table = a.tables + (size_t)s * a.table_stride;
     for (int b = tok_begin; b < tok_end; ++b) {
         const int p = p0 + b;
-        const int phys = table[p / a.bs];
-        if (phys < 0 || phys >= a.num_blocks) {
-            if (tid == 0) a.status[s] = PKV_SEQ_BAD_BLOCK;
-            continue;
+        size_t row;
+        if (ring) {
+            row = (size_t)table[0] * a.ring_size + (size_t)(p % a.ring_size);
+        } else {
+            const int phys = table[p / a.bs];
+            if (phys < 0 || phys >= a.num_blocks) {
+                if (tid == 0) a.status[s] = PKV_SEQ_BAD_BLOCK;
+                continue;
+            }
+            row = (size_t)phys * a.bs + (size_t)(p % a.bs);
         }
-        const size_t row = (size_t)phys * a.bs + (size_t)(p % a.bs);
         const uint4* ks = reinterpret_cast<const uint4*>(a.k_new + ((size_t)row0 + b) * a.row_bytes);
         const uint4* vs = reinterpret_cast<const uint4*>(a.v_new + ((size_t)row0 + b) * a.row_bytes);
         uint4* kd = reinterpret_cast<uint4*>(a.k_pool + row * a.row_bytes);
@@ -271,8 +306,9 @@ int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool
         return fail(PKV_ERR_INVALID,
                     "batch, max_new, total_rows and table_stride must be positive");
     if (batch > kMaxBatch) return fail(PKV_ERR_UNSUPPORTED, "batch must be <= 4096");
-    if (!k_pool || !v_pool || !block_tables || !table_lens || !free_list || !free_count ||
-        !pos || !tok_off || !k_new || !v_new || !status)
+    const bool ring = p->ring_size > 0;  // ring pools use no block-manager state
+    if (!k_pool || !v_pool || !block_tables || !pos || !tok_off || !k_new || !v_new ||
+        !status || (!ring && (!table_lens || !free_list || !free_count)))
         return fail(PKV_ERR_INVALID, "null device pointer");
     AppendArgs a{};
     a.k_pool = static_cast<char*>(k_pool);
@@ -292,12 +328,13 @@ int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool
     a.status = status;
     a.bs = p->block_size;
     a.num_blocks = p->num_blocks;
+    a.ring_size = p->ring_size;
     a.row_bytes = (int32_t)((size_t)p->num_kv_heads * p->head_dim * kv_elt_bytes(p->kv_dtype));
     // Tokens per scatter workgroup: ~64 KiB of K+V copies each (4 tokens at 8 x 256 fp32).
     const int tpw = (64 * 1024) / (2 * a.row_bytes);
     a.tok_per_wg = tpw < 1 ? 1 : tpw;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(alloc_kernel, dim3(1), dim3(kNT), 0, st, a);
+    if (!ring) hipLaunchKernelGGL(alloc_kernel, dim3(1), dim3(kNT), 0, st, a);
     dim3 grid((max_new + a.tok_per_wg - 1) / a.tok_per_wg, batch);
     hipLaunchKernelGGL(scatter_kernel, grid, dim3(kNT), 0, st, a);
     return check_launch("pkv_append");
@@ -313,6 +350,9 @@ int32_t pkv_rollback(void* stream, const pkv_params* p, int32_t* block_tables,
     if (rc != PKV_OK) return rc;
     if (batch <= 0 || table_stride <= 0)
         return fail(PKV_ERR_INVALID, "batch and table_stride must be positive");
+    if (p->ring_size > 0)
+        return fail(PKV_ERR_INVALID,
+                    "pkv_rollback acts on block tables: pass paged params (ring_size 0)");
     if (batch > kMaxBatch) return fail(PKV_ERR_UNSUPPORTED, "batch must be <= 4096");
     if (!block_tables || !table_lens || !free_list || !free_count || !new_len)
         return fail(PKV_ERR_INVALID, "null device pointer");

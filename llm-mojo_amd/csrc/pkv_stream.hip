@@ -315,6 +315,8 @@ struct StreamArgs {
     int32_t num_blocks;
     int32_t window;
     float scale;
+    int32_t ring_size;  // > 0: ring pools (tables hold one ring slot per sequence)
+    int64_t ring_base;  // ring mode, pos == null: first row of the sequence's ring
     int32_t max_pos;   // last query position the caller sized for
     int32_t batch;
     int32_t nwg;       // P: workgroups along the keys
@@ -351,7 +353,8 @@ __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
 
 // R query rows per wave; WPH waves per KV head split the head's rows (WPH = 2 gives two
 // waves of R rows each, reading the same K/V: the second read of a row slice hits the cache).
-template <int D, typename KV, int R, int WPH>
+// RING: ring pools (key t at row ring_base + t % ring_size) instead of block tables.
+template <int D, typename KV, int R, int WPH, bool RING>
 __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamArgs a) {
     using Acc = typename SKV<KV>::Acc;
     constexpr int kElt = SKV<KV>::kElt;
@@ -379,8 +382,21 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         int n = 0, lo = -1;
         if (p0 >= 0) {
             const int hi = p0 + a.q_len - 1;
-            if (hi <= a.max_pos && (hi >> a.bs_shift) < a.table_stride) {
-                lo = window_start(p0, a.window);
+            const int w0 = window_start(p0, a.window);
+            bool ok = hi <= a.max_pos;
+            if constexpr (RING) {
+                // Every key of the call must still be in the ring (the reference aborts,
+                // attention.mojo:265-266), and the ring slot must lie in the pool.
+                ok = ok && hi - w0 + 1 <= a.ring_size;
+                if (a.pos) {
+                    const int slot = a.tables[(size_t)i * a.table_stride];
+                    ok = ok && slot >= 0 && slot < a.num_blocks;
+                }
+            } else {
+                ok = ok && (hi >> a.bs_shift) < a.table_stride;
+            }
+            if (ok) {
+                lo = w0;
                 n = hi - lo + 1;
             } else {
                 lo = -2;
@@ -477,6 +493,12 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             for (int e = 0; e < EPL; ++e) acc[r][e] = (Acc)0;
 
         const int32_t* trow = a.tables + (size_t)s * a.table_stride;
+        int64_t rbase = 0;  // ring mode: first row of the sequence's ring
+        int r0 = 0;         // ring mode: ring row of key ta
+        if constexpr (RING) {
+            rbase = a.pos ? (int64_t)ufirst(trow[0]) * a.ring_size : a.ring_base;
+            r0 = ta % a.ring_size;
+        }
         const int last_page = (tb - 1) >> a.bs_shift;
         int pgbase = -kSW;  // page index held by lane 0 of vpg
         int vpg = 0;
@@ -484,7 +506,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
 
         for (int t = ta; t < tb; t += U) {
             const int tl = min(t + U - 1, tb - 1);
-            if ((tl >> a.bs_shift) - pgbase >= kSW) {  // page ids of the next 64 pages
+            if (!RING && (tl >> a.bs_shift) - pgbase >= kSW) {  // page ids of the next 64 pages
                 pgbase = t >> a.bs_shift;
                 int b = 0;
                 if (pgbase + lane <= last_page) {
@@ -502,8 +524,13 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int tt = min(t + u, tb - 1);
-                const int page = __builtin_amdgcn_readlane(vpg, (tt >> a.bs_shift) - pgbase);
-                const size_t off = (((size_t)page << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
+                size_t off;
+                if constexpr (RING) {
+                    off = (size_t)ring_key_row(rbase, r0, tt - ta, a.ring_size) * row_bytes;
+                } else {
+                    const int page = __builtin_amdgcn_readlane(vpg, (tt >> a.bs_shift) - pgbase);
+                    off = (((size_t)page << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
+                }
                 load_words<NWD>(uniform_ptr(kbase + off) + lane_off, kw[u]);
                 load_words<NWD>(uniform_ptr(vbase + off) + lane_off, vw[u]);
             }
@@ -700,13 +727,13 @@ int fill_workgroups(const void* fn, int threads, size_t lds) {
     return p;
 }
 
-template <int D, typename KV, int R, int WPH = 1>
-int32_t launch_r(StreamArgs a, hipStream_t st) {
+template <int D, typename KV, int R, int WPH, bool RING>
+int32_t launch_ring(StreamArgs a, hipStream_t st) {
     using Acc = typename SKV<KV>::Acc;
     const int waves = a.Hkv * WPH < kMaxWaves ? a.Hkv * WPH : kMaxWaves;
     const int threads = waves * kSW;
     const size_t lds = (size_t)(2 * a.batch + 1) * sizeof(int);
-    const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH>);
+    const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH, RING>);
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
     // Resident workgroups only: the head groups share the slots, and each workgroup
@@ -714,10 +741,17 @@ int32_t launch_r(StreamArgs a, hipStream_t st) {
     const int groups = (a.Hkv * WPH + kMaxWaves - 1) / kMaxWaves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     dim3 grid(groups, a.nwg);
-    hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH>), grid, dim3(threads), lds, st, a);
+    hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, RING>), grid, dim3(threads), lds, st,
+                       a);
     hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch), dim3(kMergeNT),
                        0, st, a);
     return PKV_OK;
+}
+
+template <int D, typename KV, int R, int WPH = 1>
+int32_t launch_r(StreamArgs a, hipStream_t st) {
+    return a.ring_size > 0 ? launch_ring<D, KV, R, WPH, true>(a, st)
+                           : launch_ring<D, KV, R, WPH, false>(a, st);
 }
 
 }  // namespace
@@ -740,8 +774,9 @@ bool stream_eligible(const pkv_params* p, int32_t rows) {
 
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
-                      const int32_t* pos, int32_t pos_scalar, int32_t q_len, int32_t batch,
-                      int32_t max_pos, float* out, void* workspace, hipStream_t st) {
+                      const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
+                      int32_t batch, int32_t max_pos, float* out, void* workspace,
+                      hipStream_t st) {
     const int G = p->num_heads / p->num_kv_heads;
     const int rows = G * q_len;
     StreamLayout lay = stream_layout(p, batch, q_len);
@@ -762,6 +797,8 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.num_blocks = p->num_blocks;
     a.window = p->window;
     a.scale = p->scale;
+    a.ring_size = p->ring_size;
+    a.ring_base = ring_base;
     a.max_pos = max_pos;
     a.batch = batch;
     a.rows_seq = p->num_heads * q_len;

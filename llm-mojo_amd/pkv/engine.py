@@ -7,6 +7,7 @@ Reference host code (phildrip/llm-mojo, Mojo):
   - pools, one table per sequence shared by all layers   :1427-1451, :1995-1998
   - inline KV append                       :1984-2001 (and the prefill/verify sites)
   - retire (free table ascending)          :3626-3628
+  - ring pools for sliding layers, kv slots :1301-1304, :1440-1442, :2316-2318, :2487-2490
 
 Here the block-manager state (tables, lengths, LIFO free list) lives in device memory
 and every mutation is a libpkv kernel, so a batched decode step never round-trips
@@ -44,13 +45,18 @@ def ring_row(slot: int, ring_size: int, t: int) -> int:
 @dataclass(frozen=True)
 class LayerSpec:
     """Geometry of one attention layer's pools (Gemma-4: sliding 16/8/256 window 1024,
-    global 16/2/512 full causal; the benchmark configs use 16/8/256 for both)."""
+    global 16/2/512 full causal; the benchmark configs use 16/8/256 for both).
+
+    ring_size > 0 keeps the layer's K/V in one ring of ring_size rows per kv slot instead
+    of pages -- the engine's default for sliding layers, ring_size = window + 8
+    (…batched.mojo:1304)."""
 
     num_heads: int = 16
     num_kv_heads: int = 8
     head_dim: int = 256
     window: int = 0
     kv_dtype: str = F32
+    ring_size: int = 0
 
     @property
     def kv_stride(self) -> int:
@@ -59,6 +65,7 @@ class LayerSpec:
 
 def make_params(spec: LayerSpec, block_size: int, num_blocks: int,
                 scale: float = 1.0) -> lib.PkvParams:
+    """pkv_params for one layer; for a ring layer num_blocks is the number of kv slots."""
     p = lib.PkvParams()
     p.num_heads = spec.num_heads
     p.num_kv_heads = spec.num_kv_heads
@@ -68,7 +75,7 @@ def make_params(spec: LayerSpec, block_size: int, num_blocks: int,
     p.window = spec.window
     p.scale = scale
     p.kv_dtype = _DTYPES[spec.kv_dtype]
-    p.ring_size = 0
+    p.ring_size = spec.ring_size
     p.reserved = 0
     return p
 
@@ -87,11 +94,18 @@ class PagedKVCache:
     the BlockManager's LIFO free list.
 
     Pools are zero-filled at creation like the reference's (…batched.mojo:1444-1447);
-    the free list starts as [0 .. num_blocks-1] with every block free (:795-799)."""
+    the free list starts as [0 .. num_blocks-1] with every block free (:795-799).
+
+    Ring layers (LayerSpec.ring_size > 0) hold `num_kv_slots` rings of ring_size rows
+    instead (:1440-1442). A sequence slot takes a kv slot at admission from a LIFO list
+    initialised to [num_kv_slots-1 .. 0] (:2316-2318, :2487-2490) and returns it at
+    retire (:2412-2433); `kv_slots` (device int32 [max_seqs]) holds the assignment and
+    is what ring-layer calls pass as their one-entry "table" per sequence."""
 
     def __init__(self, layers: list[LayerSpec], *, block_size: int, num_blocks: int,
                  max_seqs: int, max_blocks_per_seq: int, max_q_len: int = 1,
-                 max_pos: int | None = None, scale: float = 1.0, stream: hip.Stream | None = None):
+                 max_pos: int | None = None, scale: float = 1.0, stream: hip.Stream | None = None,
+                 num_kv_slots: int | None = None):
         lib.load()
         self.layers = list(layers)
         self.block_size = block_size
@@ -102,12 +116,21 @@ class PagedKVCache:
         self.max_pos = max_pos if max_pos is not None else max_blocks_per_seq * block_size - 1
         self.scale = scale
         self.stream = stream
-        self.params = [make_params(s, block_size, num_blocks, scale) for s in self.layers]
+        self.num_kv_slots = max_seqs if num_kv_slots is None else num_kv_slots
+        self.params = [make_params(s, block_size,
+                                   self.num_kv_slots if s.ring_size > 0 else num_blocks, scale)
+                       for s in self.layers]
         self.k_pools, self.v_pools = [], []
         for s in self.layers:
-            shape = (num_blocks, block_size, s.num_kv_heads, s.head_dim)
+            if s.ring_size > 0:
+                shape = (self.num_kv_slots, s.ring_size, s.num_kv_heads, s.head_dim)
+            else:
+                shape = (num_blocks, block_size, s.num_kv_heads, s.head_dim)
             self.k_pools.append(hip.DeviceArray(shape, _NP_KV[s.kv_dtype], zero=True))
             self.v_pools.append(hip.DeviceArray(shape, _NP_KV[s.kv_dtype], zero=True))
+        self.free_kv_slots = list(range(self.num_kv_slots - 1, -1, -1))
+        self.kv_slot_of = np.full(max_seqs, -1, np.int32)
+        self.kv_slots = hip.DeviceArray.from_numpy(self.kv_slot_of)
         self.tables = hip.DeviceArray((max_seqs, max_blocks_per_seq), np.int32, zero=True)
         self.table_lens = hip.DeviceArray((max_seqs,), np.int32, zero=True)
         self.free_list = hip.DeviceArray.from_numpy(np.arange(num_blocks, dtype=np.int32))
@@ -139,17 +162,44 @@ class PagedKVCache:
             return staging.ptr
         return _ptr(x)
 
+    def _tables_of(self, layer: int):
+        """(tables, stride) a layer's calls pass: block tables, or the kv-slot array."""
+        if self.layers[layer].ring_size > 0:
+            return self.kv_slots.ptr, 1
+        return self.tables.ptr, self.table_stride
+
+    # ------------------------------------------------------------- kv slots
+    def admit(self, slots) -> None:
+        """Gives each sequence slot a kv slot (ring layers) from the LIFO list
+        (…batched.mojo:2487-2490). No-op for slots that already hold one."""
+        for s in slots:
+            if self.kv_slot_of[s] < 0:
+                if not self.free_kv_slots:
+                    raise RuntimeError("no free kv slot (num_kv_slots < active sequences)")
+                self.kv_slot_of[s] = self.free_kv_slots.pop()
+        self.kv_slots.upload_at(0, self.kv_slot_of)
+
+    def _release(self, slots) -> None:
+        """Returns the kv slots of retired sequences (…batched.mojo:2412-2433)."""
+        for s in slots:
+            if self.kv_slot_of[s] >= 0:
+                self.free_kv_slots.append(int(self.kv_slot_of[s]))
+                self.kv_slot_of[s] = -1
+        self.kv_slots.upload_at(0, self.kv_slot_of)
+
     # ------------------------------------------------------------ operators
     def append(self, layer: int, pos, tok_off, k_new, v_new, max_new: int, total_rows: int,
                batch: int | None = None):
         """KV append for `batch` sequence slots (K1). pos: int32[batch]; tok_off:
         int32[batch + 1] (numpy or device) -- slot s appends rows tok_off[s] ..
         tok_off[s+1]-1 of k_new / v_new (device [total_rows][kv_stride], pool dtype) at
-        positions pos[s], pos[s] + 1, ... Returns the device status array (PKV_SEQ_*)."""
+        positions pos[s], pos[s] + 1, ... Returns the device status array (PKV_SEQ_*).
+        A ring layer writes into each sequence's ring and allocates no block."""
         b = batch or self.max_seqs
         p = self.params[layer]
+        tables, stride = self._tables_of(layer)
         lib.call("pkv_append", self._stream(), ctypes.byref(p), self.k_pools[layer].ptr,
-                 self.v_pools[layer].ptr, self.tables.ptr, self.table_stride,
+                 self.v_pools[layer].ptr, tables, stride,
                  self.table_lens.ptr, self.free_list.ptr, self.free_count.ptr,
                  self._ints(pos, self._i32_a, b), self._ints(tok_off, self._i32_b, b + 1),
                  max_new, _ptr(k_new), _ptr(v_new), total_rows, b, self.status.ptr)
@@ -161,9 +211,10 @@ class PagedKVCache:
         sequence s at position pos[s] + j."""
         b = batch or self.max_seqs
         p = self.params[layer]
+        tables, stride = self._tables_of(layer)
         lib.call("pkv_attend", self._stream(), ctypes.byref(p), _ptr(q),
-                 self.k_pools[layer].ptr, self.v_pools[layer].ptr, self.tables.ptr,
-                 self.table_stride, self._ints(pos, self._i32_a, b), q_len, b,
+                 self.k_pools[layer].ptr, self.v_pools[layer].ptr, tables,
+                 stride, self._ints(pos, self._i32_a, b), q_len, b,
                  self.max_pos if max_pos is None else max_pos, _ptr(out), self.workspace.ptr,
                  self.workspace.nbytes)
 
@@ -184,7 +235,9 @@ class PagedKVCache:
         """Truncate tables to ceil(new_len / block_size) blocks, freeing the tail in
         ascending logical order (K5). new_len[s] < 0 leaves slot s alone; 0 retires it."""
         b = batch or self.max_seqs
-        p = self.params[0]
+        p = next((q for q, s in zip(self.params, self.layers) if s.ring_size == 0), None)
+        if p is None:
+            return self.status  # ring layers only: no block tables to truncate
         lib.call("pkv_rollback", self._stream(), ctypes.byref(p), self.tables.ptr,
                  self.table_stride, self.table_lens.ptr, self.free_list.ptr,
                  self.free_count.ptr, self._ints(new_len, self._i32_a, b), b,
@@ -192,10 +245,12 @@ class PagedKVCache:
         return self.status
 
     def retire(self, slots, batch: int | None = None):
-        """Free every block of the given slots (…batched.mojo:3626-3628)."""
+        """Free every block of the given slots (…batched.mojo:3626-3628) and return
+        their kv slots."""
         b = batch or self.max_seqs
         nl = np.full(b, -1, dtype=np.int32)
         nl[list(slots)] = 0
+        self._release(slots)
         return self.rollback(nl, b)
 
     # ---------------------------------------------------------------- state
@@ -213,7 +268,7 @@ class PagedKVCache:
         for a in self.k_pools + self.v_pools:
             a.free()
         for a in (self.tables, self.table_lens, self.free_list, self.free_count, self.status,
-                  self.workspace, self._i32_a, self._i32_b):
+                  self.workspace, self._i32_a, self._i32_b, self.kv_slots):
             a.free()
 
 

@@ -43,12 +43,15 @@ def _L():
             "pkvo_bm_free": (None, [vp, vp, i32]),
             "pkvo_append": (None, [ctypes.c_int, i32, i32, vp, vp, vp, i32, vp, vp, vp, vp, vp,
                                    i32, vp, vp, i32, i32, vp]),
+            "pkvo_ring_append": (None, [ctypes.c_int, i32, i32, i32, vp, vp, vp, i32, vp, vp, i32,
+                                        vp, vp, i32, i32, vp]),
             "pkvo_rollback": (None, [i32, vp, i32, vp, vp, vp, vp, i32]),
             "pkvo_attend": (ctypes.c_int, [ctypes.c_int, i32, i32, i32, i32, i32, f32, vp, vp, vp,
                                            vp, i32, vp, vp, i32, i32, vp, ctypes.c_int,
-                                           ctypes.c_int]),
+                                           ctypes.c_int, i32]),
             "pkvo_attend_f64": (ctypes.c_int, [ctypes.c_int, i32, i32, i32, i32, i32, f32, vp,
-                                               vp, vp, vp, i32, vp, i32, i32, vp, ctypes.c_int]),
+                                               vp, vp, vp, i32, vp, i32, i32, vp, ctypes.c_int,
+                                               i32]),
             "pkvo_max_threads": (ctypes.c_int, []),
         }
         for name, (res, args) in sig.items():
@@ -230,16 +233,51 @@ class CacheState:
         return status
 
     def rollback(self, new_len):
+        """Rollback / retire of the block tables (pkvo_rollback)."""
         new_len = np.ascontiguousarray(new_len, np.int32)
         _L().pkvo_rollback(self.block_size, _p(self.tables), self.table_stride,
                            _p(self.table_lens), _p(self.bm.free_list), _p(self.bm.count),
                            _p(new_len), new_len.size)
 
 
+class RingState:
+    """CPU mirror of ring pools (sliding layers in the engine's default mode,
+    …batched.mojo:1301-1304, :1440-1442): `num_slots` rings of `ring_size` rows per layer,
+    and the kv-slot free list the scheduler pops at admission and pushes at retire
+    (:2316-2318, :2487-2490, :2412-2433)."""
+
+    def __init__(self, num_layers, kv_stride, ring_size, num_slots, dtype=np.float32):
+        self.kv_stride = kv_stride
+        self.ring_size = ring_size
+        self.num_slots = num_slots
+        self.dtype = np.dtype(dtype)
+        n = num_slots * ring_size * kv_stride
+        self.k_pools = [np.zeros(n, self.dtype) for _ in range(num_layers)]
+        self.v_pools = [np.zeros(n, self.dtype) for _ in range(num_layers)]
+
+    def append(self, layer, slots, pos, tok_off, k_new, v_new, max_new):
+        """Ring append (pkvo_ring_append): sequence s writes rows tok_off[s]..tok_off[s+1]-1
+        of k_new / v_new at ring_row(slots[s], ring_size, pos[s] + b)."""
+        slots = np.ascontiguousarray(slots, np.int32)
+        pos = np.ascontiguousarray(pos, np.int32)
+        tok_off = np.ascontiguousarray(tok_off, np.int32)
+        k_new = np.ascontiguousarray(k_new, self.dtype).reshape(-1, self.kv_stride)
+        v_new = np.ascontiguousarray(v_new, self.dtype).reshape(-1, self.kv_stride)
+        batch = pos.size
+        assert tok_off.size == batch + 1 and slots.size == batch
+        status = np.zeros(batch, np.int32)
+        _L().pkvo_ring_append(BF16 if self.dtype == np.uint16 else F32, self.kv_stride,
+                              self.ring_size, self.num_slots, _p(self.k_pools[layer]),
+                              _p(self.v_pools[layer]), _p(slots), 1, _p(pos), _p(tok_off),
+                              max_new, _p(k_new), _p(v_new), k_new.shape[0], batch, _p(status))
+        return status
+
+
 def attend(q, k_pool, v_pool, tables, table_lens, pos, q_len, num_heads, num_kv_heads,
-           head_dim, block_size, window, scale=1.0, nthreads=1, par=0):
+           head_dim, block_size, window, scale=1.0, nthreads=1, par=0, ring_size=0):
     """Batched reference attention: one paged_attention_layer call per query token
-    (…batched.mojo:601-657, :3090-3123). q: [batch, q_len, Hq, D] fp32."""
+    (…batched.mojo:601-657, :3090-3123). q: [batch, q_len, Hq, D] fp32.
+    ring_size > 0: ring pools, tables[s, 0] is sequence s's ring slot (:648)."""
     q = np.ascontiguousarray(q, np.float32)
     tables = np.ascontiguousarray(tables, np.int32)
     table_lens = np.ascontiguousarray(table_lens, np.int32)
@@ -249,14 +287,14 @@ def attend(q, k_pool, v_pool, tables, table_lens, pos, q_len, num_heads, num_kv_
     rc = _L().pkvo_attend(_dtype_of(k_pool), num_heads, num_kv_heads, head_dim, block_size,
                           window, scale, _p(q), _p(k_pool), _p(v_pool), _p(tables),
                           tables.shape[1], _p(table_lens), _p(pos), q_len, batch, _p(out),
-                          nthreads, par)
+                          nthreads, par, ring_size)
     if rc != 0:
         raise RuntimeError(f"pkvo_attend rc={rc}")
     return out
 
 
 def attend_f64(q, k_pool, v_pool, tables, pos, q_len, num_heads, num_kv_heads, head_dim,
-               block_size, window, scale=1.0, nthreads=None):
+               block_size, window, scale=1.0, nthreads=None, ring_size=0):
     """Exact (float64) attention for pkvo_attend's layout (test_attention.mojo:123-163)."""
     q = np.ascontiguousarray(q, np.float32)
     tables = np.ascontiguousarray(tables, np.int32)
@@ -266,7 +304,7 @@ def attend_f64(q, k_pool, v_pool, tables, pos, q_len, num_heads, num_kv_heads, h
     _L().pkvo_attend_f64(_dtype_of(k_pool), num_heads, num_kv_heads, head_dim, block_size,
                          window, scale, _p(q), _p(k_pool), _p(v_pool), _p(tables),
                          tables.shape[1], _p(pos), q_len, batch, _p(out),
-                         max_threads() if nthreads is None else nthreads)
+                         max_threads() if nthreads is None else nthreads, ring_size)
     return out
 
 

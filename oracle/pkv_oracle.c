@@ -22,12 +22,15 @@
  *   pkvo_append                      model_speculative_moe_batched.mojo:1984-2001 (decode),
  *                                    :2513-2523 + :2621-2630 (chunked prefill),
  *                                    :2808-2825 (CPU prefill), :3011-3023 + :3106-3116 (verify)
+ *   pkvo_ring_append                 ring-pool write sites :1996 (decode), :2625 (chunked
+ *                                    prefill), :3111 (verify): row ring_row(kv_slot, ring, p)
  *   pkvo_rollback                    retire :3626-3628 / reset :2424-2439 (ascending free order);
  *                                    truncation after rejected drafts has no reference code and
  *                                    follows the build's definition (keep ceil(len/bs) blocks,
  *                                    free the tail in ascending logical order).
  *   pkvo_attend                      execute_attention_for_token :601-657 / mtp_paged_attention
- *                                    :577-599, one paged_attention_layer call per query token.
+ *                                    :577-599, one paged_attention_layer call per query token
+ *                                    (ring pools: ring_base = ring_row(kv_slot, ring, 0), :648).
  *
  * Bit-level notes (parity of the fp32 attention output is a tolerance, not bits):
  *   - SIMD[f32, 8] accumulation is restated as 8 independent lane accumulators; the
@@ -422,6 +425,42 @@ void pkvo_append(int dtype, int32_t kv_stride, int32_t block_size, void* k_pool,
     }
 }
 
+/* ------------------------------------------------------------ ring append
+ * Ring pools (the engine's default for sliding layers, …batched.mojo:1301-1304,
+ * :1440-1442): sequence s owns ring slot slots[s * slot_stride] of num_slots, and each
+ * new token at position p is copied to row ring_row(slot, ring_size, p)
+ * (attention.mojo:144-148) as at the write sites :1996, :2625, :3111. No block is
+ * allocated. Tokens are written in order, so of more than ring_size new tokens the last
+ * ring_size remain. Status as pkvo_append: -5 for a bad token range, -3 (the C ABI's
+ * PKV_SEQ_BAD_BLOCK) for a slot outside [0, num_slots); neither writes anything. */
+void pkvo_ring_append(int dtype, int32_t kv_stride, int32_t ring_size, int32_t num_slots,
+                      void* k_pool, void* v_pool, const int32_t* slots, int32_t slot_stride,
+                      const int32_t* pos, const int32_t* tok_off, int32_t max_new,
+                      const void* k_new, const void* v_new, int32_t total_rows, int32_t batch,
+                      int32_t* status) {
+    size_t elt = dtype == PKVO_BF16 ? 2 : 4;
+    for (int32_t s = 0; s < batch; ++s) {
+        status[s] = 0;
+        int32_t r0 = tok_off[s], n = tok_off[s + 1] - tok_off[s];
+        if (pos[s] < 0 || n <= 0) continue;
+        if (n > max_new || r0 < 0 || tok_off[s + 1] > total_rows) {
+            status[s] = -5;
+            continue;
+        }
+        int32_t slot = slots[(int64_t)s * slot_stride];
+        if (slot < 0 || slot >= num_slots) {
+            status[s] = -3;
+            continue;
+        }
+        for (int32_t b = 0; b < n; ++b) {
+            int64_t row = pkvo_ring_row(slot, ring_size, (int64_t)pos[s] + b);
+            size_t src = ((size_t)r0 + b) * kv_stride * elt;
+            memcpy((char*)k_pool + row * kv_stride * elt, (const char*)k_new + src, kv_stride * elt);
+            memcpy((char*)v_pool + row * kv_stride * elt, (const char*)v_new + src, kv_stride * elt);
+        }
+    }
+}
+
 /* ------------------------------------------------------- rollback / retire
  * For each sequence s in index order with new_len[s] >= 0: keep
  * ceil(new_len / bs) blocks (never more than it holds) and free the rest in
@@ -452,12 +491,16 @@ void pkvo_rollback(int32_t block_size, int32_t* tables, int32_t table_stride, in
  * par: 0 = serial over sequences, head-pair tasks on `nthreads` threads
  *      (reference-faithful); 1 = sequences spread over `nthreads` threads;
  *      2 = (sequence, query) pairs spread over `nthreads` threads (the calls are
- *      independent once the keys are in the pool; used for long prefill chunks). */
+ *      independent once the keys are in the pool; used for long prefill chunks).
+ * ring_size > 0: ring pools; tables[s * table_stride] is sequence s's ring slot and
+ * the call passes ring_base = slot * ring_size (…batched.mojo:648). Returns -1 when a
+ * query's window exceeds the ring (the reference aborts, attention.mojo:265-266). */
 int pkvo_attend(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                 int32_t block_size, int32_t window, float q_scale, const float* q,
                 const void* k_pool, const void* v_pool, const int32_t* tables,
                 int32_t table_stride, const int32_t* table_lens, const int32_t* pos,
-                int32_t q_len, int32_t batch, float* out, int nthreads, int par) {
+                int32_t q_len, int32_t batch, float* out, int nthreads, int par,
+                int32_t ring_size) {
     int64_t max_n = 0;
     for (int32_t s = 0; s < batch; ++s) {
         int64_t p = (int64_t)pos[s] + q_len;
@@ -489,10 +532,11 @@ int pkvo_attend(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head
                     continue;
                 }
                 for (int64_t i = 0; i < hd; ++i) qs[i] = qj[i] * q_scale;
-                int rc = pkvo_paged_attention_layer(qs, k_pool, v_pool, dtype, tab, table_lens[s],
-                                                    block_size, (int64_t)pos[s] + j, num_heads,
-                                                    num_kv_heads, head_dim, window, scores, rows,
-                                                    oj, 0, 0, inner);
+                int64_t ring_base = ring_size > 0 ? tab[0] * ring_size : 0;
+                int rc = pkvo_paged_attention_layer(
+                    qs, k_pool, v_pool, dtype, tab, ring_size > 0 ? 0 : table_lens[s], block_size,
+                    (int64_t)pos[s] + j, num_heads, num_kv_heads, head_dim, window, scores, rows,
+                    oj, ring_size, ring_base, inner);
                 if (rc != 0) {
 #pragma omp atomic write
                     err = rc;
@@ -518,31 +562,45 @@ int pkvo_max_threads(void) {
 /* ---------------------------------------------- batched float64 attention
  * pkvo_attend's layout and query positions, evaluated with the float64 naive
  * oracle (test_attention.mojo:123-163): the exact attention that both fp32
- * paths approximate. q_scale multiplies q in double. pos[s] < 0 gives zeros. */
+ * paths approximate. q_scale multiplies q in double. pos[s] < 0 gives zeros.
+ * ring_size > 0 (ring pools, tables[s * table_stride] = ring slot): the float64
+ * oracle reads the ring through a one-row-per-block table, tab[t] = ring row of t. */
 int pkvo_attend_f64(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                     int32_t block_size, int32_t window, float q_scale, const float* q,
                     const void* k_pool, const void* v_pool, const int32_t* tables,
                     int32_t table_stride, const int32_t* pos, int32_t q_len, int32_t batch,
-                    double* out, int nthreads) {
+                    double* out, int nthreads, int32_t ring_size) {
     int64_t hd = (int64_t)num_heads * head_dim;
+    int64_t tab_len = table_stride > 0 ? table_stride : 1;
+    if (ring_size > 0)
+        for (int32_t s = 0; s < batch; ++s)
+            if ((int64_t)pos[s] + q_len > tab_len) tab_len = (int64_t)pos[s] + q_len;
 #pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1) if (nthreads > 1)
     {
-        int64_t* tab = (int64_t*)malloc(sizeof(int64_t) * (size_t)(table_stride > 0 ? table_stride : 1));
+        int64_t* tab = (int64_t*)malloc(sizeof(int64_t) * (size_t)tab_len);
         float* qs = (float*)malloc(sizeof(float) * (size_t)hd);
 #pragma omp for schedule(dynamic, 1) collapse(2)
         for (int32_t s = 0; s < batch; ++s) {
             for (int32_t j = 0; j < q_len; ++j) {
-                for (int32_t i = 0; i < table_stride; ++i) tab[i] = tables[(int64_t)s * table_stride + i];
                 const float* qj = q + ((int64_t)s * q_len + j) * hd;
                 double* oj = out + ((int64_t)s * q_len + j) * hd;
                 if (pos[s] < 0) {
                     for (int64_t i = 0; i < hd; ++i) oj[i] = 0.0;
                     continue;
                 }
+                int64_t p = (int64_t)pos[s] + j;
+                int64_t bsz = block_size;
+                if (ring_size > 0) {
+                    int64_t slot = tables[(int64_t)s * table_stride];
+                    for (int64_t t = 0; t <= p; ++t) tab[t] = pkvo_ring_row(slot, ring_size, t);
+                    bsz = 1;
+                } else {
+                    for (int32_t i = 0; i < table_stride; ++i)
+                        tab[i] = tables[(int64_t)s * table_stride + i];
+                }
                 /* q_scale is a power of two in every use, so the fp32 product is exact. */
                 for (int64_t i = 0; i < hd; ++i) qs[i] = qj[i] * q_scale;
-                int64_t p = (int64_t)pos[s] + j;
-                pkvo_attention_f64(qs, k_pool, v_pool, dtype, tab, block_size, p,
+                pkvo_attention_f64(qs, k_pool, v_pool, dtype, tab, bsz, p,
                                    pkvo_window_start(p, window), num_heads, num_kv_heads,
                                    head_dim, oj);
             }

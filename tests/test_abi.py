@@ -51,7 +51,10 @@ def test_workspace_size_is_monotone_and_validates():
     assert 0 < a < b
     w = _params(window=1024)
     assert L.pkv_workspace_size(ctypes.byref(w), 32, 1, 32768) < b  # window bounds the chunks
-    for bad in (_params(num_kv_heads=3), _params(head_dim=100), _params(ring_size=8),
+    ring = _params(window=1024, ring_size=1032)
+    assert 0 < L.pkv_workspace_size(ctypes.byref(ring), 32, 1, 32768) \
+        <= L.pkv_workspace_size(ctypes.byref(w), 32, 1, 32768)
+    for bad in (_params(num_kv_heads=3), _params(head_dim=100), _params(ring_size=-8),
                 _params(kv_dtype=7), _params(block_size=0)):
         assert L.pkv_workspace_size(ctypes.byref(bad), 1, 1, 10) == 0
 
@@ -59,7 +62,7 @@ def test_workspace_size_is_monotone_and_validates():
 @pytest.mark.parametrize("kw,code", [
     (dict(num_kv_heads=3), lib.PKV_ERR_INVALID),
     (dict(head_dim=96), lib.PKV_ERR_UNSUPPORTED),
-    (dict(ring_size=1024), lib.PKV_ERR_UNSUPPORTED),
+    (dict(ring_size=-1), lib.PKV_ERR_INVALID),
 ])
 def test_invalid_params_rejected_before_launch(kw, code):
     L = lib.load()
@@ -85,3 +88,27 @@ def test_null_pointers_and_small_workspace_rejected():
     # verify with too many query rows per kv head (q_len 9 x ratio 2 > 16)
     assert L.pkv_attend(None, ctypes.byref(p), 1, 1, 1, 1, 4, 1, 9, 1, 10, 1, 1, 1 << 30) \
         == lib.PKV_ERR_UNSUPPORTED
+
+
+def test_ring_mode_rejections():
+    """Ring pools: prefill and rollback refuse them, the single-sequence drop-in checks
+    ring_base against the pool and the window against the ring (the reference aborts,
+    attention.mojo:265-266) -- all before any launch."""
+    L = lib.load()
+    ring = _params(window=1024, ring_size=1032, kv_dtype=1, num_blocks=4)
+    assert L.pkv_prefill(None, ctypes.byref(ring), 1, 1, 1, 1, 4, 1, 1, 16, 1, 100, 1) \
+        == lib.PKV_ERR_UNSUPPORTED
+    assert L.pkv_rollback(None, ctypes.byref(ring), 1, 4, 1, 1, 1, 1, 1, None) \
+        == lib.PKV_ERR_INVALID
+    # (stream, q, k, v, table, bs, pos, hq, hkv, d, window, out, ring_size, ring_base,
+    #  num_blocks, dtype, ws, ws_bytes)
+    args = [None, 1, 1, 1, None, 16, 2000, 16, 8, 256, 1024, 1, 1032, 0, 4, 0, 1, 1 << 30]
+    bad_base = list(args)
+    bad_base[13] = 3 * 1032 + 1  # ring would end past the 4 rings of the pool
+    assert L.pkv_paged_attention_layer(*bad_base) == lib.PKV_ERR_INVALID
+    small_ring = list(args)
+    small_ring[12] = 1000  # window 1024 > ring 1000
+    assert L.pkv_paged_attention_layer(*small_ring) == lib.PKV_ERR_INVALID
+    full_causal = list(args)
+    full_causal[10] = 0  # pos 2000 with no window: 2001 keys > ring
+    assert L.pkv_paged_attention_layer(*full_causal) == lib.PKV_ERR_INVALID
