@@ -648,6 +648,111 @@ def bench_config5(args, log):
     return res
 
 
+def bench_producer(args, log):
+    """The producer step fused with the append (pkv_append_qkv: per-head rms_norm of Q / K,
+    rms_norm_noscale of V, RoPE, K/V rows into the pages) at config 4's prefill shape
+    (4 x 2048 tokens, bf16 pools, bf16 Q out; the timed `value`) and config 2's decode shape
+    (32 tokens, fp32 pools and Q). Every table already covers its positions, so a step
+    rewrites the same rows and the allocation pops nothing."""
+    from pkv import BF16, F32, LayerSpec, PagedKVCache, hip, synth
+
+    HQ, HKV, D, BS = 16, 8, 256, 16
+    stream = hip.Stream()
+
+    def shape_leg(B, ntok, pos0, kv_dtype, q_dtype, steps, warmup, seed):
+        span = (int(pos0.max()) + ntok) // BS + 1
+        cache = PagedKVCache([LayerSpec(HQ, HKV, D, kv_dtype=kv_dtype)], block_size=BS,
+                             num_blocks=B * span, max_seqs=B, max_blocks_per_seq=span,
+                             stream=stream)
+        cache.tables.upload(np.arange(B * span, dtype=np.int32).reshape(B, span))
+        cache.table_lens.upload(np.full(B, span, np.int32))
+        cache.free_count.upload(np.zeros(1, np.int32))
+        rows = B * ntok
+        q = synth.normal((rows, HQ * D), seed)
+        k = synth.normal((rows, HKV * D), seed + 1)
+        v = synth.normal((rows, HKV * D), seed + 2)
+        qw = synth.normal((D,), seed + 3)
+        kw = synth.normal((D,), seed + 4)
+        q_out = hip.DeviceArray((rows, HQ * D), np.uint16 if q_dtype == BF16 else np.float32)
+        D_ = hip.DeviceArray.from_numpy
+        dpos = D_(pos0.astype(np.int32))
+        doff = D_((np.arange(B + 1) * ntok).astype(np.int32))
+        ev = _event_pairs(hip, steps)
+
+        def step(i, events=None):
+            if events:
+                events[i][0].record(stream)
+            cache.append_qkv(0, dpos.ptr, doff.ptr, q, k, v, qw, kw, q_out, ntok, rows, False,
+                             q_dtype)
+            if events:
+                events[i][1].record(stream)
+
+        for i in range(warmup):
+            step(i)
+        ms = _timed(hip, stream, steps, step)
+        _timed(hip, stream, steps, lambda i: step(i, ev))
+        dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+        st_ok = bool(np.all(cache.status.numpy() == 0))
+        elt = 2 if kv_dtype == BF16 else 4
+        qelt = 2 if q_dtype == BF16 else 4
+        # read Q/K/V rows (fp32) + 2 weights; write Q out + K/V pool rows; table entries
+        nbytes = rows * ((HQ + 2 * HKV) * D * 4 + HQ * D * qelt + 2 * HKV * D * elt + 4) + 2 * D * 4
+        arrays = dict(q=q, k=k, v=v, qw=qw, kw=kw, q_out=q_out, pos=pos0, cache=cache)
+        return ms, dur, nbytes, st_ok, arrays
+
+    rng = np.random.default_rng(args.seed)
+    prefix = rng.integers(0, 6145, 4)
+    pf_ms, pf_dur, pf_bytes, pf_ok, _ = shape_leg(4, 2048, prefix, BF16, BF16, args.steps,
+                                                  args.warmup, 101)
+    dec_pos = rng.integers(128, 8193, 32)
+    dc_ms, dc_dur, dc_bytes, dc_ok, dec = shape_leg(32, 1, dec_pos, F32, F32, args.steps,
+                                                    args.warmup, 201)
+    roof = _roofline(pf_bytes, pf_dur, "alloc_kernel + qkv_append_kernel<2>")
+    res = _line("producer step (rms_norm + RoPE + KV append) tokens/s, 4 x 2048-token prefill "
+                "chunks", 4 * 2048 * args.steps / (pf_ms / 1e3), "tokens/s", args.steps,
+                args.warmup, pf_ms / args.steps, "f32 in, bf16 out",
+                "pkv_append_qkv at BASELINE config 4's shape: 4 sequences x 2048 tokens at "
+                "prefixes U[0,6144], 16q/8kv/256, block 16, fp32 projections in, bf16 pools "
+                "and bf16 Q out, sliding-layer RoPE", roof,
+                {"status_ok": pf_ok and dc_ok,
+                 "decode_shape": {"tokens": 32, "us_per_call": round(dc_dur * 1e3, 2),
+                                  "ms_per_step_back_to_back": round(dc_ms / args.steps, 4),
+                                  "gbs": round(dc_bytes / (dc_dur / 1e3) / 1e9, 1),
+                                  "bytes_per_call": int(dc_bytes),
+                                  "pools": "fp32"}})
+    if args.cpu_seconds > 0:
+        from oracle import oracle as O
+
+        c = dec["cache"]
+        q, k, v = dec["q"].numpy(), dec["k"].numpy(), dec["v"].numpy()
+        qw, kw = dec["qw"].numpy(), dec["kw"].numpy()
+        got_q = dec["q_out"].numpy()
+        st = O.CacheState(1, HKV * D, BS, c.num_blocks, 32, c.table_stride)
+        st.tables[:] = np.arange(32 * c.table_stride, dtype=np.int32).reshape(32, -1)
+        st.table_lens[:] = c.table_stride
+        st.bm.count[0] = 0
+        off = (np.arange(33)).astype(np.int32)
+        n, el, want_q = 0, 0.0, None
+        while el < args.cpu_seconds and n < 2000:
+            t = time.perf_counter()
+            _, want_q = O.append_qkv(st, 0, dec["pos"], off, q, k, v, qw, kw, 1, HQ, HKV, D,
+                                     False)
+            el += time.perf_counter() - t
+            n += 1
+        ex_q, _, _ = O.producer_f64(dec["pos"], off, q, k, v, qw, kw, 1, HQ, HKV, D, False)
+        res["cpu_baseline"] = {"value": round(32 * n / el, 2), "unit": "tokens/s",
+                               "cores": 1, "kind": "port",
+                               "sample": f"{n} decode-shape calls (32 tokens each) of the "
+                                         f"oracle's per-token rms_norm / apply_rope_qk / "
+                                         f"append, one thread"}
+        res["parity_sample"] = {"q_out_max_rel_err_vs_cpu_fp32":
+                                float(f"{O.max_rel_err(got_q, want_q):.3g}"),
+                                "q_out_max_rel_err_vs_float64":
+                                float(f"{O.max_rel_err(got_q, ex_q):.3g}"),
+                                "cpu_fp32_vs_float64": float(f"{O.max_rel_err(want_q, ex_q):.3g}")}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -661,6 +766,9 @@ def main() -> int:
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="BASELINE.json configuration (2, the default, is the headline)")
+    ap.add_argument("--leg", choices=["producer"], default=None,
+                    help="measure a path beside the configurations instead: 'producer' = "
+                         "pkv_append_qkv (norm + RoPE + append)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -679,6 +787,9 @@ def main() -> int:
     if hip.device_count() < 1:
         print("bench.py needs a GPU: no HIP device visible", file=sys.stderr)
         return 1
+    if args.leg == "producer":
+        print(json.dumps(bench_producer(args, log)), flush=True)
+        return 0
     legs = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}
     if args.config in legs:
         print(json.dumps(legs[args.config](args, log)), flush=True)

@@ -114,6 +114,33 @@ int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool
                    const int32_t* tok_off, int32_t max_new, const void* k_new,
                    const void* v_new, int32_t total_rows, int32_t batch, int32_t* status);
 
+/* K1' -- the producer step before the append, fused with it.
+ * Replaces the engine's per-token sequence rms_norm(q) / rms_norm(k) / rms_norm_noscale(v)
+ * per head + apply_rope_qk + KV write: model_speculative_moe_batched.mojo:1974-2001
+ * (decode), :2612-2630 (chunked prefill), :3099-3116 (verify); rms_norm :857-867,
+ * rms_norm_noscale :870-878, apply_rope_qk attention.mojo:69-132.
+ * Inputs are the projections' fp32 rows, ragged as in pkv_append: row r of q
+ * ([total_rows][num_heads][head_dim]), k and v ([total_rows][num_kv_heads][head_dim])
+ * belongs to token b = r - tok_off[s] of sequence s at position pos[s] + b. Per head:
+ * q = rms_norm(q, q_norm_weight), k = rms_norm(k, k_norm_weight), v = rms_norm_noscale(v)
+ * (x / sqrt(mean(x^2) + 1e-6), times the weight [head_dim]); then Q and K are rotated at
+ * the token's position with apply_rope_qk's constants (is_global != 0: the first
+ * min(64, head_dim/2) pairs, base 1e6 over 512 dims; else all pairs, base 1e4 over 256).
+ * v == NULL means V := K as read, before the norms (global layers, :1962-1964).
+ * The processed Q goes to q_out ([total_rows][num_heads][head_dim] in q_out_dtype: fp32
+ * for pkv_attend, bf16 for pkv_prefill; may alias q when fp32) for every sequence with a
+ * usable token range. K / V rows (rounded to nearest even for bf16 pools) are appended
+ * exactly as pkv_append appends k_new / v_new -- same block allocation, status codes and
+ * ring mode. head_dim 256 or 512. Two launches (one in ring mode). */
+int32_t pkv_append_qkv(void* stream, const pkv_params* p, int32_t is_global, void* k_pool,
+                       void* v_pool, int32_t* block_tables, int32_t table_stride,
+                       int32_t* table_lens, int32_t* free_list, int32_t* free_count,
+                       const int32_t* pos, const int32_t* tok_off, int32_t max_new,
+                       const float* q, const float* k, const float* v,
+                       const float* q_norm_weight, const float* k_norm_weight, void* q_out,
+                       int32_t q_out_dtype, int32_t total_rows, int32_t batch,
+                       int32_t* status);
+
 /* K2 -- split-K paged attention for decode and multi-token verify (fp32 or bf16 pools).
  * Replaces paged_attention_layer + _eval_head_range + _softmax (attention.mojo:151-294)
  * as called per query token by execute_attention_for_token

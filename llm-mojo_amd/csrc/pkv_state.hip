@@ -218,6 +218,241 @@ __global__ __launch_bounds__(kNT) void scatter_kernel(AppendArgs a) {
     }
 }
 
+// ---- fused producer step + append (pkv_append_qkv) --------------------------------
+//
+// A workgroup takes a few tokens of one sequence. Each token's RoPE angles are computed
+// once into LDS; then each wave takes whole heads: a lane holds elements [l*E, l*E+E) of the first
+// half of the head and the same of the second half, so the pair (i, i + D/2) that RoPE
+// rotates sits in one lane and the only cross-lane step is the sum of squares.
+//   Q head:  rms_norm (q_norm weight), RoPE          -> q_out row (fp32 or bf16)
+//   K head:  rms_norm (k_norm weight), RoPE          -> pool row
+//   V head:  rms_norm_noscale (input V, or K as read)  -> pool row
+// Angles: theta_i = pos / base^(2i / rope_dim) in fp32, as the reference computes them.
+// base^(2i / rope_dim) is computed on the host in double and rounded once to fp32, the
+// correctly rounded value (on every exponent the engine uses it equals the C library's
+// powf), and passed in the kernel arguments.
+// Arithmetic: the rotation runs in double -- x * weight (exact in double) times cos / sin
+// of the fp32 angle -- and each output is rounded once. Where a rotation cancels, the
+// reference's fp32 evaluation is several ulps of its terms away from exact, more than the
+// parity bound's 1e-3 floor absorbs; this one stays within an ulp of the result. The
+// RMS factor (sum of squares and 1/sqrt in fp32) scales a whole head, so its rounding
+// stays a relative error of ~1e-7 of each output.
+struct QkvArgs {
+    AppendArgs ap;
+    const float* q;    // [total_rows][Hq][D]
+    const float* k;    // [total_rows][Hkv][D]
+    const float* v;    // [total_rows][Hkv][D], or null: V := K
+    const float* q_w;  // [D]
+    const float* k_w;  // [D]
+    void* q_out;       // [total_rows][Hq][D], fp32 or bf16
+    int32_t q_out_bf16;
+    int32_t kv_bf16;
+    int32_t Hq;
+    int32_t Hkv;
+    int32_t rotary_half;
+    float inv_freq[256];  // base^(2i / rope_dim), i < rotary_half, correctly rounded fp32
+};
+
+__device__ inline uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <int E>
+__device__ inline void store_row(void* base, size_t elem, bool bf16, const float (&x)[E]) {
+    if (bf16) {
+        uint16_t* d = static_cast<uint16_t*>(base) + elem;
+        if constexpr (E == 2) {
+            *reinterpret_cast<uint32_t*>(d) =
+                (uint32_t)f32_to_bf16_rne(x[0]) | ((uint32_t)f32_to_bf16_rne(x[1]) << 16);
+        } else {
+            uint2 w;
+            w.x = (uint32_t)f32_to_bf16_rne(x[0]) | ((uint32_t)f32_to_bf16_rne(x[1]) << 16);
+            w.y = (uint32_t)f32_to_bf16_rne(x[2]) | ((uint32_t)f32_to_bf16_rne(x[3]) << 16);
+            *reinterpret_cast<uint2*>(d) = w;
+        }
+    } else {
+        float* d = static_cast<float*>(base) + elem;
+        if constexpr (E == 2) {
+            *reinterpret_cast<float2*>(d) = make_float2(x[0], x[1]);
+        } else {
+            *reinterpret_cast<float4*>(d) = make_float4(x[0], x[1], x[2], x[3]);
+        }
+    }
+}
+
+template <int E>
+__device__ inline void load_vec(const float* p, float (&x)[E]) {
+    if constexpr (E == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(p);
+        x[0] = v.x;
+        x[1] = v.y;
+    } else {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        x[0] = v.x;
+        x[1] = v.y;
+        x[2] = v.z;
+        x[3] = v.w;
+    }
+}
+
+// E elements per lane per half-head: head_dim D = 128 * E. A workgroup of kQkvWaves
+// waves takes kQkvTokens consecutive tokens of one sequence; their (token, head) items go
+// round-robin to the waves, kQkvItems(E) at a time per wave, and every item of a batch is
+// loaded before any is processed (the first batch before the angle tables are built).
+constexpr int kQkvWaves = 8;
+constexpr int kQkvTokens = 1;
+template <int E>
+constexpr int qkv_items() { return 4; }  // 32 heads (16 q + 8 k + 8 v) over 8 waves
+
+template <int E>
+__global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a) {
+    constexpr int D = 128 * E;
+    constexpr int HALF = D / 2;
+    constexpr int NT = kQkvWaves * kWave;
+    constexpr int IPW = qkv_items<E>();
+    __shared__ double s_cos[kQkvTokens][HALF], s_sin[kQkvTokens][HALF];
+    __shared__ long long s_prow[kQkvTokens];  // pool row of the token's K / V, or -1
+    const AppendArgs& ap = a.ap;
+    const int s = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const bool ring = ap.ring_size > 0;
+    // independent loads first, so they are in flight together
+    const int p0 = ap.pos[s];
+    const int row0 = ap.tok_off[s];
+    const int n = ap.tok_off[s + 1] - row0;
+    int st = ring ? PKV_SEQ_OK : ap.status[s];  // paged: written by alloc_kernel
+    if (ring) {
+        st = ring_append_status(ap, s);
+        if (blockIdx.x == 0 && tid == 0) ap.status[s] = st;
+    }
+    if (st == PKV_SEQ_BAD_ARGS) return;  // token range unusable: nothing is read
+    const int b0 = blockIdx.x * kQkvTokens;  // first token of this workgroup
+    if (p0 < 0 || n <= 0 || b0 >= n) return;
+    const int ntok = min(kQkvTokens, n - b0);
+
+    // Item it = (token t = it / heads, head hh = it % heads); heads are Q, then K, then V
+    // (V := K without v).
+    const int heads = a.Hq + 2 * a.Hkv;
+    const int items = ntok * heads;
+    auto src_of = [&](int it) -> const float* {
+        const int t = it / heads, hh = it % heads;
+        const size_t r = (size_t)row0 + b0 + t;
+        if (hh < a.Hq) return a.q + (r * a.Hq + hh) * D;
+        if (hh < a.Hq + a.Hkv) return a.k + (r * a.Hkv + (hh - a.Hq)) * D;
+        return (a.v ? a.v : a.k) + (r * a.Hkv + (hh - a.Hq - a.Hkv)) * D;
+    };
+    float f1[IPW][E], f2[IPW][E];
+    auto load_batch = [&](int first) {
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) {
+            const int it = first + j * kQkvWaves;
+            if (it < items) {
+                const float* src = src_of(it);
+                load_vec<E>(src + lane * E, f1[j]);
+                load_vec<E>(src + HALF + lane * E, f2[j]);
+            }
+        }
+    };
+    load_batch(wave);
+
+    for (int i = tid; i < ntok * a.rotary_half; i += NT) {
+        const int t = i / a.rotary_half, k = i % a.rotary_half;
+        const float theta = (float)(p0 + b0 + t) / a.inv_freq[k];
+        double sn, c;
+        sincos((double)theta, &sn, &c);
+        s_cos[t][k] = c;
+        s_sin[t][k] = sn;
+    }
+    // K / V rows are written only by an OK sequence, and in ring mode only by the last
+    // ring_size tokens of the call (earlier ones would be overwritten within it).
+    if (tid < ntok) {
+        const int b = b0 + tid, p = p0 + b;
+        long long prow = -1;
+        if (st == PKV_SEQ_OK && !(ring && b < n - ap.ring_size)) {
+            const int32_t* table = ap.tables + (size_t)s * ap.table_stride;
+            if (ring) {
+                prow = (long long)table[0] * ap.ring_size + p % ap.ring_size;
+            } else {
+                const int phys = table[p / ap.bs];
+                if (phys < 0 || phys >= ap.num_blocks) ap.status[s] = PKV_SEQ_BAD_BLOCK;
+                else prow = (long long)phys * ap.bs + p % ap.bs;
+            }
+        }
+        s_prow[tid] = prow;
+    }
+    __syncthreads();
+
+    const size_t kv_row_elems = (size_t)a.Hkv * D;
+    for (int first = wave; first < items; first += kQkvWaves * IPW) {
+        if (first != wave) load_batch(first);
+        // sums of squares of the batch's heads, reduced together (independent chains)
+        float ss[IPW];
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) {
+            ss[j] = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) ss[j] += f1[j][e] * f1[j][e] + f2[j][e] * f2[j][e];
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+            for (int j = 0; j < IPW; ++j) ss[j] += __shfl_xor(ss[j], off);
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) {
+            const int it = first + j * kQkvWaves;
+            if (it >= items) break;
+            const int t = it / heads, hh = it % heads;
+            const int kind = hh < a.Hq ? 0 : (hh < a.Hq + a.Hkv ? 1 : 2);  // q, k, v
+            const long long prow = s_prow[t];
+            if (kind != 0 && prow < 0) continue;
+            const int h = kind == 0 ? hh : (kind == 1 ? hh - a.Hq : hh - a.Hq - a.Hkv);
+            const float inv_rms = 1.0f / sqrtf(ss[j] / (float)D + 1e-6f);
+            float o1[E], o2[E];
+            if (kind < 2) {
+                const float* w = kind == 0 ? a.q_w : a.k_w;
+                float w1[E], w2[E];
+                load_vec<E>(w + lane * E, w1);
+                load_vec<E>(w + HALF + lane * E, w2);
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int i = lane * E + e;
+                    double v1 = (double)f1[j][e] * (double)w1[e];  // exact products
+                    double v2 = (double)f2[j][e] * (double)w2[e];
+                    if (i < a.rotary_half) {
+                        const double c = s_cos[t][i], sn = s_sin[t][i];
+                        const double r1 = v1 * c - v2 * sn;
+                        v2 = v2 * c + v1 * sn;
+                        v1 = r1;
+                    }
+                    o1[e] = (float)(v1 * (double)inv_rms);
+                    o2[e] = (float)(v2 * (double)inv_rms);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    o1[e] = f1[j][e] * inv_rms;
+                    o2[e] = f2[j][e] * inv_rms;
+                }
+            }
+            if (kind == 0) {
+                const size_t off = (((size_t)row0 + b0 + t) * a.Hq + h) * D;
+                store_row<E>(a.q_out, off + lane * E, a.q_out_bf16, o1);
+                store_row<E>(a.q_out, off + HALF + lane * E, a.q_out_bf16, o2);
+            } else {
+                void* pool = kind == 1 ? (void*)ap.k_pool : (void*)ap.v_pool;
+                const size_t off = (size_t)prow * kv_row_elems + (size_t)h * D;
+                store_row<E>(pool, off + lane * E, a.kv_bf16, o1);
+                store_row<E>(pool, off + HALF + lane * E, a.kv_bf16, o2);
+            }
+        }
+    }
+}
+
 struct RollbackArgs {
     int32_t* tables;
     int32_t table_stride;
@@ -338,6 +573,78 @@ int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool
     dim3 grid((max_new + a.tok_per_wg - 1) / a.tok_per_wg, batch);
     hipLaunchKernelGGL(scatter_kernel, grid, dim3(kNT), 0, st, a);
     return check_launch("pkv_append");
+}
+
+int32_t pkv_append_qkv(void* stream, const pkv_params* p, int32_t is_global, void* k_pool,
+                       void* v_pool, int32_t* block_tables, int32_t table_stride,
+                       int32_t* table_lens, int32_t* free_list, int32_t* free_count,
+                       const int32_t* pos, const int32_t* tok_off, int32_t max_new,
+                       const float* q, const float* k, const float* v,
+                       const float* q_norm_weight, const float* k_norm_weight, void* q_out,
+                       int32_t q_out_dtype, int32_t total_rows, int32_t batch,
+                       int32_t* status) {
+    using namespace pkv;
+    clear_error();
+    int32_t rc = validate_params(p);
+    if (rc != PKV_OK) return rc;
+    if (p->head_dim != 256 && p->head_dim != 512)
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_append_qkv: head_dim 256 or 512");
+    if (batch <= 0 || max_new <= 0 || table_stride <= 0 || total_rows <= 0)
+        return fail(PKV_ERR_INVALID,
+                    "batch, max_new, total_rows and table_stride must be positive");
+    if (batch > kMaxBatch) return fail(PKV_ERR_UNSUPPORTED, "batch must be <= 4096");
+    if (q_out_dtype != PKV_DTYPE_F32 && q_out_dtype != PKV_DTYPE_BF16)
+        return fail(PKV_ERR_INVALID, "q_out_dtype must be PKV_DTYPE_F32 or PKV_DTYPE_BF16");
+    const bool ring = p->ring_size > 0;
+    if (!k_pool || !v_pool || !block_tables || !pos || !tok_off || !q || !k ||
+        !q_norm_weight || !k_norm_weight || !q_out || !status ||
+        (!ring && (!table_lens || !free_list || !free_count)))
+        return fail(PKV_ERR_INVALID, "null device pointer");
+    QkvArgs a{};
+    AppendArgs& ap = a.ap;
+    ap.k_pool = static_cast<char*>(k_pool);
+    ap.v_pool = static_cast<char*>(v_pool);
+    ap.tables = block_tables;
+    ap.table_stride = table_stride;
+    ap.table_lens = table_lens;
+    ap.free_list = free_list;
+    ap.free_count = free_count;
+    ap.pos = pos;
+    ap.tok_off = tok_off;
+    ap.max_new = max_new;
+    ap.total_rows = total_rows;
+    ap.batch = batch;
+    ap.status = status;
+    ap.bs = p->block_size;
+    ap.num_blocks = p->num_blocks;
+    ap.ring_size = p->ring_size;
+    ap.row_bytes = (int32_t)((size_t)p->num_kv_heads * p->head_dim * kv_elt_bytes(p->kv_dtype));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.q_w = q_norm_weight;
+    a.k_w = k_norm_weight;
+    a.q_out = q_out;
+    a.q_out_bf16 = q_out_dtype == PKV_DTYPE_BF16;
+    a.kv_bf16 = p->kv_dtype == PKV_DTYPE_BF16;
+    a.Hq = p->num_heads;
+    a.Hkv = p->num_kv_heads;
+    // apply_rope_qk's constants (attention.mojo:78-82): global layers rotate the first
+    // min(64, D/2) pairs with base 1e6 over 512 dims, sliding layers all D/2 pairs with
+    // base 1e4 over 256 dims.
+    const int half = p->head_dim / 2;
+    a.rotary_half = is_global ? (half < 64 ? half : 64) : half;
+    const double base = is_global ? 1000000.0 : 10000.0;
+    const float rope_dim = is_global ? 512.0f : 256.0f;
+    for (int i = 0; i < a.rotary_half; ++i)
+        a.inv_freq[i] = (float)pow(base, (double)((float)(2 * i) / rope_dim));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (!ring) hipLaunchKernelGGL(alloc_kernel, dim3(1), dim3(kNT), 0, st, ap);
+    dim3 grid((max_new + kQkvTokens - 1) / kQkvTokens, batch);
+    const dim3 block(kQkvWaves * kWave);
+    if (p->head_dim == 256) hipLaunchKernelGGL(qkv_append_kernel<2>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(qkv_append_kernel<4>, grid, block, 0, st, a);
+    return check_launch("pkv_append_qkv");
 }
 
 int32_t pkv_rollback(void* stream, const pkv_params* p, int32_t* block_tables,

@@ -205,6 +205,24 @@ class PagedKVCache:
                  max_new, _ptr(k_new), _ptr(v_new), total_rows, b, self.status.ptr)
         return self.status
 
+    def append_qkv(self, layer: int, pos, tok_off, q, k, v, q_norm_w, k_norm_w, q_out,
+                   max_new: int, total_rows: int, is_global: bool, q_out_dtype: str = F32,
+                   batch: int | None = None):
+        """Producer step + append (K1'): per-head rms_norm of Q / K (weights q_norm_w,
+        k_norm_w), rms_norm_noscale of V (v=None: V := K as read), RoPE of Q and K at each
+        token's position, then the K / V rows are appended as in append(). q, k, v, the
+        weights and q_out are device arrays (q_out in q_out_dtype). Returns the status."""
+        b = batch or self.max_seqs
+        p = self.params[layer]
+        tables, stride = self._tables_of(layer)
+        lib.call("pkv_append_qkv", self._stream(), ctypes.byref(p), int(bool(is_global)),
+                 self.k_pools[layer].ptr, self.v_pools[layer].ptr, tables, stride,
+                 self.table_lens.ptr, self.free_list.ptr, self.free_count.ptr,
+                 self._ints(pos, self._i32_a, b), self._ints(tok_off, self._i32_b, b + 1),
+                 max_new, _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm_w), _ptr(k_norm_w),
+                 _ptr(q_out), _DTYPES[q_out_dtype], total_rows, b, self.status.ptr)
+        return self.status
+
     def attend(self, layer: int, q, pos, q_len: int, out, batch: int | None = None,
                max_pos: int | None = None):
         """Paged attention (K2): q/out device fp32 [batch][q_len][Hq][D]; query j of

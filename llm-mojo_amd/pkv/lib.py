@@ -56,6 +56,8 @@ PROTOTYPES = {
     "pkv_prefill": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "pkv_paged_attention_layer": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                                          _i32, _vp, _i32, _i32, _i32, _i32, _vp, _sz]),
+    "pkv_append_qkv": (_i32, [_vp, _PP, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
+                              _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "pkv_last_error": (ctypes.c_char_p, []),
     "pkv_version": (_i32, []),
 }

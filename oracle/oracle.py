@@ -53,6 +53,16 @@ def _L():
                                                vp, vp, vp, i32, vp, i32, i32, vp, ctypes.c_int,
                                                i32]),
             "pkvo_max_threads": (ctypes.c_int, []),
+            "pkvo_rms_norm": (None, [vp, vp, vp, i64]),
+            "pkvo_rms_norm_noscale": (None, [vp, vp, i64]),
+            "pkvo_apply_rope": (None, [vp, i64, i64, i64, ctypes.c_int]),
+            "pkvo_apply_rope_qk": (None, [vp, vp, i64, i64, i64, i64, ctypes.c_int]),
+            "pkvo_ref_apply_rope": (None, [vp, i64, i64, i64, ctypes.c_int]),
+            "pkvo_append_qkv_f64": (None, [i32, i32, i32, ctypes.c_int, vp, vp, i32, vp, vp, vp,
+                                           vp, vp, i32, i32, vp, vp, vp]),
+            "pkvo_append_qkv": (None, [ctypes.c_int, i32, i32, i32, i32, i32, i32, ctypes.c_int,
+                                       vp, vp, vp, i32, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp,
+                                       vp, vp, i32, i32, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -133,6 +143,97 @@ def attention_f64(q, k_pool, v_pool, block_table, block_size, pos, start_t, head
     _L().pkvo_attention_f64(_p(q), _p(k_pool), _p(v_pool), _dtype_of(k_pool), _p(tab),
                             block_size, pos, start_t, heads, kv_heads, head_dim, _p(out))
     return out
+
+
+def rms_norm(x, w) -> np.ndarray:
+    """…batched.mojo:857-867 (one head: len(x) % 8 == 0)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    _L().pkvo_rms_norm(_p(x), _p(w), _p(out), x.size)
+    return out
+
+
+def rms_norm_noscale(x) -> np.ndarray:
+    """…batched.mojo:870-878."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    _L().pkvo_rms_norm_noscale(_p(x), _p(out), x.size)
+    return out
+
+
+def apply_rope(vec, num_heads, head_dim, pos, is_global) -> np.ndarray:
+    """attention.mojo:24-66 (returns a rotated copy)."""
+    v = np.array(vec, np.float32, copy=True).reshape(-1)
+    _L().pkvo_apply_rope(_p(v), num_heads, head_dim, pos, int(is_global))
+    return v
+
+
+def apply_rope_qk(q, k, num_q_heads, num_kv_heads, head_dim, pos, is_global):
+    """attention.mojo:69-132 (returns rotated copies)."""
+    q = np.array(q, np.float32, copy=True).reshape(-1)
+    k = np.array(k, np.float32, copy=True).reshape(-1)
+    _L().pkvo_apply_rope_qk(_p(q), _p(k), num_q_heads, num_kv_heads, head_dim, pos,
+                            int(is_global))
+    return q, k
+
+
+def ref_apply_rope(vec, num_heads, head_dim, pos, is_global) -> np.ndarray:
+    """test_rope_and_parallel_attn.mojo:9-29 (scalar per-element RoPE)."""
+    v = np.array(vec, np.float32, copy=True).reshape(-1)
+    _L().pkvo_ref_apply_rope(_p(v), num_heads, head_dim, pos, int(is_global))
+    return v
+
+
+def append_qkv(state, layer, pos, tok_off, q, k, v, q_norm_w, k_norm_w, max_new, num_heads,
+               num_kv_heads, head_dim, is_global, slots=None):
+    """pkvo_append_qkv on a CacheState (paged) or RingState (ring; `slots` = ring slot of
+    each sequence). Returns (status, q_out); q_out rows of skipped sequences are NaN."""
+    pos = np.ascontiguousarray(pos, np.int32)
+    tok_off = np.ascontiguousarray(tok_off, np.int32)
+    q = np.ascontiguousarray(q, np.float32).reshape(-1, num_heads * head_dim)
+    k = np.ascontiguousarray(k, np.float32).reshape(-1, num_kv_heads * head_dim)
+    vv = None if v is None else np.ascontiguousarray(v, np.float32).reshape(k.shape)
+    qw = np.ascontiguousarray(q_norm_w, np.float32)
+    kw = np.ascontiguousarray(k_norm_w, np.float32)
+    batch = pos.size
+    status = np.zeros(batch, np.int32)
+    q_out = np.full(q.shape, np.nan, np.float32)
+    dt = BF16 if state.dtype == np.uint16 else F32
+    ring = isinstance(state, RingState)
+    if ring:
+        tables = np.ascontiguousarray(slots, np.int32)
+        args = (0, state.ring_size, state.num_slots, _p(tables), 1, None, None, None)
+    else:
+        args = (state.block_size, 0, state.num_blocks, _p(state.tables), state.table_stride,
+                _p(state.table_lens), _p(state.bm.free_list), _p(state.bm.count))
+    bs, ring_size, nblk, tab, stride, lens, fl, fc = args
+    _L().pkvo_append_qkv(dt, num_heads, num_kv_heads, head_dim, bs, ring_size, nblk,
+                         int(is_global), _p(state.k_pools[layer]), _p(state.v_pools[layer]), tab,
+                         stride, lens, fl, fc, _p(pos), _p(tok_off), max_new, _p(q), _p(k),
+                         None if vv is None else _p(vv), _p(qw), _p(kw), _p(q_out), q.shape[0],
+                         batch, _p(status))
+    return status, q_out
+
+
+def producer_f64(pos, tok_off, q, k, v, q_norm_w, k_norm_w, max_new, num_heads, num_kv_heads,
+                 head_dim, is_global):
+    """Exact (float64) processed rows of append_qkv's producer step, in input row layout:
+    (q, k, v) float64 arrays; rows of sequences without a usable token range are NaN."""
+    pos = np.ascontiguousarray(pos, np.int32)
+    tok_off = np.ascontiguousarray(tok_off, np.int32)
+    q = np.ascontiguousarray(q, np.float32).reshape(-1, num_heads * head_dim)
+    k = np.ascontiguousarray(k, np.float32).reshape(-1, num_kv_heads * head_dim)
+    vv = None if v is None else np.ascontiguousarray(v, np.float32).reshape(k.shape)
+    qw = np.ascontiguousarray(q_norm_w, np.float32)
+    kw = np.ascontiguousarray(k_norm_w, np.float32)
+    qo = np.full(q.shape, np.nan)
+    ko = np.full(k.shape, np.nan)
+    vo = np.full(k.shape, np.nan)
+    _L().pkvo_append_qkv_f64(num_heads, num_kv_heads, head_dim, int(is_global), _p(pos),
+                             _p(tok_off), max_new, _p(q), _p(k), None if vv is None else _p(vv),
+                             _p(qw), _p(kw), q.shape[0], pos.size, _p(qo), _p(ko), _p(vo))
+    return qo, ko, vo
 
 
 class Lcg:

@@ -24,6 +24,19 @@
  *                                    :2808-2825 (CPU prefill), :3011-3023 + :3106-3116 (verify)
  *   pkvo_ring_append                 ring-pool write sites :1996 (decode), :2625 (chunked
  *                                    prefill), :3111 (verify): row ring_row(kv_slot, ring, p)
+ *   pkvo_rms_norm / _noscale         model_speculative_moe_batched.mojo:857-867, :870-878
+ *   pkvo_apply_rope                  attention.mojo:24-66
+ *   pkvo_apply_rope_qk               attention.mojo:69-132
+ *   pkvo_ref_apply_rope              test_rope_and_parallel_attn.mojo:9-29 (scalar per-element
+ *                                    restatement the reference asserts bit-exact with the above)
+ *   pkvo_append_qkv                  the producer step before each append site: per-head
+ *                                    rms_norm of Q / K, rms_norm_noscale of V, apply_rope_qk
+ *                                    (:1974-1982 decode, :2612-2619 chunked prefill, :3099-3106
+ *                                    verify; V := K before the norms on global layers,
+ *                                    :1962-1964), then pkvo_append / pkvo_ring_append
+ *   pkvo_append_qkv_f64              the same producer step in float64 (the fp32 angle of the
+ *                                    reference, then exact arithmetic): the exact values both
+ *                                    fp32 evaluations approximate
  *   pkvo_rollback                    retire :3626-3628 / reset :2424-2439 (ascending free order);
  *                                    truncation after rejected drafts has no reference code and
  *                                    follows the build's definition (keep ceil(len/bs) blocks,
@@ -457,6 +470,214 @@ void pkvo_ring_append(int dtype, int32_t kv_stride, int32_t ring_size, int32_t n
             size_t src = ((size_t)r0 + b) * kv_stride * elt;
             memcpy((char*)k_pool + row * kv_stride * elt, (const char*)k_new + src, kv_stride * elt);
             memcpy((char*)v_pool + row * kv_stride * elt, (const char*)v_new + src, kv_stride * elt);
+        }
+    }
+}
+
+/* ----------------------------------------- model_speculative_moe_batched.mojo:857-878
+ * rms_norm: SIMD[f32, 8] sum of squares, reduce_add, 1 / sqrt(ss / size + 1e-6), then
+ * v * inv_rms * weight. rms_norm_noscale omits the weight. size % 8 == 0.           */
+static float sum_squares8(const float* x, int64_t size) {
+    float acc[8] = {0};
+    for (int64_t i = 0; i < size; i += 8)
+        for (int j = 0; j < 8; ++j) acc[j] = acc[j] + x[i + j] * x[i + j];
+    return reduce_add8(acc);
+}
+
+void pkvo_rms_norm(const float* x, const float* w, float* out, int64_t size) {
+    float inv_rms = 1.0f / sqrtf(sum_squares8(x, size) / (float)size + 1e-6f);
+    for (int64_t i = 0; i < size; ++i) out[i] = x[i] * inv_rms * w[i];
+}
+
+void pkvo_rms_norm_noscale(const float* x, float* out, int64_t size) {
+    float inv_rms = 1.0f / sqrtf(sum_squares8(x, size) / (float)size + 1e-6f);
+    for (int64_t i = 0; i < size; ++i) out[i] = x[i] * inv_rms;
+}
+
+/* ------------------------------------------------- attention.mojo:24-132
+ * Rotary embedding of every head of `vec` at position pos. Sliding layers rotate all
+ * head_dim / 2 pairs (i, i + head_dim / 2) with base 1e4 over rope_dim 256; global
+ * layers rotate only the first min(64, head_dim / 2) pairs, base 1e6 over rope_dim 512.
+ * theta_i = pos / base^(2i / rope_dim) in fp32; cos / sin computed once per call.   */
+static int rope_tables(int64_t head_dim, int64_t pos, int is_global, float* cos_arr,
+                       float* sin_arr) {
+    int64_t half_dim = head_dim / 2;
+    int64_t rotary_half = is_global ? (half_dim < 64 ? half_dim : 64) : half_dim;
+    float base = is_global ? 1000000.0f : 10000.0f;
+    float rope_dim = is_global ? 512.0f : 256.0f;
+    float pos_f = (float)pos;
+    for (int64_t i = 0; i < rotary_half; ++i) {
+        float theta = pos_f / powf(base, (float)(2 * i) / rope_dim);
+        cos_arr[i] = cosf(theta);
+        sin_arr[i] = sinf(theta);
+    }
+    return (int)rotary_half;
+}
+
+static void rope_heads(float* vec, int64_t num_heads, int64_t head_dim, int rotary_half,
+                       const float* c, const float* sn) {
+    int64_t half_dim = head_dim / 2;
+    for (int64_t h = 0; h < num_heads; ++h) {
+        float* v1 = vec + h * head_dim;
+        float* v2 = v1 + half_dim;
+        for (int i = 0; i < rotary_half; ++i) {
+            float a = v1[i], b = v2[i];
+            v1[i] = a * c[i] - b * sn[i];
+            v2[i] = b * c[i] + a * sn[i];
+        }
+    }
+}
+
+void pkvo_apply_rope(float* vec, int64_t num_heads, int64_t head_dim, int64_t pos,
+                     int is_global) {
+    float c[256], sn[256];
+    int rh = rope_tables(head_dim, pos, is_global, c, sn);
+    rope_heads(vec, num_heads, head_dim, rh, c, sn);
+}
+
+void pkvo_apply_rope_qk(float* q, float* k, int64_t num_q_heads, int64_t num_kv_heads,
+                        int64_t head_dim, int64_t pos, int is_global) {
+    float c[256], sn[256];
+    int rh = rope_tables(head_dim, pos, is_global, c, sn);
+    rope_heads(q, num_q_heads, head_dim, rh, c, sn);
+    rope_heads(k, num_kv_heads, head_dim, rh, c, sn);
+}
+
+/* ------------------------------ test_rope_and_parallel_attn.mojo:9-29
+ * The reference's scalar RoPE: theta per element (0 for global pairs >= 64).       */
+void pkvo_ref_apply_rope(float* vec, int64_t num_heads, int64_t head_dim, int64_t pos,
+                         int is_global) {
+    int64_t half_dim = head_dim / 2;
+    float base = is_global ? 1000000.0f : 10000.0f;
+    int64_t rope_dim = is_global ? 512 : 256;
+    for (int64_t h = 0; h < num_heads; ++h) {
+        int64_t off = h * head_dim;
+        for (int64_t i = 0; i < half_dim; ++i) {
+            float theta = 0.0f;
+            if (!is_global || i < 64)
+                theta = (float)pos / powf(base, (float)(2 * i) / (float)rope_dim);
+            float ct = cosf(theta), st = sinf(theta);
+            float v1 = vec[off + i], v2 = vec[off + half_dim + i];
+            vec[off + i] = v1 * ct - v2 * st;
+            vec[off + half_dim + i] = v2 * ct + v1 * st;
+        }
+    }
+}
+
+/* --------------------------------------------------- fused producer + append
+ * The engine's per-token producer step before each KV write (decode :1974-1982,
+ * chunked prefill :2612-2619, verify :3099-3106): per head, q = rms_norm(q, q_norm_w),
+ * k = rms_norm(k, k_norm_w), v = rms_norm_noscale(v); then apply_rope_qk(q, k) at the
+ * token's position. v == NULL gives V := K as read, before any norm (global layers,
+ * attention_k_eq_v, :1962-1964). Rows are ragged as in pkvo_append: sequence s owns
+ * input rows tok_off[s] .. tok_off[s+1]-1 at positions pos[s], pos[s] + 1, ...
+ * q_out (fp32 [total_rows][Hq][D]) receives the processed Q of every sequence with a
+ * valid token range (pos >= 0, 0 < n <= max_new, rows inside total_rows); rows of other
+ * sequences are not written. The processed K / V rows (rounded to bf16 for bf16 pools)
+ * then go through pkvo_append (ring_size == 0) or pkvo_ring_append (ring_size > 0, where
+ * tables[s * table_stride] is the ring slot and num_blocks counts ring slots).     */
+void pkvo_append_qkv(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t block_size, int32_t ring_size, int32_t num_blocks, int is_global,
+                     void* k_pool, void* v_pool, int32_t* tables, int32_t table_stride,
+                     int32_t* table_lens, int32_t* free_list, int32_t* free_count,
+                     const int32_t* pos, const int32_t* tok_off, int32_t max_new, const float* q,
+                     const float* k, const float* v, const float* q_norm_w,
+                     const float* k_norm_w, float* q_out, int32_t total_rows, int32_t batch,
+                     int32_t* status) {
+    int64_t D = head_dim, qs = (int64_t)num_heads * D, ks = (int64_t)num_kv_heads * D;
+    size_t elt = dtype == PKVO_BF16 ? 2 : 4;
+    float* kn = (float*)calloc((size_t)(total_rows > 0 ? total_rows : 1) * ks, sizeof(float));
+    float* vn = (float*)calloc((size_t)(total_rows > 0 ? total_rows : 1) * ks, sizeof(float));
+    void* kc = calloc((size_t)(total_rows > 0 ? total_rows : 1) * ks, elt);
+    void* vc = calloc((size_t)(total_rows > 0 ? total_rows : 1) * ks, elt);
+    for (int32_t s = 0; s < batch; ++s) {
+        int32_t r0 = tok_off[s], n = tok_off[s + 1] - tok_off[s];
+        if (pos[s] < 0 || n <= 0 || n > max_new || r0 < 0 || tok_off[s + 1] > total_rows)
+            continue;
+        for (int32_t b = 0; b < n; ++b) {
+            int64_t r = (int64_t)r0 + b;
+            float* qo = q_out + r * qs;
+            float* ko = kn + r * ks;
+            float* vo = vn + r * ks;
+            const float* vsrc = v ? v + r * ks : k + r * ks;
+            for (int64_t h = 0; h < num_heads; ++h)
+                pkvo_rms_norm(q + r * qs + h * D, q_norm_w, qo + h * D, D);
+            for (int64_t h = 0; h < num_kv_heads; ++h) {
+                pkvo_rms_norm(k + r * ks + h * D, k_norm_w, ko + h * D, D);
+                pkvo_rms_norm_noscale(vsrc + h * D, vo + h * D, D);
+            }
+            pkvo_apply_rope_qk(qo, ko, num_heads, num_kv_heads, D, (int64_t)pos[s] + b,
+                               is_global);
+        }
+    }
+    int64_t nall = (int64_t)(total_rows > 0 ? total_rows : 0) * ks;
+    if (dtype == PKVO_BF16) {
+        pkvo_f32_to_bf16_array(kn, (uint16_t*)kc, nall);
+        pkvo_f32_to_bf16_array(vn, (uint16_t*)vc, nall);
+    } else {
+        memcpy(kc, kn, (size_t)nall * 4);
+        memcpy(vc, vn, (size_t)nall * 4);
+    }
+    if (ring_size > 0)
+        pkvo_ring_append(dtype, (int32_t)ks, ring_size, num_blocks, k_pool, v_pool, tables,
+                         table_stride, pos, tok_off, max_new, kc, vc, total_rows, batch, status);
+    else
+        pkvo_append(dtype, (int32_t)ks, block_size, k_pool, v_pool, tables, table_stride,
+                    table_lens, free_list, free_count, pos, tok_off, max_new, kc, vc, total_rows,
+                    batch, status);
+    free(kn);
+    free(vn);
+    free(kc);
+    free(vc);
+}
+
+/* ------------------------------------------- float64 producer step
+ * pkvo_append_qkv's processed rows in float64: rms_norm / rms_norm_noscale and the
+ * rotation evaluated exactly (double) from the reference's fp32 angles
+ * theta_i = (float)pos / powf(base, 2i / rope_dim). Writes q_out / k_out / v_out
+ * (double, input row layout) for every sequence with a usable token range.       */
+void pkvo_append_qkv_f64(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                         int is_global, const int32_t* pos, const int32_t* tok_off,
+                         int32_t max_new, const float* q, const float* k, const float* v,
+                         const float* q_norm_w, const float* k_norm_w, int32_t total_rows,
+                         int32_t batch, double* q_out, double* k_out, double* v_out) {
+    int64_t D = head_dim, half = D / 2;
+    int64_t rotary_half = is_global ? (half < 64 ? half : 64) : half;
+    float base = is_global ? 1000000.0f : 10000.0f;
+    float rope_dim = is_global ? 512.0f : 256.0f;
+    for (int32_t s = 0; s < batch; ++s) {
+        int32_t r0 = tok_off[s], n = tok_off[s + 1] - tok_off[s];
+        if (pos[s] < 0 || n <= 0 || n > max_new || r0 < 0 || tok_off[s + 1] > total_rows)
+            continue;
+        for (int32_t b = 0; b < n; ++b) {
+            int64_t r = (int64_t)r0 + b;
+            float pos_f = (float)((int64_t)pos[s] + b);
+            double c[256], sn[256];
+            for (int64_t i = 0; i < rotary_half; ++i) {
+                float theta = pos_f / powf(base, (float)(2 * i) / rope_dim);
+                c[i] = cos((double)theta);
+                sn[i] = sin((double)theta);
+            }
+            for (int kind = 0; kind < 3; ++kind) {
+                int64_t heads = kind == 0 ? num_heads : num_kv_heads;
+                const float* src = kind == 0 ? q : (kind == 1 || !v ? k : v);
+                const float* w = kind == 0 ? q_norm_w : (kind == 1 ? k_norm_w : NULL);
+                double* dst = kind == 0 ? q_out : (kind == 1 ? k_out : v_out);
+                for (int64_t h = 0; h < heads; ++h) {
+                    const float* x = src + (r * heads + h) * D;
+                    double* y = dst + (r * heads + h) * D;
+                    double ss = 0.0;
+                    for (int64_t d = 0; d < D; ++d) ss += (double)x[d] * (double)x[d];
+                    double inv = 1.0 / sqrt(ss / (double)D + (double)1e-6f);
+                    for (int64_t d = 0; d < D; ++d) y[d] = (double)x[d] * inv * (w ? (double)w[d] : 1.0);
+                    if (kind == 2) continue;
+                    for (int64_t i = 0; i < rotary_half; ++i) {
+                        double a = y[i], bb = y[half + i];
+                        y[i] = a * c[i] - bb * sn[i];
+                        y[half + i] = bb * c[i] + a * sn[i];
+                    }
+                }
+            }
         }
     }
 }
