@@ -753,6 +753,106 @@ def bench_producer(args, log):
     return res
 
 
+def bench_lsa(args, log):
+    """LSA sparse attention (pkv_attend_sparse) on the model's global-layer geometry (16 q /
+    2 kv heads, head_dim 512, fp32 pools) for 32 sequences at contexts U[128, 8192]. Each
+    key list comes from lsa_expand_buckets with the engine's defaults
+    (…batched.mojo:1261-1264: top_k 256 from 20 picked buckets of up to 32 members, window
+    128, 4 sinks), so a query attends about 390 keys scattered over its context."""
+    from pkv import LayerSpec, PagedKVCache, hip, lsa_expand_buckets, synth
+
+    HQ, HKV, D, BS, B = 16, 2, 512, 16, 32
+    TOP_K, PICK, CAP, WINDOW, SINKS = 256, 20, 32, 128, 4
+    rng = np.random.default_rng(args.seed)
+    ctx = rng.integers(128, 8193, B)
+    blocks = (ctx + BS) // BS
+    nb = int(blocks.sum())
+    stride = int(blocks.max())
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((B, stride), np.int32)
+    lists, off = [], [0]
+    o = 0
+    for s in range(B):
+        tables[s, :blocks[s]] = perm[o:o + blocks[s]]
+        o += blocks[s]
+        pos = int(ctx[s])
+        nbk = pos // 16 + 1  # buckets of the closed blocks
+        sizes = np.minimum(rng.integers(8, CAP + 1, nbk), pos + 1)
+        members = np.zeros((nbk, CAP), np.int64)
+        for b in range(nbk):
+            members[b, :sizes[b]] = rng.choice(pos + 1, sizes[b], replace=False)
+        picked = rng.choice(nbk, min(PICK, nbk), replace=False)
+        sel = lsa_expand_buckets(picked, sizes, members, pos, TOP_K, SINKS, WINDOW)
+        lists.append(sel)
+        off.append(off[-1] + sel.size)
+    keys = np.concatenate(lists).astype(np.int32)
+    off = np.asarray(off, np.int32)
+    n_keys = np.diff(off)
+    max_keys = int(n_keys.max())
+    stream = hip.Stream()
+    cache = PagedKVCache([LayerSpec(HQ, HKV, D)], block_size=BS, num_blocks=nb, max_seqs=B,
+                         max_blocks_per_seq=stride, scale=0.0625, stream=stream)
+    cache.tables.upload(tables)
+    synth.fill_normal(cache.k_pools[0], 301)
+    synth.fill_normal(cache.v_pools[0], 302)
+    q = synth.normal((B, HQ, D), 303)
+    dkeys, doff = hip.DeviceArray.from_numpy(keys), hip.DeviceArray.from_numpy(off)
+    out = hip.DeviceArray((B, HQ, D), np.float32)
+    ev = _event_pairs(hip, args.steps)
+
+    def step(i, events=None):
+        if events:
+            events[i][0].record(stream)
+        cache.attend_sparse(0, q, dkeys, doff.ptr, max_keys, out)
+        if events:
+            events[i][1].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    ms = _timed(hip, stream, args.steps, step)
+    _timed(hip, stream, args.steps, lambda i: step(i, ev))
+    dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    got = out.numpy()
+    # each listed key's K and V slices once, Q in / O out, key list and table entries
+    nbytes = int(n_keys.sum()) * (2 * HKV * D * 4 + 8) + B * 2 * HQ * D * 4
+    res = _line("LSA sparse paged attention tokens/s (32 sequences, ~390-key lists, 16q/2kv/512)",
+                B * args.steps / (ms / 1e3), "tokens/s", args.steps, args.warmup,
+                ms / args.steps, "f32",
+                "LSA decode step on the global-layer geometry: 32 sequences, contexts U[128,8192], "
+                "key lists from lsa_expand_buckets (top_k 256 of 20 buckets, window 128, "
+                "4 sinks), 16q/2kv/512, block 16, fp32 KV",
+                _roofline(nbytes, dur, "stream_attend_kernel<512, float, 2, 4, sparse> + "
+                                       "stream_merge_kernel<512, double>"),
+                {"keys_per_sequence_mean": round(float(n_keys.mean()), 1),
+                 "max_keys": max_keys})
+    if args.cpu_seconds > 0:
+        from oracle import oracle as O
+
+        k = cache.k_pools[0].numpy().reshape(-1)
+        v = cache.v_pools[0].numpy().reshape(-1)
+        qh = q.numpy()
+        n, el, refs = 0, 0.0, []
+        while el < args.cpu_seconds and n < B:
+            t = time.perf_counter()
+            refs.append(O.attend_sparse(qh[n:n + 1], k, v, tables[n:n + 1], keys[off[n]:off[n + 1]],
+                                        np.array([0, n_keys[n]], np.int32), HQ, HKV, D, BS,
+                                        scale=0.0625, nthreads=args.cpu_threads))
+            el += time.perf_counter() - t
+            n += 1
+        exact = O.attend_sparse_f64(qh[:n], k, v, tables[:n], keys[:off[n]], off[:n + 1], HQ,
+                                    HKV, D, BS, scale=0.0625)
+        ref = np.concatenate(refs)
+        res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s",
+                               "cores": args.cpu_threads, "kind": "port",
+                               "sample": f"first {n} sequences, one lsa_sparse_paged_attention "
+                                         f"call each on {args.cpu_threads} head-pair threads"}
+        res["parity_sample"] = {"sequences": n,
+                                "max_rel_err_vs_cpu_fp32": float(f"{O.max_rel_err(got[:n], ref):.3g}"),
+                                "max_rel_err_vs_float64": float(f"{O.max_rel_err(got[:n], exact):.3g}"),
+                                "cpu_fp32_vs_float64": float(f"{O.max_rel_err(ref, exact):.3g}")}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -766,9 +866,9 @@ def main() -> int:
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="BASELINE.json configuration (2, the default, is the headline)")
-    ap.add_argument("--leg", choices=["producer"], default=None,
+    ap.add_argument("--leg", choices=["producer", "lsa"], default=None,
                     help="measure a path beside the configurations instead: 'producer' = "
-                         "pkv_append_qkv (norm + RoPE + append)")
+                         "pkv_append_qkv (norm + RoPE + append), 'lsa' = pkv_attend_sparse")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -787,8 +887,9 @@ def main() -> int:
     if hip.device_count() < 1:
         print("bench.py needs a GPU: no HIP device visible", file=sys.stderr)
         return 1
-    if args.leg == "producer":
-        print(json.dumps(bench_producer(args, log)), flush=True)
+    if args.leg is not None:
+        leg = {"producer": bench_producer, "lsa": bench_lsa}[args.leg]
+        print(json.dumps(leg(args, log)), flush=True)
         return 0
     legs = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}
     if args.config in legs:

@@ -171,6 +171,25 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
                    const int32_t* pos, int32_t batch, int32_t max_pos, float* out,
                    void* workspace, size_t workspace_bytes);
 
+/* Bytes of workspace pkv_attend_sparse needs for `batch` key lists of at most max_keys
+ * entries. 0 on invalid params. */
+size_t pkv_sparse_workspace_size(const pkv_params* p, int32_t batch, int32_t max_keys);
+
+/* K2' -- sparse paged attention over explicit key lists (LSA on global layers).
+ * Replaces lsa_sparse_paged_attention (lsa_core.mojo:630-680) as called by
+ * execute_attention_for_token's LSA branch (model_speculative_moe_batched.mojo:630-646)
+ * with the key list from LSALayerIndex.expand_buckets (lsa_core.mojo:573-604).
+ * Sequence s (one query: q, out fp32 [batch][num_heads][head_dim]) attends exactly the key
+ * positions keys[key_off[s] .. key_off[s+1]) of its own table -- softmax(scale * q.k) . V
+ * over that set, with the reference's sum + 1e-10 denominator; p->window is ignored. An
+ * empty list gives zeros (lsa_core.mojo:651-655). A list longer than max_keys, or a key
+ * whose block lies outside the table or the pool, gives NaN outputs. keys, key_off (int32,
+ * [batch + 1]) are device memory. Paged pools only (ring_size 0). Two launches. */
+int32_t pkv_attend_sparse(void* stream, const pkv_params* p, const float* q, const void* k_pool,
+                          const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                          const int32_t* keys, const int32_t* key_off, int32_t max_keys,
+                          int32_t batch, float* out, void* workspace, size_t workspace_bytes);
+
 /* K3 -- chunked-prefill attention over bf16 pages with bf16 MFMA (fp32 accumulation).
  * Replaces the engine's per-token prefill loop (append one token, then one
  * paged_attention_layer call for it: model_speculative_moe_batched.mojo:2600-2637 for

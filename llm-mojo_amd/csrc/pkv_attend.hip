@@ -160,6 +160,9 @@ struct AttendArgs {
     float scale;
     int32_t ring_size;  // > 0: ring pools (tables hold one ring slot per sequence)
     int64_t ring_base;  // ring mode, pos == null: first row of the sequence's ring
+    const int32_t* keys;     // sparse mode (non-null): key positions, ragged by key_off
+    const int32_t* key_off;  // [batch + 1]
+    int32_t max_keys;        // sparse mode: the longest list the caller sized for
     int32_t chunk;
     int32_t max_chunks;
     void* part_ml;  // Acc pairs (m, l) per (row, chunk)
@@ -181,6 +184,39 @@ __device__ inline bool keys_addressable(const AttendArgs& a, int s, int lo, int 
     const int slot = a.tables[(size_t)s * a.table_stride];
     *rbase = (int64_t)slot * a.ring_size;
     return slot >= 0 && slot < a.num_blocks;
+}
+
+// The keys sequence s attends, as a range [lo, hi] of chunk coordinates: key positions
+// (dense / ring modes: [window_start(pos), pos + q_len - 1]) or, in sparse mode, indices
+// into the sequence's key list. state: 0 = active, 1 = no keys (zero output), 2 = the
+// call's contract is violated (NaN output).
+struct SeqKeys {
+    int lo, hi, c_lo, nch, state, kbeg, pos0;
+    int64_t rbase;
+};
+__device__ inline SeqKeys seq_keys(const AttendArgs& a, int s) {
+    SeqKeys k{};
+    const int C = a.chunk;
+    if (a.keys) {
+        k.kbeg = a.key_off[s];
+        const int n = a.key_off[s + 1] - k.kbeg;
+        k.lo = 0;
+        k.hi = n - 1;
+        k.nch = (n + C - 1) / C;
+        k.state = n == 0 ? 1 : ((n < 0 || n > a.max_keys || k.kbeg < 0) ? 2 : 0);
+        return k;
+    }
+    k.pos0 = a.pos ? a.pos[s] : a.pos_scalar;
+    if (k.pos0 < 0) {  // inactive sequence: n <= 0 gives zeros (attention.mojo:180-185)
+        k.state = 1;
+        return k;
+    }
+    k.hi = k.pos0 + a.q_len - 1;
+    k.lo = window_start(k.pos0, a.window);
+    k.c_lo = k.lo / C;
+    k.nch = k.hi / C - k.c_lo + 1;
+    k.state = (!keys_addressable(a, s, k.lo, k.hi, &k.rbase) || k.nch > a.max_chunks) ? 2 : 0;
+    return k;
 }
 
 // Output row r of this workgroup: query j = r / G, head h = g * G + r % G.
@@ -235,40 +271,45 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     const int rl = lane % LPR;   // lane within the row
     const int rows = a.G * a.q_len;
 
-    const int pos0 = a.pos ? a.pos[s] : a.pos_scalar;
-    if (pos0 < 0) {  // inactive sequence: n <= 0 gives zeros (attention.mojo:180-185)
-        if (c == 0)
-            for (int i = tid; i < rows * D; i += kNT) a.out[out_index(a, s, g, i / D, i % D, D)] = 0.f;
+    const SeqKeys K = seq_keys(a, s);
+    if (K.state != 0) {  // no keys: zeros; contract violated: NaN
+        if (c == 0) {
+            const float fill = K.state == 1 ? 0.f : __builtin_nanf("");
+            for (int i = tid; i < rows * D; i += kNT) a.out[out_index(a, s, g, i / D, i % D, D)] = fill;
+        }
         return;
     }
-    const int hi = pos0 + a.q_len - 1;
-    const int lo = window_start(pos0, a.window);
+    const int pos0 = K.pos0, lo = K.lo, hi = K.hi, c_lo = K.c_lo, nch = K.nch;
+    const int64_t rbase = K.rbase;
     const int C = a.chunk;
-    const int c_lo = lo / C;
-    const int nch = hi / C - c_lo + 1;
-    int64_t rbase = 0;
-    if (!keys_addressable(a, s, lo, hi, &rbase) || nch > a.max_chunks) {  // contract violated
-        if (c == 0)
-            for (int i = tid; i < rows * D; i += kNT)
-                a.out[out_index(a, s, g, i / D, i % D, D)] = __builtin_nanf("");
-        return;
-    }
+    const bool sparse = a.keys != nullptr;
     if (c >= nch) return;
     const int t0 = max(lo, (c_lo + c) * C);
     const int t1 = min(hi, (c_lo + c) * C + C - 1);
     const int ntok = t1 - t0 + 1;
 
-    // Pages of this chunk -> LDS (bounds-checked against the pool).
+    // Pages of this chunk -> LDS (bounds-checked against the pool); in sparse mode the
+    // pool row of each of the chunk's keys instead.
     const int pg0 = t0 / a.bs;
-    const int npg = a.ring_size > 0 ? 0 : t1 / a.bs - pg0 + 1;
+    const int npg = sparse ? ntok : (a.ring_size > 0 ? 0 : t1 / a.bs - pg0 + 1);
     const int r_t0 = a.ring_size > 0 ? t0 % a.ring_size : 0;  // ring row of key t0
+    const int32_t* trow = a.tables + (size_t)s * a.table_stride;
     if (tid == 0) s_flag = 0;
     __syncthreads();
     for (int i = tid; i < npg; i += kNT) {
-        int b = a.tables[(size_t)s * a.table_stride + pg0 + i];
-        if (b < 0 || b >= a.num_blocks) {
-            s_flag = 1;
-            b = 0;
+        int b = 0;
+        if (sparse) {
+            const int key = a.keys[K.kbeg + t0 + i];
+            const int blk = key < 0 ? -1 : key / a.bs;
+            const int phys = (blk >= 0 && blk < a.table_stride) ? trow[blk] : -1;
+            if (phys < 0 || phys >= a.num_blocks) s_flag = 1;
+            else b = phys * a.bs + key % a.bs;
+        } else {
+            b = trow[pg0 + i];
+            if (b < 0 || b >= a.num_blocks) {
+                s_flag = 1;
+                b = 0;
+            }
         }
         s_page[i] = b;
     }
@@ -305,7 +346,9 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     auto row_off = [&](int tok) -> size_t {  // byte offset of token `tok`'s head slice
         const int t = t0 + tok;
         size_t row;
-        if (a.ring_size > 0) {
+        if (sparse) {
+            row = (size_t)s_page[tok];
+        } else if (a.ring_size > 0) {
             row = (size_t)ring_key_row(rbase, r_t0, tok, a.ring_size);
         } else {
             const int page = s_page[(t >> bs_shift) - pg0];
@@ -324,8 +367,9 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
     const int idx_own = rl / REP;
     const int r_own = idx_own % R;
     const int u_own = idx_own / R;
-    const int pq_own = pos0 + r_own / a.G;  // query position of my row
-    const int ws_own = window_start(pq_own, a.window);
+    // query position of my row and its first key (sparse mode: every listed key)
+    const int pq_own = sparse ? INT32_MAX : pos0 + r_own / a.G;
+    const int ws_own = sparse ? 0 : window_start(pq_own, a.window);
     const bool row_live = r_own < rows;
 
     Acc m_own = (Acc)-INFINITY;  // running max of my row over this wave's tokens
@@ -514,14 +558,9 @@ __global__ __launch_bounds__(kNT) void attend_merge_kernel(AttendArgs a) {
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
     const int rows = a.G * a.q_len;
-    const int pos0 = a.pos ? a.pos[s] : a.pos_scalar;
-    if (pos0 < 0) return;
-    const int hi = pos0 + a.q_len - 1;
-    const int lo = window_start(pos0, a.window);
-    const int c_lo = lo / a.chunk;
-    const int nch = hi / a.chunk - c_lo + 1;
-    int64_t rbase = 0;
-    if (!keys_addressable(a, s, lo, hi, &rbase) || nch > a.max_chunks || nch == 1) return;
+    const SeqKeys K = seq_keys(a, s);
+    const int nch = K.nch;
+    if (K.state != 0 || nch == 1) return;
 
     const Acc* part_o = static_cast<const Acc*>(a.part_o);
     const Acc* part_ml = static_cast<const Acc*>(a.part_ml);
@@ -632,15 +671,18 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
         return fail(PKV_ERR_INVALID, "null device pointer");
     const int G = p->num_heads / p->num_kv_heads;
     const int rows = G * q_len;
-    if (rows > 16) return fail(PKV_ERR_UNSUPPORTED, "q_len * (num_heads / num_kv_heads) must be <= 16");
     if (batch > 4096) return fail(PKV_ERR_INVALID, "batch must be <= 4096");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (stream_eligible(p, rows) && workspace_bytes >= stream_layout(p, batch, q_len).total) {
+    if (stream_eligible(p, G) && workspace_bytes >= stream_layout(p, batch, q_len).total) {
         rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
-                           ring_base, q_len, batch, max_pos, out, workspace, st);
+                           ring_base, q_len, batch, max_pos, nullptr, nullptr, 0, out,
+                           workspace, st);
         if (rc != PKV_OK) return rc;
         return check_launch("pkv_attend");
     }
+    if (rows > 16)
+        return fail(PKV_ERR_UNSUPPORTED, "this geometry allows at most 16 query rows "
+                                         "(q_len * num_heads / num_kv_heads) per kv head");
     AttendLayout lay = attend_layout(p, batch, q_len, max_pos);
     if (lay.chunk > kMaxChunk) return fail(PKV_ERR_UNSUPPORTED, "chunk larger than the kernel's LDS bound");
     if (workspace_bytes < lay.total)
@@ -686,10 +728,105 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     return check_launch("pkv_attend");
 }
 
+// Layout of the sparse mode's workspace: the chunk kernel's partials for key lists of up
+// to max_keys entries (window and ring do not bound a key list). Chunks index the list,
+// so they need not align with blocks: the largest of 256 / 128 / 64 / 32 keys that still
+// gives two workgroups per CU of the 256 (LSA lists are a few hundred keys).
+AttendLayout sparse_layout(const pkv_params* p, int32_t batch, int32_t max_keys) {
+    AttendLayout L{};
+    int chunk = 256;
+    while (chunk > 32 &&
+           (int64_t)batch * p->num_kv_heads * ((max_keys + chunk - 1) / chunk) < 512)
+        chunk /= 2;
+    L.chunk = chunk;
+    L.max_chunks = (max_keys + chunk - 1) / chunk;
+    auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t rows = (size_t)batch * p->num_heads;
+    L.ml_off = 0;
+    L.o_off = align(rows * L.max_chunks * 2 * sizeof(double));
+    L.total = L.o_off + align(rows * L.max_chunks * (size_t)p->head_dim * sizeof(double));
+    return L;
+}
+
 }  // namespace
 }  // namespace pkv
 
 extern "C" {
+
+size_t pkv_sparse_workspace_size(const pkv_params* p, int32_t batch, int32_t max_keys) {
+    if (pkv::validate_params(p) != PKV_OK) return 0;
+    if (batch <= 0 || max_keys <= 0) return 0;
+    const size_t chunked = pkv::sparse_layout(p, batch, max_keys).total;
+    const size_t stream = pkv::stream_layout(p, batch, 1).total;
+    return chunked > stream ? chunked : stream;
+}
+
+int32_t pkv_attend_sparse(void* stream, const pkv_params* p, const float* q, const void* k_pool,
+                          const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                          const int32_t* keys, const int32_t* key_off, int32_t max_keys,
+                          int32_t batch, float* out, void* workspace, size_t workspace_bytes) {
+    using namespace pkv;
+    clear_error();
+    int32_t rc = validate_params(p);
+    if (rc != PKV_OK) return rc;
+    if (p->ring_size > 0)
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_attend_sparse: paged pools only (ring_size 0)");
+    if (batch <= 0 || batch > 65535 || max_keys <= 0 || table_stride <= 0 ||
+        p->num_kv_heads > 65535)
+        return fail(PKV_ERR_INVALID, "batch, max_keys and table_stride must be positive");
+    if (!q || !k_pool || !v_pool || !block_tables || !keys || !key_off || !out || !workspace)
+        return fail(PKV_ERR_INVALID, "null device pointer");
+    const int G = p->num_heads / p->num_kv_heads;
+    if (G > 16) return fail(PKV_ERR_UNSUPPORTED, "num_heads / num_kv_heads must be <= 16");
+    if ((int64_t)p->num_blocks * p->block_size > INT32_MAX)
+        return fail(PKV_ERR_UNSUPPORTED, "pool rows must fit in int32");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (stream_eligible(p, G) && workspace_bytes >= stream_layout(p, batch, 1).total) {
+        rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, nullptr, 0, 0, 1,
+                           batch, 0, keys, key_off, max_keys, out, workspace, st);
+        if (rc != PKV_OK) return rc;
+        return check_launch("pkv_attend_sparse");
+    }
+    AttendLayout lay = sparse_layout(p, batch, max_keys);
+    if (lay.chunk > kMaxChunk) return fail(PKV_ERR_UNSUPPORTED, "chunk larger than the kernel's LDS bound");
+    if (workspace_bytes < lay.total)
+        return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_sparse_workspace_size()");
+    AttendArgs a{};
+    char* ws = static_cast<char*>(workspace);
+    a.q = q;
+    a.k_pool = static_cast<const char*>(k_pool);
+    a.v_pool = static_cast<const char*>(v_pool);
+    a.tables = block_tables;
+    a.table_stride = table_stride;
+    a.q_len = 1;
+    a.Hq = p->num_heads;
+    a.Hkv = p->num_kv_heads;
+    a.G = G;
+    a.bs = p->block_size;
+    a.num_blocks = p->num_blocks;
+    a.scale = p->scale;
+    a.keys = keys;
+    a.key_off = key_off;
+    a.max_keys = max_keys;
+    a.chunk = lay.chunk;
+    a.max_chunks = lay.max_chunks;
+    a.part_ml = ws + lay.ml_off;
+    a.part_o = ws + lay.o_off;
+    a.out = out;
+    dim3 grid(lay.max_chunks, p->num_kv_heads, batch);
+    const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
+    switch (p->head_dim) {
+        case 64: rc = bf16 ? dispatch_rows<64, uint16_t>(a, G, grid, st)
+                           : dispatch_rows<64, float>(a, G, grid, st); break;
+        case 256: rc = bf16 ? dispatch_rows<256, uint16_t>(a, G, grid, st)
+                            : dispatch_rows<256, float>(a, G, grid, st); break;
+        case 512: rc = bf16 ? dispatch_rows<512, uint16_t>(a, G, grid, st)
+                            : dispatch_rows<512, float>(a, G, grid, st); break;
+        default: return fail(PKV_ERR_UNSUPPORTED, "head_dim");
+    }
+    if (rc != PKV_OK) return rc;
+    return check_launch("pkv_attend_sparse");
+}
 
 int32_t pkv_attend(void* stream, const pkv_params* p, const float* q, const void* k_pool,
                    const void* v_pool, const int32_t* block_tables, int32_t table_stride,

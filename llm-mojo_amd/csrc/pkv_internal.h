@@ -50,15 +50,18 @@ struct StreamLayout {
     size_t total;
 };
 StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len);
-// True when the stream kernel covers this geometry (head_dim 256, <= 8 rows per kv head).
-bool stream_eligible(const pkv_params* p, int32_t rows);
+// True when the stream kernel covers this geometry: head_dim 256 or 512 with
+// G = num_heads / num_kv_heads <= 8 (any number of queries: launched in groups).
+bool stream_eligible(const pkv_params* p, int32_t G);
 // pos == NULL: one sequence at pos_scalar; in ring mode its ring starts at row
 // ring_base (otherwise ring slot block_tables[s * table_stride] starts at row
-// slot * ring_size).
+// slot * ring_size). keys != NULL: sparse mode, sequence s attends the key positions
+// keys[key_off[s] .. key_off[s+1]) (q_len 1, at most max_keys each).
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                       const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
-                      int32_t batch, int32_t max_pos, float* out, void* workspace,
+                      int32_t batch, int32_t max_pos, const int32_t* keys,
+                      const int32_t* key_off, int32_t max_keys, float* out, void* workspace,
                       hipStream_t st);
 
 __host__ __device__ inline int32_t window_start(int32_t pos, int32_t window) {

@@ -1,7 +1,10 @@
 // K2 hot path -- stream-K paged attention over whole pages (decode and verify).
 //
 // Replaces the reference's three-pass CPU loop (attention.mojo:151-294) for head_dim
-// 256 with up to 8 query rows per KV head (decode: G = Hq / Hkv rows; verify: G x q_len).
+// 256 or 512 with up to 8 query rows per KV head per launch (decode: G = Hq / Hkv rows;
+// verify: G x the launch's queries; the host splits longer verifies into query groups).
+// Keys come from block tables, rings (attention.mojo:264-269) or, for LSA, explicit key
+// lists (lsa_core.mojo:630-680).
 //
 // Work split. The keys every sequence attends ([window_start(pos), pos + q_len - 1])
 // are laid end to end, sequence after sequence; workgroup w takes the w-th run of
@@ -79,11 +82,18 @@ struct SKV<uint16_t> {  // bf16 bits
 #ifndef PKV_STREAM_U16
 #define PKV_STREAM_U16 16
 #endif
-template <typename KV, int R>
+template <int D, typename KV, int R>
 constexpr int batch_tokens() {
-    constexpr int u = sizeof(KV) == 4 ? PKV_STREAM_U32 : PKV_STREAM_U16;  // at R <= 2
+    constexpr int u0 = sizeof(KV) == 4 ? PKV_STREAM_U32 : PKV_STREAM_U16;  // D 256, R <= 2
+    constexpr int u = D == 512 ? u0 / 2 : u0;  // same bytes in flight per wave
     return R <= 2 ? u : (R == 4 ? u / 2 : u / 4);
 }
+
+// Where a sequence's keys live: pages through its block table, its ring, or the pool
+// rows of an explicit key list (sparse attention, no causal mask).
+constexpr int kAddrPaged = 0;
+constexpr int kAddrRing = 1;
+constexpr int kAddrSparse = 2;
 
 // ---- cross-lane primitives (wave64) -------------------------------------------------
 
@@ -307,7 +317,12 @@ struct StreamArgs {
     int32_t table_stride;
     const int32_t* pos;  // null -> pos_scalar (single sequence)
     int32_t pos_scalar;
-    int32_t q_len;
+    int32_t q_len;       // queries per sequence in q / out (their layout)
+    int32_t j0;          // first query of this launch
+    int32_t q_cnt;       // queries of this launch
+    const int32_t* keys;     // sparse: key positions, ragged by key_off [batch + 1]
+    const int32_t* key_off;
+    int32_t max_keys;
     int32_t Hq;
     int32_t Hkv;
     int32_t G;
@@ -320,7 +335,7 @@ struct StreamArgs {
     int32_t max_pos;   // last query position the caller sized for
     int32_t batch;
     int32_t nwg;       // P: workgroups along the keys
-    int32_t rows_seq;  // Hq * q_len
+    int32_t rows_seq;  // Hq * q_cnt: workspace rows per sequence
     int32_t* plan;     // [0] = per, [1 + s] = key prefix of sequence s (s <= batch)
     void* part_ml;     // Acc (m, l) per (slot, row)
     void* part_o;      // Acc [D] per (slot, row)
@@ -328,7 +343,7 @@ struct StreamArgs {
 };
 
 __device__ inline size_t out_row(const StreamArgs& a, int s, int g, int r) {
-    const int j = r / a.G, h = g * a.G + r % a.G;
+    const int j = a.j0 + r / a.G, h = g * a.G + r % a.G;
     return ((size_t)s * a.q_len + j) * a.Hq + h;
 }
 
@@ -353,14 +368,16 @@ __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
 
 // R query rows per wave; WPH waves per KV head split the head's rows (WPH = 2 gives two
 // waves of R rows each, reading the same K/V: the second read of a row slice hits the cache).
-// RING: ring pools (key t at row ring_base + t % ring_size) instead of block tables.
-template <int D, typename KV, int R, int WPH, bool RING>
+// ADDR: kAddrPaged, kAddrRing (key t at row ring_base + t % ring_size) or kAddrSparse.
+template <int D, typename KV, int R, int WPH, int ADDR>
 __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamArgs a) {
     using Acc = typename SKV<KV>::Acc;
     constexpr int kElt = SKV<KV>::kElt;
     constexpr int EPL = D / kSW;                // elements per lane per token
     constexpr int NWD = EPL * kElt / 4;         // 32-bit words per lane per token
-    constexpr int U = batch_tokens<KV, R>();    // tokens per batch
+    constexpr int U = batch_tokens<D, KV, R>(); // tokens per batch
+    constexpr bool RING = ADDR == kAddrRing;
+    constexpr bool SPARSE = ADDR == kAddrSparse;
     constexpr int NV = U * R;                   // dots per batch
     static_assert(NV <= kSW && (NV & (NV - 1)) == 0, "dots per batch: power of two <= 64");
     constexpr int REP = kSW / NV;               // lanes holding the same reduced dot
@@ -378,16 +395,25 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     const int B = a.batch;
 
     for (int i = tid; i < B; i += nthr) {
-        const int p0 = a.pos ? a.pos[i] : a.pos_scalar;
         int n = 0, lo = -1;
+        if constexpr (SPARSE) {  // the list's indices; an empty list gives zeros
+            const int kb = a.key_off[i], cnt = a.key_off[i + 1] - kb;
+            if (cnt < 0 || cnt > a.max_keys || kb < 0) lo = -2;
+            else if (cnt > 0) lo = 0, n = cnt;
+            s_pre[i] = n;
+            s_lo[i] = lo;
+            continue;
+        }
+        const int p0 = a.pos ? a.pos[i] : a.pos_scalar;
         if (p0 >= 0) {
-            const int hi = p0 + a.q_len - 1;
-            const int w0 = window_start(p0, a.window);
+            const int hi = p0 + a.j0 + a.q_cnt - 1;
+            const int w0 = window_start(p0 + a.j0, a.window);
             bool ok = hi <= a.max_pos;
             if constexpr (RING) {
                 // Every key of the call must still be in the ring (the reference aborts,
-                // attention.mojo:265-266), and the ring slot must lie in the pool.
-                ok = ok && hi - w0 + 1 <= a.ring_size;
+                // attention.mojo:265-266) -- the call's later queries have already written
+                // theirs -- and the ring slot must lie in the pool.
+                ok = ok && (p0 + a.q_len - 1) - w0 + 1 <= a.ring_size;
                 if (a.pos) {
                     const int slot = a.tables[(size_t)i * a.table_stride];
                     ok = ok && slot >= 0 && slot < a.num_blocks;
@@ -419,8 +445,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             const int lo = s_lo[s];
             if (lo >= 0) continue;
             const float fill = lo == -1 ? 0.f : __builtin_nanf("");
-            for (int i = tid; i < a.rows_seq * D; i += nthr)
-                a.out[((size_t)s * a.rows_seq + i / D) * D + i % D] = fill;
+            float* o = a.out + ((size_t)s * a.q_len + a.j0) * a.Hq * D;
+            for (int i = tid; i < a.rows_seq * D; i += nthr) o[i] = fill;
         }
     }
     const int k0 = w * per;
@@ -430,7 +456,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     const int rb = (wave % WPH) * R;  // first of this wave's rows of the head
     if (g >= a.Hkv) return;
 
-    const int rows = a.G * a.q_len;
+    const int rows = a.G * a.q_cnt;
     const size_t row_bytes = (size_t)a.Hkv * D * kElt;
     const char* kbase = a.k_pool + (size_t)g * D * kElt;  // wave-uniform
     const char* vbase = a.v_pool + (size_t)g * D * kElt;
@@ -463,7 +489,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
         const int tb = lo_key + min(k1, pe) - ps;  // one past the last
         const bool single = (ps / per) == ((pe - 1) / per);
-        const int pos0 = a.pos ? ufirst(a.pos[s]) : a.pos_scalar;
+        const int pos0 = SPARSE ? 0 : (a.pos ? ufirst(a.pos[s]) : a.pos_scalar);
 
         // Query rows -> registers (scaled); rows beyond `rows` stay zero.
         Acc qr[R][EPL];
@@ -482,8 +508,10 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
                 for (int e = 0; e < EPL; ++e) qr[r][e] = (Acc)0;
             }
         }
-        const int pq_own = pos0 + (rb + r_own) / a.G;  // query position of my row
-        const int ws_own = window_start(pq_own, a.window);
+        // query position of my row and its first key (sparse: every listed key)
+        const int pq_own = SPARSE ? INT32_MAX : pos0 + a.j0 + (rb + r_own) / a.G;
+        const int ws_own = SPARSE ? 0 : window_start(pq_own, a.window);
+        const int kbeg = SPARSE ? ufirst(a.key_off[s]) : 0;
 
         Acc m_own = (Acc)-INFINITY, l_own = (Acc)0;
         Acc acc[R][EPL];
@@ -506,7 +534,19 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
 
         for (int t = ta; t < tb; t += U) {
             const int tl = min(t + U - 1, tb - 1);
-            if (!RING && (tl >> a.bs_shift) - pgbase >= kSW) {  // page ids of the next 64 pages
+            if (SPARSE && tl - pgbase >= kSW) {  // pool rows of the next 64 listed keys
+                pgbase = t;
+                int row = 0;
+                if (t + lane < tb) {
+                    const int key = a.keys[kbeg + t + lane];
+                    const int blk = key >> a.bs_shift;
+                    const int phys = (key >= 0 && blk < a.table_stride) ? trow[blk] : -1;
+                    if (phys < 0 || phys >= a.num_blocks) bad = true;
+                    else row = (phys << a.bs_shift) | (key & bs_mask);
+                }
+                vpg = row;
+            }
+            if (ADDR == kAddrPaged && (tl >> a.bs_shift) - pgbase >= kSW) {  // next 64 page ids
                 pgbase = t >> a.bs_shift;
                 int b = 0;
                 if (pgbase + lane <= last_page) {
@@ -527,6 +567,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
                 size_t off;
                 if constexpr (RING) {
                     off = (size_t)ring_key_row(rbase, r0, tt - ta, a.ring_size) * row_bytes;
+                } else if constexpr (SPARSE) {
+                    off = (size_t)(uint32_t)__builtin_amdgcn_readlane(vpg, tt - pgbase) * row_bytes;
                 } else {
                     const int page = __builtin_amdgcn_readlane(vpg, (tt >> a.bs_shift) - pgbase);
                     off = (((size_t)page << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
@@ -690,7 +732,8 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
         }
         for (; c < cnt; ++c) o8[0] = fma(s_w[c], po[slot_row(c) * D + d], o8[0]);
         const Acc o = ((o8[0] + o8[1]) + (o8[2] + o8[3])) + ((o8[4] + o8[5]) + (o8[6] + o8[7]));
-        a.out[((size_t)s * a.rows_seq + row) * D + d] = nan ? __builtin_nanf("") : (float)(o * inv);
+        a.out[(((size_t)s * a.q_len + a.j0) * a.Hq + row) * D + d] =
+            nan ? __builtin_nanf("") : (float)(o * inv);
     }
 }
 
@@ -727,13 +770,13 @@ int fill_workgroups(const void* fn, int threads, size_t lds) {
     return p;
 }
 
-template <int D, typename KV, int R, int WPH, bool RING>
-int32_t launch_ring(StreamArgs a, hipStream_t st) {
+template <int D, typename KV, int R, int WPH, int ADDR>
+int32_t launch_addr(StreamArgs a, hipStream_t st) {
     using Acc = typename SKV<KV>::Acc;
     const int waves = a.Hkv * WPH < kMaxWaves ? a.Hkv * WPH : kMaxWaves;
     const int threads = waves * kSW;
     const size_t lds = (size_t)(2 * a.batch + 1) * sizeof(int);
-    const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH, RING>);
+    const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH, ADDR>);
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
     // Resident workgroups only: the head groups share the slots, and each workgroup
@@ -741,7 +784,7 @@ int32_t launch_ring(StreamArgs a, hipStream_t st) {
     const int groups = (a.Hkv * WPH + kMaxWaves - 1) / kMaxWaves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     dim3 grid(groups, a.nwg);
-    hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, RING>), grid, dim3(threads), lds, st,
+    hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, ADDR>), grid, dim3(threads), lds, st,
                        a);
     hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch), dim3(kMergeNT),
                        0, st, a);
@@ -750,8 +793,25 @@ int32_t launch_ring(StreamArgs a, hipStream_t st) {
 
 template <int D, typename KV, int R, int WPH = 1>
 int32_t launch_r(StreamArgs a, hipStream_t st) {
-    return a.ring_size > 0 ? launch_ring<D, KV, R, WPH, true>(a, st)
-                           : launch_ring<D, KV, R, WPH, false>(a, st);
+    if (a.keys) return launch_addr<D, KV, R, WPH, kAddrSparse>(a, st);
+    return a.ring_size > 0 ? launch_addr<D, KV, R, WPH, kAddrRing>(a, st)
+                           : launch_addr<D, KV, R, WPH, kAddrPaged>(a, st);
+}
+
+// One launch (attention + merge) for `rows` <= 8 query rows per kv head. head_dim 256:
+// one wave holds up to 4 rows (two waves of 4 for 5..8); head_dim 512: waves of 2 rows.
+template <typename KV>
+int32_t launch_rows(StreamArgs a, int D, int rows, hipStream_t st) {
+    if (D == 256) {
+        if (rows <= 1) return launch_r<256, KV, 1>(a, st);
+        if (rows <= 2) return launch_r<256, KV, 2>(a, st);
+        if (rows <= 4) return launch_r<256, KV, 4>(a, st);
+        return launch_r<256, KV, 4, 2>(a, st);
+    }
+    if (rows <= 1) return launch_r<512, KV, 1>(a, st);
+    if (rows <= 2) return launch_r<512, KV, 2>(a, st);
+    if (rows <= 4) return launch_r<512, KV, 2, 2>(a, st);
+    return launch_r<512, KV, 2, 4>(a, st);
 }
 
 }  // namespace
@@ -768,17 +828,18 @@ StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len) {
     return L;
 }
 
-bool stream_eligible(const pkv_params* p, int32_t rows) {
-    return p->head_dim == 256 && rows <= 8 && rows >= 1;
+bool stream_eligible(const pkv_params* p, int32_t G) {
+    return (p->head_dim == 256 || p->head_dim == 512) && G >= 1 && G <= 8;
 }
 
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                       const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
-                      int32_t batch, int32_t max_pos, float* out, void* workspace,
+                      int32_t batch, int32_t max_pos, const int32_t* keys,
+                      const int32_t* key_off, int32_t max_keys, float* out, void* workspace,
                       hipStream_t st) {
     const int G = p->num_heads / p->num_kv_heads;
-    const int rows = G * q_len;
+    if (!stream_eligible(p, G)) return fail(PKV_ERR_UNSUPPORTED, "stream path: geometry");
     StreamLayout lay = stream_layout(p, batch, q_len);
     StreamArgs a{};
     char* ws = static_cast<char*>(workspace);
@@ -790,6 +851,9 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.pos = pos;
     a.pos_scalar = pos_scalar;
     a.q_len = q_len;
+    a.keys = keys;
+    a.key_off = key_off;
+    a.max_keys = max_keys;
     a.Hq = p->num_heads;
     a.Hkv = p->num_kv_heads;
     a.G = G;
@@ -801,19 +865,24 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.ring_base = ring_base;
     a.max_pos = max_pos;
     a.batch = batch;
-    a.rows_seq = p->num_heads * q_len;
     a.plan = reinterpret_cast<int32_t*>(ws + lay.plan_off);
     a.part_ml = ws + lay.ml_off;
     a.part_o = ws + lay.o_off;
     a.out = out;
     const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
-    if (p->head_dim != 256) return fail(PKV_ERR_UNSUPPORTED, "stream path: head_dim 256 only");
-    if (rows <= 1) return bf16 ? launch_r<256, uint16_t, 1>(a, st) : launch_r<256, float, 1>(a, st);
-    if (rows <= 2) return bf16 ? launch_r<256, uint16_t, 2>(a, st) : launch_r<256, float, 2>(a, st);
-    if (rows <= 4) return bf16 ? launch_r<256, uint16_t, 4>(a, st) : launch_r<256, float, 4>(a, st);
-    // 5..8 rows (verify): two waves of 4 rows per kv head
-    if (rows <= 8) return bf16 ? launch_r<256, uint16_t, 4, 2>(a, st) : launch_r<256, float, 4, 2>(a, st);
-    return fail(PKV_ERR_UNSUPPORTED, "stream path: at most 8 query rows per kv head");
+    // Queries in groups of at most 8 query rows per kv head, one launch pair each; the
+    // launches share the workspace in stream order.
+    const int per_launch = 8 / G;
+    for (int j0 = 0; j0 < q_len; j0 += per_launch) {
+        a.j0 = j0;
+        a.q_cnt = q_len - j0 < per_launch ? q_len - j0 : per_launch;
+        a.rows_seq = p->num_heads * a.q_cnt;
+        const int rows = G * a.q_cnt;
+        const int32_t rc = bf16 ? launch_rows<uint16_t>(a, p->head_dim, rows, st)
+                                : launch_rows<float>(a, p->head_dim, rows, st);
+        if (rc != PKV_OK) return rc;
+    }
+    return PKV_OK;
 }
 
 }  // namespace pkv

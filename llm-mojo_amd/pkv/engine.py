@@ -236,6 +236,24 @@ class PagedKVCache:
                  self.max_pos if max_pos is None else max_pos, _ptr(out), self.workspace.ptr,
                  self.workspace.nbytes)
 
+    def attend_sparse(self, layer: int, q, keys, key_off, max_keys: int, out,
+                      batch: int | None = None):
+        """Sparse paged attention over explicit key lists (K2', LSA): q / out device fp32
+        [batch][Hq][D]; sequence s attends key positions keys[key_off[s] .. key_off[s+1])
+        (device int32 arrays, e.g. from lsa_expand_buckets) of its table."""
+        b = batch or self.max_seqs
+        p = self.params[layer]
+        need = lib.load().pkv_sparse_workspace_size(ctypes.byref(p), b, max_keys)
+        if need == 0:
+            raise lib.PkvError(-1, "pkv_sparse_workspace_size", lib.load().pkv_last_error().decode())
+        if need > self.workspace.nbytes:
+            self.workspace.free()
+            self.workspace = hip.DeviceArray((need,), np.uint8, zero=True)
+        lib.call("pkv_attend_sparse", self._stream(), ctypes.byref(p), _ptr(q),
+                 self.k_pools[layer].ptr, self.v_pools[layer].ptr, self.tables.ptr,
+                 self.table_stride, _ptr(keys), self._ints(key_off, self._i32_b, b + 1),
+                 max_keys, b, _ptr(out), self.workspace.ptr, self.workspace.nbytes)
+
     def prefill(self, layer: int, q, pos, q_off, max_q: int, out, batch: int | None = None,
                 max_pos: int | None = None):
         """Chunked-prefill attention (K3, bf16 pools): q bf16 [rows][Hq][D] (device),
@@ -288,6 +306,28 @@ class PagedKVCache:
         for a in (self.tables, self.table_lens, self.free_list, self.free_count, self.status,
                   self.workspace, self._i32_a, self._i32_b, self.kv_slots):
             a.free()
+
+
+def lsa_expand_buckets(picked, sizes, members, pos: int, top_k: int, sink_size: int,
+                       window_size: int) -> np.ndarray:
+    """Key list of one LSA query (LSALayerIndex.expand_buckets, lsa_core.mojo:573-604):
+    members of the picked buckets, in order, that lie in [sink_size, window_start), at most
+    top_k of them; then the window [window_start, pos], window_start = max(0, pos + 1 -
+    window_size); then the sinks [0, min(sink_size, window_start, pos + 1)).
+    members: [buckets][bucket_cap] positions, sizes: [buckets]."""
+    window_start = max(0, pos + 1 - window_size)
+    sel: list[int] = []
+    for b in picked:
+        for tok in members[b][: int(sizes[b])]:
+            if sink_size <= tok < window_start:
+                sel.append(int(tok))
+                if len(sel) >= top_k:
+                    break
+        if len(sel) >= top_k:
+            break
+    sel.extend(range(window_start, pos + 1))
+    sel.extend(range(min(sink_size, window_start, pos + 1)))
+    return np.asarray(sel, np.int32)
 
 
 def paged_attention_layer(q, k_pool, v_pool, block_table, block_size: int, pos: int,

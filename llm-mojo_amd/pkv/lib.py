@@ -58,6 +58,9 @@ PROTOTYPES = {
                                          _i32, _vp, _i32, _i32, _i32, _i32, _vp, _sz]),
     "pkv_append_qkv": (_i32, [_vp, _PP, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
                               _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "pkv_sparse_workspace_size": (_sz, [_PP, _i32, _i32]),
+    "pkv_attend_sparse": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _vp,
+                                 _vp, _sz]),
     "pkv_last_error": (ctypes.c_char_p, []),
     "pkv_version": (_i32, []),
 }

@@ -58,6 +58,13 @@ def _L():
             "pkvo_apply_rope": (None, [vp, i64, i64, i64, ctypes.c_int]),
             "pkvo_apply_rope_qk": (None, [vp, vp, i64, i64, i64, i64, ctypes.c_int]),
             "pkvo_ref_apply_rope": (None, [vp, i64, i64, i64, ctypes.c_int]),
+            "pkvo_lsa_sparse_paged_attention": (None, [vp, vp, vp, ctypes.c_int, vp, i64, vp, i64,
+                                                       i64, i64, i64, vp, vp, vp, ctypes.c_int]),
+            "pkvo_lsa_expand_buckets": (i64, [vp, i64, vp, vp, i64, i64, i64, i64, i64, vp]),
+            "pkvo_attend_sparse": (None, [ctypes.c_int, i32, i32, i32, i32, f32, vp, vp, vp, vp,
+                                          i32, vp, vp, i32, vp, ctypes.c_int, ctypes.c_int]),
+            "pkvo_attend_sparse_f64": (None, [ctypes.c_int, i32, i32, i32, i32, f32, vp, vp, vp,
+                                              vp, i32, vp, vp, i32, vp]),
             "pkvo_append_qkv_f64": (None, [i32, i32, i32, ctypes.c_int, vp, vp, i32, vp, vp, vp,
                                            vp, vp, i32, i32, vp, vp, vp]),
             "pkvo_append_qkv": (None, [ctypes.c_int, i32, i32, i32, i32, i32, i32, ctypes.c_int,
@@ -234,6 +241,64 @@ def producer_f64(pos, tok_off, q, k, v, q_norm_w, k_norm_w, max_new, num_heads, 
                              _p(tok_off), max_new, _p(q), _p(k), None if vv is None else _p(vv),
                              _p(qw), _p(kw), q.shape[0], pos.size, _p(qo), _p(ko), _p(vo))
     return qo, ko, vo
+
+
+def lsa_sparse_paged_attention(q, k_pool, v_pool, block_table, block_size, selected, num_heads,
+                               num_kv_heads, head_dim, nthreads=1):
+    """lsa_core.mojo:630-680 (single query, explicit key list). Returns attn_out."""
+    q = np.ascontiguousarray(q, np.float32)
+    tab = np.ascontiguousarray(np.asarray(block_table, dtype=np.int64))
+    sel = np.ascontiguousarray(np.asarray(selected, dtype=np.int64))
+    n = max(sel.size, 1)
+    scores = np.empty(num_heads * n, np.float32)
+    rows = np.empty(n, np.int64)
+    out = np.empty(num_heads * head_dim, np.float32)
+    _L().pkvo_lsa_sparse_paged_attention(_p(q), _p(k_pool), _p(v_pool), _dtype_of(k_pool),
+                                         _p(tab), block_size, _p(sel), sel.size, num_heads,
+                                         num_kv_heads, head_dim, _p(scores), _p(rows), _p(out),
+                                         nthreads)
+    return out
+
+
+def lsa_expand_buckets(picked, sizes, members, pos, top_k, sink_size, window_size):
+    """lsa_core.mojo:573-604. members: [buckets][bucket_cap]. Returns the key list."""
+    picked = np.ascontiguousarray(np.asarray(picked, dtype=np.int64))
+    sizes = np.ascontiguousarray(np.asarray(sizes, dtype=np.int64))
+    members = np.ascontiguousarray(np.asarray(members, dtype=np.int64))
+    out = np.empty(top_k + window_size + sink_size + 1, np.int64)
+    n = _L().pkvo_lsa_expand_buckets(_p(picked), picked.size, _p(sizes), _p(members),
+                                     members.shape[1], pos, top_k, sink_size, window_size, _p(out))
+    return out[:n].copy()
+
+
+def attend_sparse(q, k_pool, v_pool, tables, keys, key_off, num_heads, num_kv_heads, head_dim,
+                  block_size, scale=1.0, nthreads=1, par=0):
+    """One lsa_sparse_paged_attention call per sequence; q: [batch, Hq, D] fp32."""
+    q = np.ascontiguousarray(q, np.float32)
+    tables = np.ascontiguousarray(tables, np.int32)
+    keys = np.ascontiguousarray(keys, np.int32)
+    key_off = np.ascontiguousarray(key_off, np.int32)
+    batch = key_off.size - 1
+    out = np.empty((batch, num_heads, head_dim), np.float32)
+    _L().pkvo_attend_sparse(_dtype_of(k_pool), num_heads, num_kv_heads, head_dim, block_size,
+                            scale, _p(q), _p(k_pool), _p(v_pool), _p(tables), tables.shape[1],
+                            _p(keys), _p(key_off), batch, _p(out), nthreads, par)
+    return out
+
+
+def attend_sparse_f64(q, k_pool, v_pool, tables, keys, key_off, num_heads, num_kv_heads,
+                      head_dim, block_size, scale=1.0):
+    """Exact (float64) attention over each sequence's key list."""
+    q = np.ascontiguousarray(q, np.float32)
+    tables = np.ascontiguousarray(tables, np.int32)
+    keys = np.ascontiguousarray(keys, np.int32)
+    key_off = np.ascontiguousarray(key_off, np.int32)
+    batch = key_off.size - 1
+    out = np.empty((batch, num_heads, head_dim), np.float64)
+    _L().pkvo_attend_sparse_f64(_dtype_of(k_pool), num_heads, num_kv_heads, head_dim, block_size,
+                                scale, _p(q), _p(k_pool), _p(v_pool), _p(tables), tables.shape[1],
+                                _p(keys), _p(key_off), batch, _p(out))
+    return out
 
 
 class Lcg:

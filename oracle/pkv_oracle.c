@@ -37,6 +37,9 @@
  *   pkvo_append_qkv_f64              the same producer step in float64 (the fp32 angle of the
  *                                    reference, then exact arithmetic): the exact values both
  *                                    fp32 evaluations approximate
+ *   pkvo_lsa_sparse_paged_attention  lsa_core.mojo:630-680 (attention over an explicit key list)
+ *   pkvo_lsa_expand_buckets          lsa_core.mojo:573-604 (bucket members, window, sinks)
+ *   pkvo_attend_sparse / _f64        lsa_sparse_paged_attention per sequence of a batch
  *   pkvo_rollback                    retire :3626-3628 / reset :2424-2439 (ascending free order);
  *                                    truncation after rejected drafts has no reference code and
  *                                    follows the build's definition (keep ceil(len/bs) blocks,
@@ -680,6 +683,140 @@ void pkvo_append_qkv_f64(int32_t num_heads, int32_t num_kv_heads, int32_t head_d
             }
         }
     }
+}
+
+/* ------------------------------------------------- lsa_core.mojo:630-680
+ * Sparse paged attention over the key positions selected[0 .. n_sel): rows from the
+ * block table, then the dispatch of paged_attention_layer (head pairs on `nthreads`
+ * threads when n_sel >= 64) over the same _eval_head_range. n_sel == 0 gives zeros.  */
+void pkvo_lsa_sparse_paged_attention(const float* q, const void* k_pool, const void* v_pool,
+                                     int dtype, const int64_t* block_table, int64_t block_size,
+                                     const int64_t* selected, int64_t n_sel, int64_t num_heads,
+                                     int64_t num_kv_heads, int64_t head_dim, float* scores,
+                                     int64_t* rows, float* out, int nthreads) {
+    if (n_sel == 0) {
+        for (int64_t i = 0; i < num_heads * head_dim; ++i) out[i] = 0.0f;
+        return;
+    }
+    int64_t kv_stride = num_kv_heads * head_dim;
+    int64_t ratio = num_heads / num_kv_heads;
+    for (int64_t idx = 0; idx < n_sel; ++idx) {
+        int64_t t = selected[idx];
+        rows[idx] = (block_table[t / block_size] * block_size + t % block_size) * kv_stride;
+    }
+    if (n_sel >= 64 && num_heads >= 4 && (num_heads % 2 == 0) && (ratio % 2 == 0)) {
+#pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static, 1) if (nthreads > 1)
+        for (int64_t t = 0; t < num_heads / 2; ++t) {
+            int64_t h_start = t * 2;
+            eval_head_range(q, k_pool, v_pool, dtype, rows, scores, out, n_sel,
+                            (h_start / ratio) * head_dim, h_start, h_start + 2, head_dim);
+        }
+    } else {
+        for (int64_t g = 0; g < num_kv_heads; ++g)
+            eval_head_range(q, k_pool, v_pool, dtype, rows, scores, out, n_sel, g * head_dim,
+                            g * ratio, g * ratio + ratio, head_dim);
+    }
+}
+
+/* ------------------------------------------------- lsa_core.mojo:573-604
+ * Expands picked buckets into the key list: members of each picked bucket (in order) that
+ * lie in [sink_size, window_start), stopping at top_k of them; then the window
+ * [window_start, pos] with window_start = max(0, pos + 1 - window_size); then the sinks
+ * [0, min(sink_size, window_start, pos + 1)). members is [bucket][bucket_cap]. Returns
+ * the count written to out (at most top_k + window_size + sink_size entries).        */
+int64_t pkvo_lsa_expand_buckets(const int64_t* picked, int64_t n_picked, const int64_t* sizes,
+                                const int64_t* members, int64_t bucket_cap, int64_t pos,
+                                int64_t top_k, int64_t sink_size, int64_t window_size,
+                                int64_t* out) {
+    int64_t window_start = pos + 1 - window_size;
+    if (window_start < 0) window_start = 0;
+    int64_t n = 0;
+    for (int64_t bi = 0; bi < n_picked; ++bi) {
+        int64_t b = picked[bi];
+        for (int64_t m = 0; m < sizes[b]; ++m) {
+            int64_t tok = members[b * bucket_cap + m];
+            if (tok >= sink_size && tok < window_start) {
+                out[n++] = tok;
+                if (n >= top_k) break;
+            }
+        }
+        if (n >= top_k) break;
+    }
+    for (int64_t t = window_start; t <= pos; ++t) out[n++] = t;
+    int64_t sink_limit = sink_size < window_start ? sink_size : window_start;
+    if (pos + 1 < sink_limit) sink_limit = pos + 1;
+    for (int64_t t = 0; t < sink_limit; ++t) out[n++] = t;
+    return n;
+}
+
+/* ------------------------------------------------ batched sparse attention
+ * Sequence s attends the key positions keys[key_off[s] .. key_off[s+1]) through its
+ * table (one lsa_sparse_paged_attention call); q / out are [batch][num_heads][head_dim].
+ * q_scale multiplies q first (a power of two, exact). par: as pkvo_attend (0: head-pair
+ * tasks on nthreads threads; 1: sequences spread over the threads).                  */
+void pkvo_attend_sparse(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        int32_t block_size, float q_scale, const float* q, const void* k_pool,
+                        const void* v_pool, const int32_t* tables, int32_t table_stride,
+                        const int32_t* keys, const int32_t* key_off, int32_t batch, float* out,
+                        int nthreads, int par) {
+    int64_t hd = (int64_t)num_heads * head_dim;
+    int64_t max_n = 1;
+    for (int32_t s = 0; s < batch; ++s)
+        if (key_off[s + 1] - key_off[s] > max_n) max_n = key_off[s + 1] - key_off[s];
+    int outer = (par >= 1 && nthreads > 1) ? nthreads : 1;
+    int inner = par >= 1 ? 1 : nthreads;
+#pragma omp parallel num_threads(outer) if (outer > 1)
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)(num_heads * max_n));
+        int64_t* rows = (int64_t*)malloc(sizeof(int64_t) * (size_t)max_n);
+        int64_t* sel = (int64_t*)malloc(sizeof(int64_t) * (size_t)max_n);
+        int64_t* tab = (int64_t*)malloc(sizeof(int64_t) * (size_t)(table_stride > 0 ? table_stride : 1));
+        float* qs = (float*)malloc(sizeof(float) * (size_t)hd);
+#pragma omp for schedule(dynamic, 1)
+        for (int32_t s = 0; s < batch; ++s) {
+            int64_t n = key_off[s + 1] - key_off[s];
+            for (int32_t i = 0; i < table_stride; ++i) tab[i] = tables[(int64_t)s * table_stride + i];
+            for (int64_t i = 0; i < n; ++i) sel[i] = keys[key_off[s] + i];
+            for (int64_t i = 0; i < hd; ++i) qs[i] = q[s * hd + i] * q_scale;
+            pkvo_lsa_sparse_paged_attention(qs, k_pool, v_pool, dtype, tab, block_size, sel, n,
+                                            num_heads, num_kv_heads, head_dim, scores, rows,
+                                            out + s * hd, inner);
+        }
+        free(scores);
+        free(rows);
+        free(sel);
+        free(tab);
+        free(qs);
+    }
+}
+
+/* The same in float64 (test_attention.mojo:123-163's naive oracle over the listed keys,
+ * read through a one-row-per-block table). n = 0 gives zeros.                      */
+void pkvo_attend_sparse_f64(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t block_size, float q_scale, const float* q,
+                            const void* k_pool, const void* v_pool, const int32_t* tables,
+                            int32_t table_stride, const int32_t* keys, const int32_t* key_off,
+                            int32_t batch, double* out) {
+    int64_t hd = (int64_t)num_heads * head_dim;
+    float* qs = (float*)malloc(sizeof(float) * (size_t)hd);
+    for (int32_t s = 0; s < batch; ++s) {
+        int64_t n = key_off[s + 1] - key_off[s];
+        if (n <= 0) {
+            for (int64_t i = 0; i < hd; ++i) out[s * hd + i] = 0.0;
+            continue;
+        }
+        int64_t* tab = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+        for (int64_t i = 0; i < n; ++i) {
+            int64_t t = keys[key_off[s] + i];
+            tab[i] = (int64_t)tables[(int64_t)s * table_stride + t / block_size] * block_size +
+                     t % block_size;
+        }
+        for (int64_t i = 0; i < hd; ++i) qs[i] = q[s * hd + i] * q_scale;
+        pkvo_attention_f64(qs, k_pool, v_pool, dtype, tab, 1, n - 1, 0, num_heads, num_kv_heads,
+                           head_dim, out + s * hd);
+        free(tab);
+    }
+    free(qs);
 }
 
 /* ------------------------------------------------------- rollback / retire

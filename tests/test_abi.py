@@ -85,8 +85,9 @@ def test_null_pointers_and_small_workspace_rejected():
         == lib.PKV_ERR_INVALID
     assert L.pkv_append(None, ctypes.byref(p), 1, 1, 1, 4, 1, 1, 1, 1, 1, 1, 1, 1, 1, 5000, 1) \
         == lib.PKV_ERR_UNSUPPORTED
-    # verify with too many query rows per kv head (q_len 9 x ratio 2 > 16)
-    assert L.pkv_attend(None, ctypes.byref(p), 1, 1, 1, 1, 4, 1, 9, 1, 10, 1, 1, 1 << 30) \
+    # head_dim 64 (no stream kernel) with too many query rows per kv head (9 x 2 > 16)
+    d64 = _params(head_dim=64)
+    assert L.pkv_attend(None, ctypes.byref(d64), 1, 1, 1, 1, 4, 1, 9, 1, 10, 1, 1, 1 << 30) \
         == lib.PKV_ERR_UNSUPPORTED
 
 

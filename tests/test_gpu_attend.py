@@ -199,6 +199,19 @@ def test_verify_sliding_bf16(gpu):
     _batched_case(rng, 5, 4, ctx, 16, 8, 256, 16, 1024, BF16, 0.0625)
 
 
+@pytest.mark.parametrize("geom,q_len,window,kv_dtype", [
+    ((16, 2, 512), 5, 0, F32),     # the model's global layers: 5 verify queries, 40 rows
+    ((16, 2, 512), 5, 0, BF16),
+    ((16, 8, 256), 9, 1024, F32),  # sliding: 9 queries (18 rows) in query groups
+], ids=["g512-f32", "g512-bf16", "s256-q9"])
+def test_verify_query_groups(gpu, geom, q_len, window, kv_dtype):
+    print(f"[attend] verify query groups {geom} q_len={q_len}", flush=True)
+    rng = np.random.default_rng(q_len + geom[2])
+    ctx = rng.integers(300, 3000, 5)
+    ctx[0] = 0
+    _batched_case(rng, 5, q_len, ctx, *geom, 16, window, kv_dtype, 0.0625)
+
+
 def test_gqa8_d512(gpu):
     rng = np.random.default_rng(12)
     ctx = rng.integers(1, 4000, 4)
