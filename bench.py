@@ -283,6 +283,8 @@ def _line(metric, value, unit, steps, warmup, ms_per_step, dtype, workload, roof
          "N(0,1) K/V/Q, seeded random non-overlapping block tables",
          "config": {"workload": workload}, "roofline": roofline}
     r.update(extra)
+    if "data" in extra:
+        r["data"] = extra["data"]
     return r
 
 
@@ -853,6 +855,75 @@ def bench_lsa(args, log):
     return res
 
 
+def bench_wo(args, log):
+    """The Wo projection after attention (pkv_q4_matmul: Q4_0 weights x attn_out) at the
+    decode batch of config 2 (32 sequences), for the sliding layers' 4096 -> 2816 and the
+    global layers' 8192 -> 2816 (16 q heads x 256 / 512 -> hidden 2816, config.json)."""
+    from pkv import hip, q4_matmul, synth
+
+    from oracle import oracle as O
+
+    B, C_OUT = 32, 2816
+    stream = hip.Stream()
+    rng = np.random.default_rng(args.seed)
+    legs = {}
+    for name, c_in in (("sliding", 4096), ("global", 8192)):
+        packed, scales = O.quantize_q4_0((rng.standard_normal((C_OUT, c_in)) * 0.05)
+                                         .astype(np.float32))
+        dw, ds = hip.DeviceArray.from_numpy(packed), hip.DeviceArray.from_numpy(scales)
+        x = synth.normal((B, c_in), 401)
+        out = hip.DeviceArray((B, C_OUT), np.float32)
+        ws = q4_matmul(dw, ds, x, out, c_in, C_OUT, B, stream=stream)
+        ev = _event_pairs(hip, args.steps)
+
+        def step(i, events=None):
+            if events:
+                events[i][0].record(stream)
+            q4_matmul(dw, ds, x, out, c_in, C_OUT, B, workspace=ws, stream=stream)
+            if events:
+                events[i][1].record(stream)
+
+        for i in range(args.warmup):
+            step(i)
+        ms = _timed(hip, stream, args.steps, step)
+        _timed(hip, stream, args.steps, lambda i: step(i, ev))
+        dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+        nbytes = C_OUT * c_in // 2 + C_OUT * c_in // 32 * 4 + B * c_in * 4 + B * C_OUT * 4
+        legs[name] = dict(ms=ms, dur=dur, nbytes=nbytes, packed=packed, scales=scales,
+                          x=x.numpy(), got=out.numpy(), c_in=c_in)
+    g, sl = legs["global"], legs["sliding"]
+    res = _line("Wo projection (Q4_0) sequences/s at the decode batch, global layer 8192 -> 2816",
+                B * args.steps / (g["ms"] / 1e3), "sequences/s", args.steps, args.warmup,
+                g["ms"] / args.steps, "q4_0 x f32",
+                "pkv_q4_matmul: 32 sequences' attn_out (16 q heads x 512 = 8192) times the Q4_0 "
+                "Wo matrix (2816 x 8192, block 32), fp32 out",
+                _roofline(g["nbytes"], g["dur"], "q4_matmul_kernel + q4_reduce_kernel"),
+                {"data": "synthetic: seeded N(0,1) x, Q4_0 weights quantized from seeded "
+                         "N(0, 0.05) matrices (random-init, no checkpoint)",
+                 "sliding_4096": {"us_per_call": round(sl["dur"] * 1e3, 2),
+                                  "gbs": round(sl["nbytes"] / (sl["dur"] / 1e3) / 1e9, 1),
+                                  "bytes_per_call": int(sl["nbytes"])}})
+    if args.cpu_seconds > 0:
+        n, el = 0, 0.0
+        errs = []
+        while el < args.cpu_seconds and n < B:
+            t = time.perf_counter()
+            ref = O.q4_matmul_vec(g["packed"], g["scales"], g["x"][n])
+            el += time.perf_counter() - t
+            exact = O.q4_matmul_f64(g["packed"], g["scales"], g["x"][n])
+            errs.append((float(np.max(np.abs(g["got"][n] - ref))),
+                         float(np.max(np.abs(g["got"][n] - exact))),
+                         float(np.max(np.abs(ref - exact)))))
+            n += 1
+        res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "sequences/s", "cores": 1,
+                               "kind": "port",
+                               "sample": f"{n} q4_matmul_vec calls (8192 -> 2816), one thread"}
+        res["parity_sample"] = {"max_abs_err_vs_cpu_fp32": float(f"{max(e[0] for e in errs):.3g}"),
+                                "max_abs_err_vs_float64": float(f"{max(e[1] for e in errs):.3g}"),
+                                "cpu_fp32_vs_float64": float(f"{max(e[2] for e in errs):.3g}")}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -866,9 +937,10 @@ def main() -> int:
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="BASELINE.json configuration (2, the default, is the headline)")
-    ap.add_argument("--leg", choices=["producer", "lsa"], default=None,
+    ap.add_argument("--leg", choices=["producer", "lsa", "wo"], default=None,
                     help="measure a path beside the configurations instead: 'producer' = "
-                         "pkv_append_qkv (norm + RoPE + append), 'lsa' = pkv_attend_sparse")
+                         "pkv_append_qkv (norm + RoPE + append), 'lsa' = pkv_attend_sparse, "
+                         "'wo' = pkv_q4_matmul")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -888,7 +960,7 @@ def main() -> int:
         print("bench.py needs a GPU: no HIP device visible", file=sys.stderr)
         return 1
     if args.leg is not None:
-        leg = {"producer": bench_producer, "lsa": bench_lsa}[args.leg]
+        leg = {"producer": bench_producer, "lsa": bench_lsa, "wo": bench_wo}[args.leg]
         print(json.dumps(leg(args, log)), flush=True)
         return 0
     legs = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}

@@ -247,6 +247,23 @@ int32_t pkv_paged_attention_layer(void* stream, const float* q, const void* k_po
                                   int32_t num_blocks, int32_t kv_dtype, void* workspace,
                                   size_t workspace_bytes);
 
+/* Bytes of workspace pkv_q4_matmul needs (split-K partials); 0 on invalid sizes. */
+size_t pkv_q4_matmul_workspace_size(int32_t c_in, int32_t c_out, int32_t batch);
+
+/* Wo projection after attention -- batched Q4_0 matrix-vector products.
+ * Replaces q4_matmul_vec (moe_kernels.mojo:59-163) as called on attn_out
+ * (model_speculative_moe_batched.mojo:2011-2051), for `batch` input vectors at once:
+ * out[s][r] = sum_k W[r][k] * x[s][k], x fp32 [batch][c_in] (e.g. pkv_attend's output,
+ * c_in = num_heads * head_dim), out fp32 [batch][c_out]. W is in the reference's Q4_0
+ * block-32 form (moe_kernels.mojo:7-57): w_packed uint8 [c_out][c_in / 2] (byte j of a
+ * block: element 2j in the low nibble, 2j + 1 in the high one; value nibble - 8) and
+ * scales fp32 [c_out][c_in / 32]. c_in % 32 == 0, batch <= 64; w_packed and scales 4-byte,
+ * x 16-byte aligned. Products are exact (bf16 matrix cores on a three-way split of x) and
+ * sums are fp32. One or two launches. */
+int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales, const float* x,
+                      int32_t c_in, int32_t c_out, int32_t batch, float* out, void* workspace,
+                      size_t workspace_bytes);
+
 /* Message for the calling thread's most recent error ("" if none). */
 const char* pkv_last_error(void);
 

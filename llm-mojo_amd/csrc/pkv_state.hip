@@ -253,13 +253,6 @@ struct QkvArgs {
     float inv_freq[256];  // base^(2i / rope_dim), i < rotary_half, correctly rounded fp32
 };
 
-__device__ inline uint16_t f32_to_bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-
 template <int E>
 __device__ inline void store_row(void* base, size_t elem, bool bf16, const float (&x)[E]) {
     if (bf16) {

@@ -65,6 +65,10 @@ def _L():
                                           i32, vp, vp, i32, vp, ctypes.c_int, ctypes.c_int]),
             "pkvo_attend_sparse_f64": (None, [ctypes.c_int, i32, i32, i32, i32, f32, vp, vp, vp,
                                               vp, i32, vp, vp, i32, vp]),
+            "pkvo_quantize_q4_0": (None, [vp, vp, vp, i64]),
+            "pkvo_q4_matmul_vec": (None, [vp, vp, vp, vp, i64, i64]),
+            "pkvo_scalar_q4": (None, [vp, vp, vp, vp, i64, i64]),
+            "pkvo_q4_matmul_f64": (None, [vp, vp, vp, vp, i64, i64]),
             "pkvo_append_qkv_f64": (None, [i32, i32, i32, ctypes.c_int, vp, vp, i32, vp, vp, vp,
                                            vp, vp, i32, i32, vp, vp, vp]),
             "pkvo_append_qkv": (None, [ctypes.c_int, i32, i32, i32, i32, i32, i32, ctypes.c_int,
@@ -298,6 +302,47 @@ def attend_sparse_f64(q, k_pool, v_pool, tables, keys, key_off, num_heads, num_k
     _L().pkvo_attend_sparse_f64(_dtype_of(k_pool), num_heads, num_kv_heads, head_dim, block_size,
                                 scale, _p(q), _p(k_pool), _p(v_pool), _p(tables), tables.shape[1],
                                 _p(keys), _p(key_off), batch, _p(out))
+    return out
+
+
+def quantize_q4_0(w) -> tuple[np.ndarray, np.ndarray]:
+    """moe_kernels.mojo:7-57 on a [rows][c_in] fp32 matrix: (packed uint8 [rows][c_in/2],
+    scales fp32 [rows][c_in/32])."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, c_in = w.shape
+    packed = np.empty((rows, c_in // 2), np.uint8)
+    scales = np.empty((rows, c_in // 32), np.float32)
+    _L().pkvo_quantize_q4_0(_p(w), _p(packed), _p(scales), w.size)
+    return packed, scales
+
+
+def q4_matmul_vec(packed, scales, x) -> np.ndarray:
+    """moe_kernels.mojo:59-163: out[r] for one input vector x [c_in]."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(packed.shape[0], np.float32)
+    _L().pkvo_q4_matmul_vec(_p(packed), _p(scales), _p(x), _p(out), x.size, packed.shape[0])
+    return out
+
+
+def scalar_q4(packed, scales, x) -> np.ndarray:
+    """test_q4_4row_tiling.mojo:14-34 (independent scalar oracle)."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(packed.shape[0], np.float32)
+    _L().pkvo_scalar_q4(_p(packed), _p(scales), _p(x), _p(out), x.size, packed.shape[0])
+    return out
+
+
+def q4_matmul_f64(packed, scales, x) -> np.ndarray:
+    """The dequantized product in float64."""
+    packed = np.ascontiguousarray(packed, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(packed.shape[0], np.float64)
+    _L().pkvo_q4_matmul_f64(_p(packed), _p(scales), _p(x), _p(out), x.size, packed.shape[0])
     return out
 
 

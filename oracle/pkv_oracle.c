@@ -40,6 +40,11 @@
  *   pkvo_lsa_sparse_paged_attention  lsa_core.mojo:630-680 (attention over an explicit key list)
  *   pkvo_lsa_expand_buckets          lsa_core.mojo:573-604 (bucket members, window, sinks)
  *   pkvo_attend_sparse / _f64        lsa_sparse_paged_attention per sequence of a batch
+ *   pkvo_quantize_q4_0               moe_kernels.mojo:7-57 (Q4_0 block-32 quantization)
+ *   pkvo_q4_matmul_vec               moe_kernels.mojo:59-163 (the Wo projection after attention,
+ *                                    model_speculative_moe_batched.mojo:2011-2051)
+ *   pkvo_scalar_q4                   test_q4_4row_tiling.mojo:14-34 (scalar dequantizing oracle)
+ *   pkvo_q4_matmul_f64               the same product in float64
  *   pkvo_rollback                    retire :3626-3628 / reset :2424-2439 (ascending free order);
  *                                    truncation after rejected drafts has no reference code and
  *                                    follows the build's definition (keep ceil(len/bs) blocks,
@@ -817,6 +822,104 @@ void pkvo_attend_sparse_f64(int dtype, int32_t num_heads, int32_t num_kv_heads, 
         free(tab);
     }
     free(qs);
+}
+
+/* ----------------------------------------------------- moe_kernels.mojo:7-57
+ * Q4_0 block-32: per block of 32 values, scale = max(max|v| / 7, 1e-5); q = clamp(round(v /
+ * scale), -8, 7) + 8; byte j of the block's 16 holds element 2j in its low nibble and
+ * element 2j + 1 in its high nibble. round() is restated as roundf (halves away from
+ * zero); the rounding of exact halves is not pinned to Mojo's.                       */
+void pkvo_quantize_q4_0(const float* src, uint8_t* packed, float* scales, int64_t n) {
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const float* v = src + b * 32;
+        float max_abs = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            float a = fabsf(v[i]);
+            if (a > max_abs) max_abs = a;
+        }
+        float scale = max_abs / 7.0f;
+        if (scale < 1e-5f) scale = 1e-5f;
+        scales[b] = scale;
+        float inv = 1.0f / scale;
+        for (int j = 0; j < 16; ++j) {
+            float q0 = roundf(v[2 * j] * inv), q1 = roundf(v[2 * j + 1] * inv);
+            q0 = q0 < -8.0f ? -8.0f : (q0 > 7.0f ? 7.0f : q0);
+            q1 = q1 < -8.0f ? -8.0f : (q1 > 7.0f ? 7.0f : q1);
+            packed[b * 16 + j] = (uint8_t)((uint8_t)(q0 + 8.0f) | ((uint8_t)(q1 + 8.0f) << 4));
+        }
+    }
+}
+
+/* SIMD[f32, 16].reduce_add as a halving tree. */
+static inline float reduce_add16(const float* a) {
+    float h[8];
+    for (int j = 0; j < 8; ++j) h[j] = a[j] + a[j + 8];
+    return reduce_add8(h);
+}
+
+/* ---------------------------------------------------- moe_kernels.mojo:59-163
+ * out[r] = sum over blocks b of the dequantized row times x: x is split into its even and
+ * odd elements per block ("dual-space deinterleave"); per block and lane j < 16,
+ * acc[j] = fma(we[j], xe[j], fma(wo[j], xo[j], acc[j])) with we / wo = (nibble - 8) * scale;
+ * finally out[r] = reduce_add(acc). The reference's 2-row and 1-row loops do the same per
+ * row.                                                                              */
+void pkvo_q4_matmul_vec(const uint8_t* w_packed, const float* scales, const float* x, float* out,
+                        int64_t c_in, int64_t c_out) {
+    int64_t cp = c_in / 2, nb = c_in / 32;
+    for (int64_t r = 0; r < c_out; ++r) {
+        float acc[16] = {0};
+        for (int64_t b = 0; b < nb; ++b) {
+            float sc = scales[r * nb + b];
+            const uint8_t* bytes = w_packed + r * cp + b * 16;
+            for (int j = 0; j < 16; ++j) {
+                float we = (float)((int)(bytes[j] & 15) - 8) * sc;
+                float wo = (float)((int)(bytes[j] >> 4) - 8) * sc;
+                float xe = x[b * 32 + 2 * j], xo = x[b * 32 + 2 * j + 1];
+                acc[j] = fmaf(we, xe, fmaf(wo, xo, acc[j]));
+            }
+        }
+        out[r] = reduce_add16(acc);
+    }
+}
+
+/* -------------------------------------------- test_q4_4row_tiling.mojo:14-34
+ * Independent scalar dequantizing oracle: per block, sum w_lo * x[2j] + w_hi * x[2j+1]
+ * over the 16 bytes, times the scale, accumulated over blocks.                       */
+void pkvo_scalar_q4(const uint8_t* w_packed, const float* scales, const float* x, float* out,
+                    int64_t c_in, int64_t c_out) {
+    int64_t cp = c_in / 2, nb = c_in / 32;
+    for (int64_t r = 0; r < c_out; ++r) {
+        float row_sum = 0.0f;
+        for (int64_t b = 0; b < nb; ++b) {
+            float sc = scales[r * nb + b];
+            float blk = 0.0f;
+            for (int j = 0; j < 16; ++j) {
+                int byte = w_packed[r * cp + b * 16 + j];
+                float w_lo = (float)((byte & 15) - 8), w_hi = (float)((byte >> 4) - 8);
+                blk = blk + (w_lo * x[b * 32 + 2 * j] + w_hi * x[b * 32 + 2 * j + 1]);
+            }
+            row_sum = row_sum + blk * sc;
+        }
+        out[r] = row_sum;
+    }
+}
+
+/* The dequantized product in float64 (the exact value both fp32 forms approximate).  */
+void pkvo_q4_matmul_f64(const uint8_t* w_packed, const float* scales, const float* x,
+                        double* out, int64_t c_in, int64_t c_out) {
+    int64_t cp = c_in / 2, nb = c_in / 32;
+    for (int64_t r = 0; r < c_out; ++r) {
+        double sum = 0.0;
+        for (int64_t b = 0; b < nb; ++b) {
+            double sc = scales[r * nb + b];
+            for (int j = 0; j < 16; ++j) {
+                int byte = w_packed[r * cp + b * 16 + j];
+                sum += ((double)((byte & 15) - 8) * sc) * (double)x[b * 32 + 2 * j] +
+                       ((double)((byte >> 4) - 8) * sc) * (double)x[b * 32 + 2 * j + 1];
+            }
+        }
+        out[r] = sum;
+    }
 }
 
 /* ------------------------------------------------------- rollback / retire

@@ -113,3 +113,12 @@ def test_ring_mode_rejections():
     full_causal = list(args)
     full_causal[10] = 0  # pos 2000 with no window: 2001 keys > ring
     assert L.pkv_paged_attention_layer(*full_causal) == lib.PKV_ERR_INVALID
+
+
+def test_q4_matmul_rejections_before_launch():
+    L = lib.load()
+    assert L.pkv_q4_matmul(None, 4, 4, 16, 100, 8, 1, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID
+    assert L.pkv_q4_matmul(None, 4, 4, 16, 128, 8, 65, 16, 16, 1 << 20) == lib.PKV_ERR_UNSUPPORTED
+    assert L.pkv_q4_matmul(None, 4, 4, 16, 4096, 8, 8, 16, 16, 16) == lib.PKV_ERR_WORKSPACE
+    assert L.pkv_q4_matmul(None, 4, 4, 8, 4096, 8, 8, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID  # x alignment
+    assert L.pkv_q4_matmul_workspace_size(4096, 2816, 32) == 16 * 32 * 2816 * 4
