@@ -761,7 +761,7 @@ def bench_lsa(args, log):
     key list comes from lsa_expand_buckets with the engine's defaults
     (…batched.mojo:1261-1264: top_k 256 from 20 picked buckets of up to 32 members, window
     128, 4 sinks), so a query attends about 390 keys scattered over its context."""
-    from pkv import LayerSpec, PagedKVCache, hip, lsa_expand_buckets, synth
+    from pkv import LayerSpec, LSABucketCache, PagedKVCache, hip, lsa_expand_buckets, synth
 
     HQ, HKV, D, BS, B = 16, 2, 512, 16, 32
     TOP_K, PICK, CAP, WINDOW, SINKS = 256, 20, 32, 128, 4
@@ -773,6 +773,11 @@ def bench_lsa(args, log):
     perm = rng.permutation(nb).astype(np.int32)
     tables = np.zeros((B, stride), np.int32)
     lists, off = [], [0]
+    lsa = LSABucketCache(B, 8192 + 512)  # one index instance per sequence
+    c_sizes = np.zeros((B, lsa.max_buckets), np.int32)
+    c_members = np.zeros((B, lsa.max_buckets, CAP), np.int32)
+    c_picked = np.zeros((B, PICK), np.int32)
+    c_npicked = np.zeros(B, np.int32)
     o = 0
     for s in range(B):
         tables[s, :blocks[s]] = perm[o:o + blocks[s]]
@@ -784,6 +789,8 @@ def bench_lsa(args, log):
         for b in range(nbk):
             members[b, :sizes[b]] = rng.choice(pos + 1, sizes[b], replace=False)
         picked = rng.choice(nbk, min(PICK, nbk), replace=False)
+        c_sizes[s, :nbk], c_members[s, :nbk] = sizes, members
+        c_picked[s, :picked.size], c_npicked[s] = picked, picked.size
         sel = lsa_expand_buckets(picked, sizes, members, pos, TOP_K, SINKS, WINDOW)
         lists.append(sel)
         off.append(off[-1] + sel.size)
@@ -815,6 +822,37 @@ def bench_lsa(args, log):
     _timed(hip, stream, args.steps, lambda i: step(i, ev))
     dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
     got = out.numpy()
+    # The same lists built on the device (pkv_lsa_expand over the bucket cache), alone and
+    # chained into the attention.
+    lsa.sizes.upload_at(0, c_sizes)
+    lsa.members.upload_at(0, c_members)
+    dev = [hip.DeviceArray.from_numpy(a) for a in (np.arange(B, dtype=np.int32), c_picked,
+                                                   c_npicked, ctx.astype(np.int32))]
+    per = LSABucketCache.max_keys(TOP_K, SINKS, WINDOW)
+    xk, xo, xs = (hip.DeviceArray((B * per,), np.int32), hip.DeviceArray((B + 1,), np.int32),
+                  hip.DeviceArray((B,), np.int32))
+
+    def expand(i, events=None, chain=False):
+        if events:
+            events[i][0].record(stream)
+        lsa.expand(*dev, TOP_K, SINKS, WINDOW, xk, xo, xs, stream=stream)
+        if chain:
+            cache.attend_sparse(0, q, xk, xo.ptr, per, out)
+        if events:
+            events[i][1].record(stream)
+
+    for i in range(args.warmup):
+        expand(i, chain=True)
+    _timed(hip, stream, args.steps, lambda i: expand(i, ev))
+    dur_x = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    _timed(hip, stream, args.steps, lambda i: expand(i, ev, chain=True))
+    dur_xa = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    n_off = xo.numpy()
+    device_lists_equal = bool(np.array_equal(n_off, off) and
+                              np.array_equal(xk.numpy()[:n_off[-1]], keys) and
+                              not xs.numpy().any())
+    chained = out.numpy()
+    chained_diff = float(np.max(np.abs(chained - got) / (np.abs(got) + 1e-3)))
     # each listed key's K and V slices once, Q in / O out, key list and table entries
     nbytes = int(n_keys.sum()) * (2 * HKV * D * 4 + 8) + B * 2 * HQ * D * 4
     res = _line("LSA sparse paged attention tokens/s (32 sequences, ~390-key lists, 16q/2kv/512)",
@@ -826,7 +864,11 @@ def bench_lsa(args, log):
                 _roofline(nbytes, dur, "stream_attend_kernel<512, float, 2, 4, sparse> + "
                                        "stream_merge_kernel<512, double>"),
                 {"keys_per_sequence_mean": round(float(n_keys.mean()), 1),
-                 "max_keys": max_keys})
+                 "max_keys": max_keys,
+                 "device_expand": {"us_per_call": round(dur_x * 1e3, 2),
+                                   "expand_plus_attend_us": round(dur_xa * 1e3, 2),
+                                   "lists_equal_host_expand": device_lists_equal,
+                                   "chained_max_rel_diff": float(f"{chained_diff:.3g}")}})
     if args.cpu_seconds > 0:
         from oracle import oracle as O
 

@@ -60,6 +60,7 @@ extern "C" {
 #define PKV_SEQ_BAD_BLOCK (-3)     /* a table entry outside [0, num_blocks)         */
 #define PKV_SEQ_FREE_OVERFLOW (-4) /* freeing would overflow the free list          */
 #define PKV_SEQ_BAD_ARGS (-5)      /* token range outside [0, total_rows) or > max_new */
+#define PKV_SEQ_BAD_INDEX (-6)     /* LSA index or bucket id out of range (skipped)   */
 
 /* Layer geometry and numerics, shared by every entry point.
  * Mirrors paged_attention_layer's scalar arguments (attention.mojo:240-256). */
@@ -189,6 +190,59 @@ int32_t pkv_attend_sparse(void* stream, const pkv_params* p, const float* q, con
                           const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                           const int32_t* keys, const int32_t* key_off, int32_t max_keys,
                           int32_t batch, float* out, void* workspace, size_t workspace_bytes);
+
+/* LSA bucket cache in device memory. The reference keeps one LSALayerIndex per kv slot and
+ * global-layer group (model_speculative_moe_batched.mojo:1885-1888, :632); its bucket
+ * cache (lsa_core.mojo:222-233) lives here as index instance i = kv_slot * 5 + group:
+ *   int32 sizes[num_indices][max_buckets]        member count per bucket (<= 32);
+ *   int32 members[num_indices][max_buckets][32]  token positions, in append order;
+ *   int32 closed_blocks[num_indices], total_tokens[num_indices];
+ * max_buckets = ceil(max_capacity / 512) * 32. Filling a block's buckets when its 512
+ * tokens close (Ward clustering, lsa_core.mojo:325-518) and picking buckets
+ * (select_top_p, :520-566) stay with the index on the host, which copies a closed
+ * block's 32 sizes and member rows in. */
+
+/* Longest key list pkv_lsa_expand can build: max(top_k, 1) + window_size + sink_size
+ * (-1 if that overflows int32). Use it for keys_capacity / batch and as
+ * pkv_attend_sparse's max_keys. */
+int32_t pkv_lsa_max_keys(int32_t top_k, int32_t sink_size, int32_t window_size);
+
+/* Bytes of workspace pkv_lsa_expand needs (the lists at a fixed stride, then their
+ * lengths); 0 on invalid sizes. */
+size_t pkv_lsa_expand_workspace_size(int32_t batch, int32_t top_k, int32_t sink_size,
+                                     int32_t window_size);
+
+/* LSALayerIndex.expand_buckets (lsa_core.mojo:568-604) for a batch of queries, writing
+ * the CSR key lists pkv_attend_sparse takes. Sequence s uses index instance
+ * index_ids[s] and its picked buckets picked[s * picked_stride + j], j < n_picked[s], in
+ * order. Its list is the members of those buckets that lie in [sink_size, window_start),
+ * in order, up to top_k of them (the reference stops once the list holds top_k after an
+ * append, so top_k <= 0 keeps one); then the window [window_start, pos[s]] with
+ * window_start = max(0, pos[s] + 1 - window_size); then the sinks [0, min(sink_size,
+ * window_start, pos[s] + 1)). keys[key_off[s] .. key_off[s+1]) receives it; key_off is
+ * int32 [batch + 1]. keys_capacity (int32 entries) must be >= batch *
+ * pkv_lsa_max_keys(). status[s] = PKV_SEQ_BAD_INDEX when the index id, n_picked or a
+ * bucket id is out of range (the offending part is skipped), else PKV_SEQ_OK. All arrays
+ * are device memory; batch <= 1024; sink_size, window_size >= 0. Two launches. */
+int32_t pkv_lsa_expand(void* stream, const int32_t* index_ids, const int32_t* picked,
+                       int32_t picked_stride, const int32_t* n_picked, const int32_t* pos,
+                       int32_t top_k, int32_t sink_size, int32_t window_size, int32_t batch,
+                       const int32_t* sizes, const int32_t* members, int32_t num_indices,
+                       int32_t max_buckets, int32_t* keys, int32_t* key_off,
+                       int64_t keys_capacity, int32_t* status, void* workspace,
+                       size_t workspace_bytes);
+
+/* LSALayerIndex.rollback_to (lsa_core.mojo:287-303) -- and reset (:281-285) for targets
+ * <= 0 -- as the engine calls it after verify (model_speculative_moe_batched.mojo:3368,
+ * rollback_to(seq.pos) for each of the sequence's groups) and on admission (:2415,
+ * :2432). Entry k applies to instance index_ids[k] with target_tokens[k], entries in
+ * order: total_tokens = min(target, max_capacity); every closed 512-token block past
+ * total_tokens / 512 reopens and its 32 buckets get size 0 (members and centroids stay, as
+ * in the reference). Out-of-range ids are skipped. Device arrays; one launch. */
+int32_t pkv_lsa_rollback(void* stream, const int32_t* index_ids, const int32_t* target_tokens,
+                         int32_t count, int32_t num_indices, int32_t max_capacity,
+                         int32_t max_buckets, int32_t* closed_blocks, int32_t* total_tokens,
+                         int32_t* sizes);
 
 /* K3 -- chunked-prefill attention over bf16 pages with bf16 MFMA (fp32 accumulation).
  * Replaces the engine's per-token prefill loop (append one token, then one

@@ -347,6 +347,80 @@ def lsa_expand_buckets(picked, sizes, members, pos: int, top_k: int, sink_size: 
     return np.asarray(sel, np.int32)
 
 
+class LSABucketCache:
+    """The bucket caches of the engine's LSA indices (one LSALayerIndex per kv slot and
+    global-layer group, model_speculative_moe_batched.mojo:1885-1888, :632) held in device
+    memory: per instance the member counts and member positions of its buckets
+    (lsa_core.mojo:222-233), its closed cluster blocks and tokens appended. expand() is
+    expand_buckets for a batch of queries, writing pkv_attend_sparse's key lists on the
+    device; rollback_to() is rollback_to / reset for a batch of instances. Filling a block's
+    buckets (Ward clustering on block close) and picking buckets stay with the index on the
+    host, which copies a closed block in with load_block()."""
+
+    BUCKET_CAP = 32
+    BLOCK_BUCKETS = 32
+
+    def __init__(self, num_indices: int, max_capacity: int = 131072):
+        self.num_indices = num_indices
+        self.max_capacity = max_capacity
+        self.max_buckets = (max_capacity + 511) // 512 * self.BLOCK_BUCKETS
+        self.sizes = hip.DeviceArray((num_indices, self.max_buckets), np.int32, zero=True)
+        self.members = hip.DeviceArray((num_indices, self.max_buckets, self.BUCKET_CAP),
+                                       np.int32, zero=True)
+        self.closed_blocks = hip.DeviceArray((num_indices,), np.int32, zero=True)
+        self.total_tokens = hip.DeviceArray((num_indices,), np.int32, zero=True)
+        self.workspace = None
+
+    def load_block(self, index: int, block: int, sizes, members) -> None:
+        """Copy one closed cluster block's 32 bucket sizes and [32][32] member rows in."""
+        sizes = np.ascontiguousarray(sizes, np.int32).reshape(self.BLOCK_BUCKETS)
+        members = np.ascontiguousarray(members, np.int32).reshape(self.BLOCK_BUCKETS,
+                                                                   self.BUCKET_CAP)
+        b0 = (index * self.max_buckets + block * self.BLOCK_BUCKETS)
+        self.sizes.upload_at(b0 * 4, sizes)
+        self.members.upload_at(b0 * self.BUCKET_CAP * 4, members)
+
+    @staticmethod
+    def max_keys(top_k: int, sink_size: int, window_size: int) -> int:
+        """Longest list expand() builds (pkv_lsa_max_keys)."""
+        return lib.load().pkv_lsa_max_keys(top_k, sink_size, window_size)
+
+    def expand(self, index_ids, picked, n_picked, pos, top_k: int, sink_size: int,
+               window_size: int, keys=None, key_off=None, status=None,
+               stream: hip.Stream | None = None):
+        """expand_buckets (lsa_core.mojo:568-604) for sequence s = 0..batch-1 on instance
+        index_ids[s], buckets picked[s][:n_picked[s]]; device int32 arrays. Returns the
+        device arrays (keys, key_off, status) for pkv_attend_sparse."""
+        batch = index_ids.shape[0]
+        per = self.max_keys(top_k, sink_size, window_size)
+        if per < 0:
+            raise lib.PkvError(lib.PKV_ERR_INVALID, "pkv_lsa_max_keys", "overflow")
+        if keys is None:
+            keys = hip.DeviceArray((batch * per,), np.int32)
+        if key_off is None:
+            key_off = hip.DeviceArray((batch + 1,), np.int32)
+        if status is None:
+            status = hip.DeviceArray((batch,), np.int32)
+        stride = picked.shape[1] if len(picked.shape) > 1 else 0
+        need = lib.load().pkv_lsa_expand_workspace_size(batch, top_k, sink_size, window_size)
+        if self.workspace is None or self.workspace.nbytes < need:
+            self.workspace = hip.DeviceArray((need,), np.uint8)
+        lib.call("pkv_lsa_expand", stream.handle if stream else None, _ptr(index_ids),
+                 _ptr(picked), stride, _ptr(n_picked), _ptr(pos), top_k, sink_size,
+                 window_size, batch, self.sizes.ptr, self.members.ptr, self.num_indices,
+                 self.max_buckets, _ptr(keys), _ptr(key_off), keys.nbytes // 4, _ptr(status),
+                 self.workspace.ptr, self.workspace.nbytes)
+        return keys, key_off, status
+
+    def rollback_to(self, index_ids, target_tokens, stream: hip.Stream | None = None) -> None:
+        """rollback_to (lsa_core.mojo:287-303; reset for targets <= 0) of instance
+        index_ids[k] to target_tokens[k], entries in order (device int32 arrays)."""
+        lib.call("pkv_lsa_rollback", stream.handle if stream else None, _ptr(index_ids),
+                 _ptr(target_tokens), index_ids.shape[0], self.num_indices, self.max_capacity,
+                 self.max_buckets, self.closed_blocks.ptr, self.total_tokens.ptr,
+                 self.sizes.ptr)
+
+
 def paged_attention_layer(q, k_pool, v_pool, block_table, block_size: int, pos: int,
                           num_heads: int, num_kv_heads: int, head_dim: int, window: int,
                           attn_out, ring_size: int = 0, ring_base: int = 0, *,

@@ -24,6 +24,7 @@ PKV_SEQ_TABLE_FULL = -2
 PKV_SEQ_BAD_BLOCK = -3
 PKV_SEQ_FREE_OVERFLOW = -4
 PKV_SEQ_BAD_ARGS = -5
+PKV_SEQ_BAD_INDEX = -6
 
 # Every exported entry point and its (restype, argtypes).
 _vp, _i32, _sz, _f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t, ctypes.c_float
@@ -63,6 +64,11 @@ PROTOTYPES = {
                                  _vp, _sz]),
     "pkv_q4_matmul_workspace_size": (_sz, [_i32, _i32, _i32]),
     "pkv_q4_matmul": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _sz]),
+    "pkv_lsa_max_keys": (_i32, [_i32, _i32, _i32]),
+    "pkv_lsa_expand_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
+    "pkv_lsa_expand": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp,
+                              _i32, _i32, _vp, _vp, ctypes.c_int64, _vp, _vp, _sz]),
+    "pkv_lsa_rollback": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "pkv_last_error": (ctypes.c_char_p, []),
     "pkv_version": (_i32, []),
 }

@@ -61,6 +61,8 @@ def _L():
             "pkvo_lsa_sparse_paged_attention": (None, [vp, vp, vp, ctypes.c_int, vp, i64, vp, i64,
                                                        i64, i64, i64, vp, vp, vp, ctypes.c_int]),
             "pkvo_lsa_expand_buckets": (i64, [vp, i64, vp, vp, i64, i64, i64, i64, i64, vp]),
+            "pkvo_lsa_reset": (None, [i64, vp, vp, vp]),
+            "pkvo_lsa_rollback_to": (None, [i64, i64, vp, vp, vp, i64]),
             "pkvo_attend_sparse": (None, [ctypes.c_int, i32, i32, i32, i32, f32, vp, vp, vp, vp,
                                           i32, vp, vp, i32, vp, ctypes.c_int, ctypes.c_int]),
             "pkvo_attend_sparse_f64": (None, [ctypes.c_int, i32, i32, i32, i32, f32, vp, vp, vp,
@@ -269,10 +271,32 @@ def lsa_expand_buckets(picked, sizes, members, pos, top_k, sink_size, window_siz
     picked = np.ascontiguousarray(np.asarray(picked, dtype=np.int64))
     sizes = np.ascontiguousarray(np.asarray(sizes, dtype=np.int64))
     members = np.ascontiguousarray(np.asarray(members, dtype=np.int64))
-    out = np.empty(top_k + window_size + sink_size + 1, np.int64)
+    out = np.empty(max(top_k, 1) + max(window_size, 0) + max(sink_size, 0), np.int64)
     n = _L().pkvo_lsa_expand_buckets(_p(picked), picked.size, _p(sizes), _p(members),
                                      members.shape[1], pos, top_k, sink_size, window_size, _p(out))
     return out[:n].copy()
+
+
+class LsaIndexState:
+    """The integer state of one LSALayerIndex (lsa_core.mojo:222-233, :246-262): closed
+    cluster blocks, tokens appended, and per-bucket member counts."""
+
+    def __init__(self, max_capacity: int):
+        self.max_capacity = max_capacity
+        self.max_buckets = (max_capacity + 511) // 512 * 32
+        self.closed_blocks = np.zeros(1, np.int64)
+        self.total_tokens = np.zeros(1, np.int64)
+        self.sizes = np.zeros(self.max_buckets, np.int64)
+
+    def reset(self):
+        """lsa_core.mojo:281-285."""
+        _L().pkvo_lsa_reset(self.max_buckets, _p(self.closed_blocks), _p(self.total_tokens),
+                            _p(self.sizes))
+
+    def rollback_to(self, target_tokens: int):
+        """lsa_core.mojo:287-303."""
+        _L().pkvo_lsa_rollback_to(self.max_capacity, self.max_buckets, _p(self.closed_blocks),
+                                  _p(self.total_tokens), _p(self.sizes), target_tokens)
 
 
 def attend_sparse(q, k_pool, v_pool, tables, keys, key_off, num_heads, num_kv_heads, head_dim,

@@ -40,6 +40,8 @@
  *   pkvo_lsa_sparse_paged_attention  lsa_core.mojo:630-680 (attention over an explicit key list)
  *   pkvo_lsa_expand_buckets          lsa_core.mojo:573-604 (bucket members, window, sinks)
  *   pkvo_attend_sparse / _f64        lsa_sparse_paged_attention per sequence of a batch
+ *   pkvo_lsa_reset                   LSALayerIndex.reset, lsa_core.mojo:281-285
+ *   pkvo_lsa_rollback_to             LSALayerIndex.rollback_to, lsa_core.mojo:287-303
  *   pkvo_quantize_q4_0               moe_kernels.mojo:7-57 (Q4_0 block-32 quantization)
  *   pkvo_q4_matmul_vec               moe_kernels.mojo:59-163 (the Wo projection after attention,
  *                                    model_speculative_moe_batched.mojo:2011-2051)
@@ -752,6 +754,36 @@ int64_t pkvo_lsa_expand_buckets(const int64_t* picked, int64_t n_picked, const i
     if (pos + 1 < sink_limit) sink_limit = pos + 1;
     for (int64_t t = 0; t < sink_limit; ++t) out[n++] = t;
     return n;
+}
+
+/* ------------------------------------------------ lsa_core.mojo:281-303
+ * LSALayerIndex.reset and rollback_to on the index's integer state: the number of closed
+ * 512-token cluster blocks, the tokens appended, and the member count of each bucket (32
+ * buckets per block). rollback_to keeps min(target, max_capacity) tokens and reopens every
+ * closed block from that count / 512 on, emptying its buckets; members and centroids are
+ * left in place. (The reference asserts that at most one block reopens, :294-298, a
+ * debug_assert; its loop handles any number, and so does this one.)                   */
+void pkvo_lsa_reset(int64_t max_buckets, int64_t* closed_blocks, int64_t* total_tokens,
+                    int64_t* sizes) {
+    *closed_blocks = 0;
+    *total_tokens = 0;
+    for (int64_t i = 0; i < max_buckets; ++i) sizes[i] = 0;
+}
+
+void pkvo_lsa_rollback_to(int64_t max_capacity, int64_t max_buckets, int64_t* closed_blocks,
+                          int64_t* total_tokens, int64_t* sizes, int64_t target_tokens) {
+    if (target_tokens <= 0) {
+        pkvo_lsa_reset(max_buckets, closed_blocks, total_tokens, sizes);
+        return;
+    }
+    const int64_t clamped = target_tokens < max_capacity ? target_tokens : max_capacity;
+    *total_tokens = clamped;
+    const int64_t valid_closed = clamped / 512;
+    while (*closed_blocks > valid_closed) {
+        *closed_blocks -= 1;
+        const int64_t base = *closed_blocks * 32;
+        for (int64_t i = 0; i < 32; ++i) sizes[base + i] = 0;
+    }
 }
 
 /* ------------------------------------------------ batched sparse attention

@@ -122,3 +122,35 @@ def test_q4_matmul_rejections_before_launch():
     assert L.pkv_q4_matmul(None, 4, 4, 16, 4096, 8, 8, 16, 16, 16) == lib.PKV_ERR_WORKSPACE
     assert L.pkv_q4_matmul(None, 4, 4, 8, 4096, 8, 8, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID  # x alignment
     assert L.pkv_q4_matmul_workspace_size(4096, 2816, 32) == 16 * 32 * 2816 * 4
+
+
+def test_lsa_cache_rejections_before_launch():
+    L = lib.load()
+    assert L.pkv_lsa_max_keys(64, 4, 16) == 84
+    assert L.pkv_lsa_max_keys(0, 4, 16) == 21 and L.pkv_lsa_max_keys(-3, -1, -1) == 1
+    assert L.pkv_lsa_max_keys(2**31 - 1, 2**31 - 1, 1) == -1
+    p = 16  # a stand-in non-null address; none of these calls reaches a launch
+    args = dict(ids=p, picked=p, stride=8, npk=p, pos=p, top_k=64, sink=4, window=16, batch=4,
+                sizes=p, members=p, nidx=6, maxb=128, keys=p, off=p, cap=4 * 84, status=p,
+                ws=p, ws_bytes=(4 * 84 + 4) * 4)
+    assert L.pkv_lsa_expand_workspace_size(4, 64, 4, 16) == (4 * 84 + 4) * 4
+    assert L.pkv_lsa_expand_workspace_size(0, 64, 4, 16) == 0
+
+    def expand(**kw):
+        a = {**args, **kw}
+        return L.pkv_lsa_expand(None, a["ids"], a["picked"], a["stride"], a["npk"], a["pos"],
+                                a["top_k"], a["sink"], a["window"], a["batch"], a["sizes"],
+                                a["members"], a["nidx"], a["maxb"], a["keys"], a["off"],
+                                a["cap"], a["status"], a["ws"], a["ws_bytes"])
+    assert expand(batch=0) == lib.PKV_ERR_INVALID
+    assert expand(batch=1025) == lib.PKV_ERR_UNSUPPORTED
+    assert expand(keys=None) == lib.PKV_ERR_INVALID
+    assert expand(window=-1) == lib.PKV_ERR_INVALID
+    assert expand(nidx=0) == lib.PKV_ERR_INVALID
+    assert expand(cap=4 * 84 - 1) == lib.PKV_ERR_WORKSPACE
+    assert expand(ws_bytes=(4 * 84 + 4) * 4 - 1) == lib.PKV_ERR_WORKSPACE
+    assert expand(ws=None) == lib.PKV_ERR_INVALID
+    assert L.pkv_lsa_rollback(None, p, p, 3, 6, 2048, 100, p, p, p) == lib.PKV_ERR_INVALID
+    assert L.pkv_lsa_rollback(None, p, p, -1, 6, 2048, 128, p, p, p) == lib.PKV_ERR_INVALID
+    assert L.pkv_lsa_rollback(None, None, p, 3, 6, 2048, 128, p, p, p) == lib.PKV_ERR_INVALID
+    assert L.pkv_lsa_rollback(None, None, None, 0, 6, 2048, 128, None, None, None) == lib.PKV_OK
