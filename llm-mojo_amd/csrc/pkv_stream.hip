@@ -667,9 +667,14 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
 //   out = sum_c o_c e^(m_c - M) / (sum_c l_c e^(m_c - M) + 1e-10),  M = max_c m_c,
 // the reference's softmax(x)_i = e^(x_i - max) / (sum + 1e-10). One workgroup per
 // (row, sequence). A NaN m_c marks a piece that met a table entry outside the pool.
+// After the plan, every piece's (m, l) and the o rows of the first kMergeRegs pieces are
+// requested together, so a typical sequence costs two memory round trips.
 template <int D, typename Acc>
 __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
     constexpr int kMaxPieces = 1024;
+    constexpr int kMergeRegs = 16;          // pieces whose o rows are held in registers
+    constexpr int DPT = D / kMergeNT;       // elements per thread
+    static_assert(DPT * kMergeNT == D, "head_dim a multiple of the merge width");
     __shared__ Acc s_w[kMaxPieces];
     __shared__ Acc s_part[kMergeNT / kSW];
     __shared__ int s_nan;
@@ -688,10 +693,28 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
     const Acc* po = static_cast<const Acc*>(a.part_o);
     auto slot_row = [&](int c) -> size_t { return (size_t)(wf + c + s) * a.rows_seq + row; };
 
+    // Requests: (m, l) of this thread's pieces, o of the first kMergeRegs pieces.
+    Acc m0 = (Acc)-INFINITY, l0 = (Acc)0;
+    if (tid < cnt) {
+        m0 = pml[slot_row(tid) * 2];
+        l0 = pml[slot_row(tid) * 2 + 1];
+    }
+    Acc oreg[kMergeRegs][DPT];
+#pragma unroll
+    for (int c = 0; c < kMergeRegs; ++c)
+#pragma unroll
+        for (int e = 0; e < DPT; ++e)
+            oreg[c][e] = c < cnt ? po[slot_row(c) * D + tid + e * kMergeNT] : (Acc)0;
+
     if (tid == 0) s_nan = 0;
     __syncthreads();
     Acc M = (Acc)-INFINITY;
-    for (int c = tid; c < cnt; c += kMergeNT) {
+    if (tid < cnt) {
+        if (m0 != m0) s_nan = 1;
+        M = m0;
+        s_w[tid] = m0;
+    }
+    for (int c = tid + kMergeNT; c < cnt; c += kMergeNT) {
         const Acc m = pml[slot_row(c) * 2];
         if (m != m) s_nan = 1;
         M = fmax(M, m);
@@ -706,7 +729,12 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
     for (int i = 1; i < kMergeNT / kSW; ++i) M = fmax(M, s_part[i]);
     __syncthreads();
     Acc L = (Acc)0;
-    for (int c = tid; c < cnt; c += kMergeNT) {
+    if (tid < cnt) {
+        const Acc wgt = (m0 == (Acc)-INFINITY) ? (Acc)0 : exp_acc(m0 - M);
+        s_w[tid] = wgt;
+        L = l0 * wgt;
+    }
+    for (int c = tid + kMergeNT; c < cnt; c += kMergeNT) {
         const Acc m = s_w[c];
         const Acc wgt = (m == (Acc)-INFINITY) ? (Acc)0 : exp_acc(m - M);
         s_w[c] = wgt;
@@ -721,11 +749,16 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
     for (int i = 0; i < kMergeNT / kSW; ++i) L += s_part[i];
     const Acc inv = (Acc)1 / (L + (Acc)1e-10);
     const bool nan = s_nan != 0;
-    for (int d = tid; d < D; d += kMergeNT) {
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+        const int d = tid + e * kMergeNT;
         Acc o8[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) o8[i] = (Acc)0;
-        int c = 0;
+#pragma unroll
+        for (int c = 0; c < kMergeRegs; ++c)  // pieces past cnt hold weight-free zeros
+            if (c < cnt) o8[c % 8] = fma(s_w[c], oreg[c][e], o8[c % 8]);
+        int c = kMergeRegs;
         for (; c + 8 <= cnt; c += 8) {  // eight independent loads in flight
 #pragma unroll
             for (int i = 0; i < 8; ++i) o8[i] = fma(s_w[c + i], po[slot_row(c + i) * D + d], o8[i]);
