@@ -253,18 +253,20 @@ struct QkvArgs {
     float inv_freq[256];  // base^(2i / rope_dim), i < rotary_half, correctly rounded fp32
 };
 
+// Two fp32 values as packed bf16 bits, rounded to nearest even (v_cvt_pk_bf16_f32).
+__device__ inline uint32_t pack_bf16x2(float x0, float x1) {
+    const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+}
+
 template <int E>
 __device__ inline void store_row(void* base, size_t elem, bool bf16, const float (&x)[E]) {
     if (bf16) {
         uint16_t* d = static_cast<uint16_t*>(base) + elem;
         if constexpr (E == 2) {
-            *reinterpret_cast<uint32_t*>(d) =
-                (uint32_t)f32_to_bf16_rne(x[0]) | ((uint32_t)f32_to_bf16_rne(x[1]) << 16);
+            *reinterpret_cast<uint32_t*>(d) = pack_bf16x2(x[0], x[1]);
         } else {
-            uint2 w;
-            w.x = (uint32_t)f32_to_bf16_rne(x[0]) | ((uint32_t)f32_to_bf16_rne(x[1]) << 16);
-            w.y = (uint32_t)f32_to_bf16_rne(x[2]) | ((uint32_t)f32_to_bf16_rne(x[3]) << 16);
-            *reinterpret_cast<uint2*>(d) = w;
+            *reinterpret_cast<uint2*>(d) = make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]));
         }
     } else {
         float* d = static_cast<float*>(base) + elem;
@@ -292,22 +294,41 @@ __device__ inline void load_vec(const float* p, float (&x)[E]) {
 }
 
 // E elements per lane per half-head: head_dim D = 128 * E. A workgroup of kQkvWaves
-// waves takes kQkvTokens consecutive tokens of one sequence; their (token, head) items go
-// round-robin to the waves, kQkvItems(E) at a time per wave, and every item of a batch is
-// loaded before any is processed (the first batch before the angle tables are built).
+// waves takes one token; its heads go round-robin to the waves, kQkvItems at a time per
+// wave, and every item of a batch is loaded before any is processed (the first batch
+// before the angle table is built). Per batch, the heads' 1 / sqrt(mean + eps) runs once
+// for all of them (lane j takes head j), and the partial-rotary test is a select, so the
+// per-element path has no branch.
 constexpr int kQkvWaves = 8;
-constexpr int kQkvTokens = 1;
-template <int E>
-constexpr int qkv_items() { return 4; }  // 32 heads (16 q + 8 k + 8 v) over 8 waves
+constexpr int kQkvItems = 4;  // 32 heads (16 q + 8 k + 8 v) over 8 waves
+
+// Sum over the 64 lanes, in every lane, without LDS: lane l ^ 32 and l ^ 16 by the
+// permlane swaps (each returns both halves, so a + b pairs every lane with its partner),
+// then l ^ 8 and the 4-lane classes by row rotations, then l ^ 2 and l ^ 1 by quad
+// permutes.
+__device__ inline float wave_sum(float x) {
+    const uint32_t u = __float_as_uint(x);
+    auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    x = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+    const uint32_t u16 = __float_as_uint(x);
+    auto r16 = __builtin_amdgcn_permlane16_swap(u16, u16, false, false);
+    x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));  // row_ror:8
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xf, 0xf, false));  // row_ror:4
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));   // l ^ 2
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));   // l ^ 1
+    return x;
+}
+static_assert(kQkvItems <= kWave, "one lane per head of a batch");
 
 template <int E>
 __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a) {
     constexpr int D = 128 * E;
     constexpr int HALF = D / 2;
     constexpr int NT = kQkvWaves * kWave;
-    constexpr int IPW = qkv_items<E>();
-    __shared__ double s_cos[kQkvTokens][HALF], s_sin[kQkvTokens][HALF];
-    __shared__ long long s_prow[kQkvTokens];  // pool row of the token's K / V, or -1
+    constexpr int IPW = kQkvItems;
+    __shared__ double s_cos[HALF], s_sin[HALF];
+    __shared__ long long s_prow;  // pool row of the token's K / V, or -1
     const AppendArgs& ap = a.ap;
     const int s = blockIdx.y;
     const int tid = threadIdx.x;
@@ -324,17 +345,14 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
         if (blockIdx.x == 0 && tid == 0) ap.status[s] = st;
     }
     if (st == PKV_SEQ_BAD_ARGS) return;  // token range unusable: nothing is read
-    const int b0 = blockIdx.x * kQkvTokens;  // first token of this workgroup
-    if (p0 < 0 || n <= 0 || b0 >= n) return;
-    const int ntok = min(kQkvTokens, n - b0);
+    const int b = blockIdx.x;             // this workgroup's token
+    if (p0 < 0 || n <= 0 || b >= n) return;
+    const int p = p0 + b;
+    const size_t r = (size_t)row0 + b;    // its row in q / k / v
 
-    // Item it = (token t = it / heads, head hh = it % heads); heads are Q, then K, then V
-    // (V := K without v).
+    // Item hh: heads are Q, then K, then V (V := K without v).
     const int heads = a.Hq + 2 * a.Hkv;
-    const int items = ntok * heads;
-    auto src_of = [&](int it) -> const float* {
-        const int t = it / heads, hh = it % heads;
-        const size_t r = (size_t)row0 + b0 + t;
+    auto src_of = [&](int hh) -> const float* {
         if (hh < a.Hq) return a.q + (r * a.Hq + hh) * D;
         if (hh < a.Hq + a.Hkv) return a.k + (r * a.Hkv + (hh - a.Hq)) * D;
         return (a.v ? a.v : a.k) + (r * a.Hkv + (hh - a.Hq - a.Hkv)) * D;
@@ -343,9 +361,9 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
     auto load_batch = [&](int first) {
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
-            const int it = first + j * kQkvWaves;
-            if (it < items) {
-                const float* src = src_of(it);
+            const int hh = first + j * kQkvWaves;
+            if (hh < heads) {
+                const float* src = src_of(hh);
                 load_vec<E>(src + lane * E, f1[j]);
                 load_vec<E>(src + HALF + lane * E, f2[j]);
             }
@@ -353,18 +371,16 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
     };
     load_batch(wave);
 
-    for (int i = tid; i < ntok * a.rotary_half; i += NT) {
-        const int t = i / a.rotary_half, k = i % a.rotary_half;
-        const float theta = (float)(p0 + b0 + t) / a.inv_freq[k];
+    for (int i = tid; i < a.rotary_half; i += NT) {
+        const float theta = (float)p / a.inv_freq[i];
         double sn, c;
         sincos((double)theta, &sn, &c);
-        s_cos[t][k] = c;
-        s_sin[t][k] = sn;
+        s_cos[i] = c;
+        s_sin[i] = sn;
     }
     // K / V rows are written only by an OK sequence, and in ring mode only by the last
     // ring_size tokens of the call (earlier ones would be overwritten within it).
-    if (tid < ntok) {
-        const int b = b0 + tid, p = p0 + b;
+    if (tid == 0) {
         long long prow = -1;
         if (st == PKV_SEQ_OK && !(ring && b < n - ap.ring_size)) {
             const int32_t* table = ap.tables + (size_t)s * ap.table_stride;
@@ -376,12 +392,13 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
                 else prow = (long long)phys * ap.bs + p % ap.bs;
             }
         }
-        s_prow[tid] = prow;
+        s_prow = prow;
     }
     __syncthreads();
+    const long long prow = s_prow;
 
     const size_t kv_row_elems = (size_t)a.Hkv * D;
-    for (int first = wave; first < items; first += kQkvWaves * IPW) {
+    for (int first = wave; first < heads; first += kQkvWaves * IPW) {
         if (first != wave) load_batch(first);
         // sums of squares of the batch's heads, reduced together (independent chains)
         float ss[IPW];
@@ -392,19 +409,21 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
             for (int e = 0; e < E; ++e) ss[j] += f1[j][e] * f1[j][e] + f2[j][e] * f2[j][e];
         }
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1)
+        for (int j = 0; j < IPW; ++j) ss[j] = wave_sum(ss[j]);
+        // 1 / sqrt(mean + eps) of head j on lane j, then each head's value from its lane
+        float ssl = ss[0];
 #pragma unroll
-            for (int j = 0; j < IPW; ++j) ss[j] += __shfl_xor(ss[j], off);
+        for (int j = 1; j < IPW; ++j) ssl = lane == j ? ss[j] : ssl;
+        const float inv_l = 1.0f / sqrtf(ssl / (float)D + 1e-6f);
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
-            const int it = first + j * kQkvWaves;
-            if (it >= items) break;
-            const int t = it / heads, hh = it % heads;
+            const int hh = first + j * kQkvWaves;
+            if (hh >= heads) break;
             const int kind = hh < a.Hq ? 0 : (hh < a.Hq + a.Hkv ? 1 : 2);  // q, k, v
-            const long long prow = s_prow[t];
             if (kind != 0 && prow < 0) continue;
             const int h = kind == 0 ? hh : (kind == 1 ? hh - a.Hq : hh - a.Hq - a.Hkv);
-            const float inv_rms = 1.0f / sqrtf(ss[j] / (float)D + 1e-6f);
+            const float inv_rms = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_l), j));
             float o1[E], o2[E];
             if (kind < 2) {
                 const float* w = kind == 0 ? a.q_w : a.k_w;
@@ -414,16 +433,14 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
                     const int i = lane * E + e;
-                    double v1 = (double)f1[j][e] * (double)w1[e];  // exact products
-                    double v2 = (double)f2[j][e] * (double)w2[e];
-                    if (i < a.rotary_half) {
-                        const double c = s_cos[t][i], sn = s_sin[t][i];
-                        const double r1 = v1 * c - v2 * sn;
-                        v2 = v2 * c + v1 * sn;
-                        v1 = r1;
-                    }
-                    o1[e] = (float)(v1 * (double)inv_rms);
-                    o2[e] = (float)(v2 * (double)inv_rms);
+                    const double v1 = (double)f1[j][e] * (double)w1[e];  // exact products
+                    const double v2 = (double)f2[j][e] * (double)w2[e];
+                    const bool rot = i < a.rotary_half;  // a select, not a branch
+                    const double c = s_cos[rot ? i : 0], sn = s_sin[rot ? i : 0];
+                    const double r1 = rot ? v1 * c - v2 * sn : v1;
+                    const double r2 = rot ? v2 * c + v1 * sn : v2;
+                    o1[e] = (float)(r1 * (double)inv_rms);
+                    o2[e] = (float)(r2 * (double)inv_rms);
                 }
             } else {
 #pragma unroll
@@ -433,7 +450,7 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
                 }
             }
             if (kind == 0) {
-                const size_t off = (((size_t)row0 + b0 + t) * a.Hq + h) * D;
+                const size_t off = (r * a.Hq + h) * D;
                 store_row<E>(a.q_out, off + lane * E, a.q_out_bf16, o1);
                 store_row<E>(a.q_out, off + HALF + lane * E, a.q_out_bf16, o2);
             } else {
@@ -633,7 +650,7 @@ int32_t pkv_append_qkv(void* stream, const pkv_params* p, int32_t is_global, voi
         a.inv_freq[i] = (float)pow(base, (double)((float)(2 * i) / rope_dim));
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (!ring) hipLaunchKernelGGL(alloc_kernel, dim3(1), dim3(kNT), 0, st, ap);
-    dim3 grid((max_new + kQkvTokens - 1) / kQkvTokens, batch);
+    dim3 grid(max_new, batch);
     const dim3 block(kQkvWaves * kWave);
     if (p->head_dim == 256) hipLaunchKernelGGL(qkv_append_kernel<2>, grid, block, 0, st, a);
     else hipLaunchKernelGGL(qkv_append_kernel<4>, grid, block, 0, st, a);
