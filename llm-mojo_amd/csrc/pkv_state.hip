@@ -293,14 +293,17 @@ __device__ inline void load_vec(const float* p, float (&x)[E]) {
     }
 }
 
-// E elements per lane per half-head: head_dim D = 128 * E. A workgroup of kQkvWaves
-// waves takes one token; its heads go round-robin to the waves, kQkvItems at a time per
-// wave, and every item of a batch is loaded before any is processed (the first batch
-// before the angle table is built). Per batch, the heads' 1 / sqrt(mean + eps) runs once
-// for all of them (lane j takes head j), and the partial-rotary test is a select, so the
-// per-element path has no branch.
+// A workgroup of kQkvWaves waves takes one token. A wave processes HS heads at once
+// (HS = 2 for head_dim 256 when no pair of heads would mix Q, K and V: lanes 0-31 one
+// head, 32-63 the next; else HS = 1), so a lane holds EL = D * HS / 128 elements of each
+// half of its head (4 for head_dim 512 and for paired 256: 16-byte loads), with the RoPE
+// pair (i, i + D/2) in one lane. Slots of HS heads go round-robin to the waves,
+// kQkvHeads / HS at a time per wave; every slot of a batch is loaded before any is
+// processed (the first batch before the angle table is built). Per batch, the heads'
+// 1 / sqrt(mean + eps) runs once for all of them (lane j + 32 sub takes slot j's head
+// sub), and the partial-rotary test is a select, so the per-element path has no branch.
 constexpr int kQkvWaves = 8;
-constexpr int kQkvItems = 4;  // 32 heads (16 q + 8 k + 8 v) over 8 waves
+constexpr int kQkvHeads = 4;  // heads per wave and batch: 32 heads (16 q + 8 k + 8 v) in one
 
 // Sum over the 64 lanes, in every lane, without LDS: lane l ^ 32 and l ^ 16 by the
 // permlane swaps (each returns both halves, so a + b pairs every lane with its partner),
@@ -319,14 +322,27 @@ __device__ inline float wave_sum(float x) {
     x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));   // l ^ 1
     return x;
 }
-static_assert(kQkvItems <= kWave, "one lane per head of a batch");
 
-template <int E>
+// The same over each half of the wave (lanes 0-31 and 32-63 separately).
+__device__ inline float half_wave_sum(float x) {
+    const uint32_t u16 = __float_as_uint(x);
+    auto r16 = __builtin_amdgcn_permlane16_swap(u16, u16, false, false);
+    x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));  // row_ror:8
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xf, 0xf, false));  // row_ror:4
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));   // l ^ 2
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));   // l ^ 1
+    return x;
+}
+template <int D, int HS>
 __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a) {
-    constexpr int D = 128 * E;
     constexpr int HALF = D / 2;
+    constexpr int LPH = kWave / HS;   // lanes per head
+    constexpr int EL = HALF / LPH;    // elements per lane per half
+    static_assert((EL == 2 || EL == 4) && (HS == 1 || HS == 2), "8- or 16-byte lane slices");
     constexpr int NT = kQkvWaves * kWave;
-    constexpr int IPW = kQkvItems;
+    constexpr int IPW = kQkvHeads / HS;  // slots per wave and batch
+    static_assert(IPW <= kWave / 2, "one lane per slot and head");
     __shared__ double s_cos[HALF], s_sin[HALF];
     __shared__ long long s_prow;  // pool row of the token's K / V, or -1
     const AppendArgs& ap = a.ap;
@@ -334,6 +350,7 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
+    const int sub = lane / LPH, hl = lane % LPH;  // head of the slot, lane within the head
     const bool ring = ap.ring_size > 0;
     // independent loads first, so they are in flight together
     const int p0 = ap.pos[s];
@@ -350,22 +367,24 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
     const int p = p0 + b;
     const size_t r = (size_t)row0 + b;    // its row in q / k / v
 
-    // Item hh: heads are Q, then K, then V (V := K without v).
+    // Slot it holds heads HS * it .. HS * it + HS - 1: Q, then K, then V (V := K without
+    // v). Hq and Hkv are multiples of HS, so a slot never mixes kinds.
     const int heads = a.Hq + 2 * a.Hkv;
+    const int slots = heads / HS;
     auto src_of = [&](int hh) -> const float* {
         if (hh < a.Hq) return a.q + (r * a.Hq + hh) * D;
         if (hh < a.Hq + a.Hkv) return a.k + (r * a.Hkv + (hh - a.Hq)) * D;
         return (a.v ? a.v : a.k) + (r * a.Hkv + (hh - a.Hq - a.Hkv)) * D;
     };
-    float f1[IPW][E], f2[IPW][E];
+    float f1[IPW][EL], f2[IPW][EL];
     auto load_batch = [&](int first) {
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
-            const int hh = first + j * kQkvWaves;
-            if (hh < heads) {
-                const float* src = src_of(hh);
-                load_vec<E>(src + lane * E, f1[j]);
-                load_vec<E>(src + HALF + lane * E, f2[j]);
+            const int it = first + j * kQkvWaves;
+            if (it < slots) {
+                const float* src = src_of(it * HS + sub);
+                load_vec<EL>(src + hl * EL, f1[j]);
+                load_vec<EL>(src + HALF + hl * EL, f2[j]);
             }
         }
     };
@@ -398,7 +417,7 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
     const long long prow = s_prow;
 
     const size_t kv_row_elems = (size_t)a.Hkv * D;
-    for (int first = wave; first < heads; first += kQkvWaves * IPW) {
+    for (int first = wave; first < slots; first += kQkvWaves * IPW) {
         if (first != wave) load_batch(first);
         // sums of squares of the batch's heads, reduced together (independent chains)
         float ss[IPW];
@@ -406,33 +425,37 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
         for (int j = 0; j < IPW; ++j) {
             ss[j] = 0.f;
 #pragma unroll
-            for (int e = 0; e < E; ++e) ss[j] += f1[j][e] * f1[j][e] + f2[j][e] * f2[j][e];
+            for (int e = 0; e < EL; ++e) ss[j] += f1[j][e] * f1[j][e] + f2[j][e] * f2[j][e];
         }
 #pragma unroll
-        for (int j = 0; j < IPW; ++j) ss[j] = wave_sum(ss[j]);
-        // 1 / sqrt(mean + eps) of head j on lane j, then each head's value from its lane
+        for (int j = 0; j < IPW; ++j) ss[j] = HS == 2 ? half_wave_sum(ss[j]) : wave_sum(ss[j]);
+        // 1 / sqrt(mean + eps) of slot j's head `sub` on lane j + 32 sub, then each lane
+        // takes its own head's value
         float ssl = ss[0];
 #pragma unroll
-        for (int j = 1; j < IPW; ++j) ssl = lane == j ? ss[j] : ssl;
+        for (int j = 1; j < IPW; ++j) ssl = (lane & 31) == j ? ss[j] : ssl;
         const float inv_l = 1.0f / sqrtf(ssl / (float)D + 1e-6f);
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
-            const int hh = first + j * kQkvWaves;
-            if (hh >= heads) break;
-            const int kind = hh < a.Hq ? 0 : (hh < a.Hq + a.Hkv ? 1 : 2);  // q, k, v
+            const int it = first + j * kQkvWaves;
+            if (it >= slots) break;
+            const int hh0 = it * HS;  // the slot's first head; the kind is the slot's
+            const int kind = hh0 < a.Hq ? 0 : (hh0 < a.Hq + a.Hkv ? 1 : 2);  // q, k, v
             if (kind != 0 && prow < 0) continue;
+            const int hh = hh0 + sub;
             const int h = kind == 0 ? hh : (kind == 1 ? hh - a.Hq : hh - a.Hq - a.Hkv);
-            const float inv_rms = __builtin_bit_cast(
-                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_l), j));
-            float o1[E], o2[E];
+            const int inv_lo = __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_l), j);
+            const int inv_hi = __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_l), 32 + j);
+            const float inv_rms = __builtin_bit_cast(float, sub ? inv_hi : inv_lo);
+            float o1[EL], o2[EL];
             if (kind < 2) {
                 const float* w = kind == 0 ? a.q_w : a.k_w;
-                float w1[E], w2[E];
-                load_vec<E>(w + lane * E, w1);
-                load_vec<E>(w + HALF + lane * E, w2);
+                float w1[EL], w2[EL];
+                load_vec<EL>(w + hl * EL, w1);
+                load_vec<EL>(w + HALF + hl * EL, w2);
 #pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    const int i = lane * E + e;
+                for (int e = 0; e < EL; ++e) {
+                    const int i = hl * EL + e;
                     const double v1 = (double)f1[j][e] * (double)w1[e];  // exact products
                     const double v2 = (double)f2[j][e] * (double)w2[e];
                     const bool rot = i < a.rotary_half;  // a select, not a branch
@@ -444,20 +467,20 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < E; ++e) {
+                for (int e = 0; e < EL; ++e) {
                     o1[e] = f1[j][e] * inv_rms;
                     o2[e] = f2[j][e] * inv_rms;
                 }
             }
             if (kind == 0) {
                 const size_t off = (r * a.Hq + h) * D;
-                store_row<E>(a.q_out, off + lane * E, a.q_out_bf16, o1);
-                store_row<E>(a.q_out, off + HALF + lane * E, a.q_out_bf16, o2);
+                store_row<EL>(a.q_out, off + hl * EL, a.q_out_bf16, o1);
+                store_row<EL>(a.q_out, off + HALF + hl * EL, a.q_out_bf16, o2);
             } else {
                 void* pool = kind == 1 ? (void*)ap.k_pool : (void*)ap.v_pool;
                 const size_t off = (size_t)prow * kv_row_elems + (size_t)h * D;
-                store_row<E>(pool, off + lane * E, a.kv_bf16, o1);
-                store_row<E>(pool, off + HALF + lane * E, a.kv_bf16, o2);
+                store_row<EL>(pool, off + hl * EL, a.kv_bf16, o1);
+                store_row<EL>(pool, off + HALF + hl * EL, a.kv_bf16, o2);
             }
         }
     }
@@ -652,8 +675,11 @@ int32_t pkv_append_qkv(void* stream, const pkv_params* p, int32_t is_global, voi
     if (!ring) hipLaunchKernelGGL(alloc_kernel, dim3(1), dim3(kNT), 0, st, ap);
     dim3 grid(max_new, batch);
     const dim3 block(kQkvWaves * kWave);
-    if (p->head_dim == 256) hipLaunchKernelGGL(qkv_append_kernel<2>, grid, block, 0, st, a);
-    else hipLaunchKernelGGL(qkv_append_kernel<4>, grid, block, 0, st, a);
+    // head_dim 256 pairs heads within a wave when no slot would mix Q, K and V heads
+    if (p->head_dim == 512) hipLaunchKernelGGL((qkv_append_kernel<512, 1>), grid, block, 0, st, a);
+    else if (p->num_heads % 2 == 0 && p->num_kv_heads % 2 == 0)
+        hipLaunchKernelGGL((qkv_append_kernel<256, 2>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((qkv_append_kernel<256, 1>), grid, block, 0, st, a);
     return check_launch("pkv_append_qkv");
 }
 

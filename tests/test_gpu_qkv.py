@@ -123,7 +123,8 @@ def _state_match(cache, st):
     (False, 16, 8, 256, F32, True, False),   # sliding layer, fp32 pools
     (True, 16, 2, 512, BF16, False, True),   # global layer, V := K, bf16 pools and Q
     (True, 16, 8, 256, F32, True, False),    # the configs' 16/8/256 global stand-in
-], ids=["sliding-f32", "global512-bf16", "global256-f32"])
+    (False, 6, 3, 256, BF16, True, True),    # odd kv heads: one head per wave, not pairs
+], ids=["sliding-f32", "global512-bf16", "global256-f32", "odd-heads-256-bf16"])
 def test_append_qkv_decode_and_chunks(gpu, is_global, hq, hkv, D, kv_dtype, with_v, q_bf16):
     print(f"[qkv] global={is_global} {hq}/{hkv}/{D} {kv_dtype}", flush=True)
     rng = np.random.default_rng(D + hkv)
