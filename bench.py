@@ -709,7 +709,7 @@ def bench_producer(args, log):
     dec_pos = rng.integers(128, 8193, 32)
     dc_ms, dc_dur, dc_bytes, dc_ok, dec = shape_leg(32, 1, dec_pos, F32, F32, args.steps,
                                                     args.warmup, 201)
-    roof = _roofline(pf_bytes, pf_dur, "alloc_kernel + qkv_append_kernel<2>")
+    roof = _roofline(pf_bytes, pf_dur, "alloc_kernel + qkv_append_kernel<256, 2>")
     res = _line("producer step (rms_norm + RoPE + KV append) tokens/s, 4 x 2048-token prefill "
                 "chunks", 4 * 2048 * args.steps / (pf_ms / 1e3), "tokens/s", args.steps,
                 args.warmup, pf_ms / args.steps, "f32 in, bf16 out",
