@@ -172,6 +172,24 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
                    const int32_t* pos, int32_t batch, int32_t max_pos, float* out,
                    void* workspace, size_t workspace_bytes);
 
+/* K2'' -- verify attention with a query count per sequence. The engine verifies each
+ * sequence's own draft: verify_b = drafts + 1 tokens (model_speculative_moe_batched.mojo
+ * :3005), fewer when drafting stopped early at a terminal token (:2990-2993), so counts
+ * differ across the batch. Replaces that loop (:3090-3123) for the whole batch at once:
+ * sequence s has q_lens[s] in [0, max_q_len] queries, rows j < q_lens[s] of q / out (fp32
+ * [batch][max_q_len][num_heads][head_dim], the pkv_attend layout for q_len = max_q_len) at
+ * positions pos[s] + j, each attending [window_start(pos[s] + j), pos[s] + j]. Rows
+ * j >= q_lens[s] of out are not written. A count outside [0, max_q_len] gives NaN rows;
+ * the other contract violations behave as in pkv_attend. max_pos bounds pos[s] +
+ * q_lens[s] - 1. Workspace: pkv_workspace_size(p, batch, max_q_len, max_pos). head_dim
+ * 256 or 512 with num_heads / num_kv_heads <= 8 (every geometry of the engine); other
+ * geometries give PKV_ERR_UNSUPPORTED. Two launches per group of up to 8 query rows per
+ * kv head. */
+int32_t pkv_verify(void* stream, const pkv_params* p, const float* q, const void* k_pool,
+                   const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                   const int32_t* pos, const int32_t* q_lens, int32_t max_q_len, int32_t batch,
+                   int32_t max_pos, float* out, void* workspace, size_t workspace_bytes);
+
 /* Bytes of workspace pkv_attend_sparse needs for `batch` key lists of at most max_keys
  * entries. 0 on invalid params. */
 size_t pkv_sparse_workspace_size(const pkv_params* p, int32_t batch, int32_t max_keys);

@@ -656,12 +656,13 @@ int32_t dispatch_rows(const AttendArgs& a, int rows, dim3 grid, hipStream_t st) 
 }
 
 // pos == NULL: one sequence at pos_scalar (whose ring, in ring mode, starts at row
-// ring_base; block_tables is then not read and may be NULL).
+// ring_base; block_tables is then not read and may be NULL). q_lens != NULL: sequence s
+// has q_lens[s] <= q_len queries (stream path only).
 int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const void* k_pool,
                     const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                     const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
-                    int32_t batch, int32_t max_pos, float* out, void* workspace,
-                    size_t workspace_bytes) {
+                    const int32_t* q_lens, int32_t batch, int32_t max_pos, float* out,
+                    void* workspace, size_t workspace_bytes) {
     int32_t rc = validate_params(p);
     if (rc != PKV_OK) return rc;
     if (batch <= 0 || q_len <= 0 || table_stride <= 0 || max_pos < 0)
@@ -675,10 +676,16 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (stream_eligible(p, G) && workspace_bytes >= stream_layout(p, batch, q_len).total) {
         rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
-                           ring_base, q_len, batch, max_pos, nullptr, nullptr, 0, out,
+                           ring_base, q_len, q_lens, batch, max_pos, nullptr, nullptr, 0, out,
                            workspace, st);
         if (rc != PKV_OK) return rc;
         return check_launch("pkv_attend");
+    }
+    if (q_lens) {
+        if (!stream_eligible(p, G))
+            return fail(PKV_ERR_UNSUPPORTED, "per-sequence query counts need head_dim 256 or 512 "
+                                             "and num_heads / num_kv_heads <= 8");
+        return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_workspace_size()");
     }
     if (rows > 16)
         return fail(PKV_ERR_UNSUPPORTED, "this geometry allows at most 16 query rows "
@@ -783,7 +790,7 @@ int32_t pkv_attend_sparse(void* stream, const pkv_params* p, const float* q, con
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (stream_eligible(p, G) && workspace_bytes >= stream_layout(p, batch, 1).total) {
         rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, nullptr, 0, 0, 1,
-                           batch, 0, keys, key_off, max_keys, out, workspace, st);
+                           nullptr, batch, 0, keys, key_off, max_keys, out, workspace, st);
         if (rc != PKV_OK) return rc;
         return check_launch("pkv_attend_sparse");
     }
@@ -835,7 +842,17 @@ int32_t pkv_attend(void* stream, const pkv_params* p, const float* q, const void
     pkv::clear_error();
     if (!pos) return pkv::fail(PKV_ERR_INVALID, "pos is NULL");
     return pkv::attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0, 0,
-                            q_len, batch, max_pos, out, workspace, workspace_bytes);
+                            q_len, nullptr, batch, max_pos, out, workspace, workspace_bytes);
+}
+
+int32_t pkv_verify(void* stream, const pkv_params* p, const float* q, const void* k_pool,
+                   const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                   const int32_t* pos, const int32_t* q_lens, int32_t max_q_len, int32_t batch,
+                   int32_t max_pos, float* out, void* workspace, size_t workspace_bytes) {
+    pkv::clear_error();
+    if (!pos || !q_lens) return pkv::fail(PKV_ERR_INVALID, "pos or q_lens is NULL");
+    return pkv::attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0, 0,
+                            max_q_len, q_lens, batch, max_pos, out, workspace, workspace_bytes);
 }
 
 int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void* k_pool,
@@ -875,14 +892,14 @@ int32_t pkv_paged_attention_layer(void* stream, const float* q, const void* k_po
         if (n > ring_size)
             return pkv::fail(PKV_ERR_INVALID, "ring_size smaller than the attended window");
         return pkv::attend_impl(stream, &p, q, k_pool, v_pool, nullptr, 1, nullptr, pos,
-                                ring_base, 1, 1, pos < 0 ? 0 : pos, attn_out, workspace,
+                                ring_base, 1, nullptr, 1, pos < 0 ? 0 : pos, attn_out, workspace,
                                 workspace_bytes);
     }
     // The table must cover pos (attention.mojo:271); the kernel checks against the
     // stride, so the stride is exactly the entries needed.
     int32_t stride = (pos < 0 ? 0 : pos / (block_size > 0 ? block_size : 1)) + 1;
     return pkv::attend_impl(stream, &p, q, k_pool, v_pool, block_table, stride, nullptr, pos, 0,
-                            1, 1, pos < 0 ? 0 : pos, attn_out, workspace, workspace_bytes);
+                            1, nullptr, 1, pos < 0 ? 0 : pos, attn_out, workspace, workspace_bytes);
 }
 
 }  // extern "C"

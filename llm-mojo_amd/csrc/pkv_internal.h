@@ -56,11 +56,12 @@ bool stream_eligible(const pkv_params* p, int32_t G);
 // pos == NULL: one sequence at pos_scalar; in ring mode its ring starts at row
 // ring_base (otherwise ring slot block_tables[s * table_stride] starts at row
 // slot * ring_size). keys != NULL: sparse mode, sequence s attends the key positions
-// keys[key_off[s] .. key_off[s+1]) (q_len 1, at most max_keys each).
+// keys[key_off[s] .. key_off[s+1]) (q_len 1, at most max_keys each). q_lens != NULL:
+// sequence s has q_lens[s] <= q_len queries; its other rows of out are not written.
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                       const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
-                      int32_t batch, int32_t max_pos, const int32_t* keys,
+                      const int32_t* q_lens, int32_t batch, int32_t max_pos, const int32_t* keys,
                       const int32_t* key_off, int32_t max_keys, float* out, void* workspace,
                       hipStream_t st);
 

@@ -318,6 +318,7 @@ struct StreamArgs {
     const int32_t* pos;  // null -> pos_scalar (single sequence)
     int32_t pos_scalar;
     int32_t q_len;       // queries per sequence in q / out (their layout)
+    const int32_t* q_lens;  // queries of each sequence (<= q_len), or null: q_len for all
     int32_t j0;          // first query of this launch
     int32_t q_cnt;       // queries of this launch
     const int32_t* keys;     // sparse: key positions, ragged by key_off [batch + 1]
@@ -341,6 +342,11 @@ struct StreamArgs {
     void* part_o;      // Acc [D] per (slot, row)
     float* out;
 };
+
+// Queries of sequence s in this launch (the rest of its rows are left untouched).
+__device__ inline int seq_queries(const StreamArgs& a, int s) {
+    return a.q_lens ? min(max(a.q_lens[s] - a.j0, 0), a.q_cnt) : a.q_cnt;
+}
 
 __device__ inline size_t out_row(const StreamArgs& a, int s, int g, int r) {
     const int j = a.j0 + r / a.G, h = g * a.G + r % a.G;
@@ -405,15 +411,21 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             continue;
         }
         const int p0 = a.pos ? a.pos[i] : a.pos_scalar;
-        if (p0 >= 0) {
-            const int hi = p0 + a.j0 + a.q_cnt - 1;
+        const int qlen = a.q_lens ? a.q_lens[i] : a.q_len;
+        const int qc = seq_queries(a, i);
+        if (qlen < 0 || qlen > a.q_len) {
+            lo = -2;  // a query count outside the layout: NaN rows
+        } else if (qc == 0) {
+            lo = -3;  // no query of this sequence in this launch: nothing to do
+        } else if (p0 >= 0) {
+            const int hi = p0 + a.j0 + qc - 1;
             const int w0 = window_start(p0 + a.j0, a.window);
             bool ok = hi <= a.max_pos;
             if constexpr (RING) {
                 // Every key of the call must still be in the ring (the reference aborts,
                 // attention.mojo:265-266) -- the call's later queries have already written
                 // theirs -- and the ring slot must lie in the pool.
-                ok = ok && (p0 + a.q_len - 1) - w0 + 1 <= a.ring_size;
+                ok = ok && (p0 + qlen - 1) - w0 + 1 <= a.ring_size;
                 if (a.pos) {
                     const int slot = a.tables[(size_t)i * a.table_stride];
                     ok = ok && slot >= 0 && slot < a.num_blocks;
@@ -443,10 +455,13 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         for (int i = tid; i <= B; i += nthr) a.plan[1 + i] = s_pre[i];
         for (int s = 0; s < B; ++s) {
             const int lo = s_lo[s];
-            if (lo >= 0) continue;
+            if (lo >= 0 || lo == -3) continue;
             const float fill = lo == -1 ? 0.f : __builtin_nanf("");
+            // rows of the sequence's queries; an invalid query count marks the whole group
+            const bool qbad = a.q_lens && (a.q_lens[s] < 0 || a.q_lens[s] > a.q_len);
+            const int nrow = (qbad ? a.q_cnt : seq_queries(a, s)) * a.Hq;
             float* o = a.out + ((size_t)s * a.q_len + a.j0) * a.Hq * D;
-            for (int i = tid; i < a.rows_seq * D; i += nthr) o[i] = fill;
+            for (int i = tid; i < nrow * D; i += nthr) o[i] = fill;
         }
     }
     const int k0 = w * per;
@@ -490,6 +505,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         const int tb = lo_key + min(k1, pe) - ps;  // one past the last
         const bool single = (ps / per) == ((pe - 1) / per);
         const int pos0 = SPARSE ? 0 : (a.pos ? ufirst(a.pos[s]) : a.pos_scalar);
+        const int rows_s = a.G * seq_queries(a, s);  // this sequence's live rows
+        const bool live_own = row_live && rb + r_own < rows_s;
 
         // Query rows -> registers (scaled); rows beyond `rows` stay zero.
         Acc qr[R][EPL];
@@ -593,7 +610,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             }
             xred<NV, kSW / 2>(dots, lane);
             const int t_own = t + u_own;
-            const bool ok = row_live && t_own < tb && t_own <= pq_own && t_own >= ws_own;
+            const bool ok = live_own && t_own < tb && t_own <= pq_own && t_own >= ws_own;
             const Acc sc = ok ? dots[0] : (Acc)-INFINITY;
             const Acc mb = allreduce_hi<ROWB>(sc, OpMax());
             const Acc m_new = fmax(m_own, mb);
@@ -630,7 +647,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         if (single) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (rb + r < rows) {
+                if (rb + r < rows_s) {
                     const Acc inv = (Acc)1 / (bcast(l_own, r * REP) + (Acc)1e-10);
                     float* op = a.out + out_row(a, s, g, rb + r) * D + lane * EPL;
 #pragma unroll
@@ -683,6 +700,7 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
     const int wave = tid / kSW;
+    if (row / a.Hq >= seq_queries(a, s)) return;  // a row past the sequence's queries
     const int per = a.plan[0];
     const int ps = a.plan[1 + s], pe = a.plan[2 + s];
     if (pe == ps) return;
@@ -868,7 +886,7 @@ bool stream_eligible(const pkv_params* p, int32_t G) {
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                       const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
-                      int32_t batch, int32_t max_pos, const int32_t* keys,
+                      const int32_t* q_lens, int32_t batch, int32_t max_pos, const int32_t* keys,
                       const int32_t* key_off, int32_t max_keys, float* out, void* workspace,
                       hipStream_t st) {
     const int G = p->num_heads / p->num_kv_heads;
@@ -884,6 +902,7 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.pos = pos;
     a.pos_scalar = pos_scalar;
     a.q_len = q_len;
+    a.q_lens = q_lens;
     a.keys = keys;
     a.key_off = key_off;
     a.max_keys = max_keys;

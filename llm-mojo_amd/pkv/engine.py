@@ -236,6 +236,20 @@ class PagedKVCache:
                  self.max_pos if max_pos is None else max_pos, _ptr(out), self.workspace.ptr,
                  self.workspace.nbytes)
 
+    def verify(self, layer: int, q, pos, q_lens, max_q_len: int, out, batch: int | None = None,
+               max_pos: int | None = None):
+        """Verify attention with a query count per sequence (pkv_verify): q / out device
+        fp32 [batch][max_q_len][Hq][D]; sequence s has q_lens[s] queries at positions
+        pos[s] + j, and its rows past q_lens[s] are not written."""
+        b = batch or self.max_seqs
+        p = self.params[layer]
+        tables, stride = self._tables_of(layer)
+        lib.call("pkv_verify", self._stream(), ctypes.byref(p), _ptr(q),
+                 self.k_pools[layer].ptr, self.v_pools[layer].ptr, tables, stride,
+                 self._ints(pos, self._i32_a, b), self._ints(q_lens, self._i32_b, b), max_q_len,
+                 b, self.max_pos if max_pos is None else max_pos, _ptr(out), self.workspace.ptr,
+                 self.workspace.nbytes)
+
     def attend_sparse(self, layer: int, q, keys, key_off, max_keys: int, out,
                       batch: int | None = None):
         """Sparse paged attention over explicit key lists (K2', LSA): q / out device fp32

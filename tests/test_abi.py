@@ -154,3 +154,16 @@ def test_lsa_cache_rejections_before_launch():
     assert L.pkv_lsa_rollback(None, p, p, -1, 6, 2048, 128, p, p, p) == lib.PKV_ERR_INVALID
     assert L.pkv_lsa_rollback(None, None, p, 3, 6, 2048, 128, p, p, p) == lib.PKV_ERR_INVALID
     assert L.pkv_lsa_rollback(None, None, None, 0, 6, 2048, 128, None, None, None) == lib.PKV_OK
+
+
+def test_verify_rejections_before_launch():
+    L = lib.load()
+    p = _params()
+    import ctypes
+    ptr = 16
+    # q_lens is required; a geometry without the stream path cannot take per-sequence counts
+    assert L.pkv_verify(None, ctypes.byref(p), ptr, ptr, ptr, ptr, 8, ptr, None, 4, 2, 100, ptr,
+                        ptr, 1 << 20) == lib.PKV_ERR_INVALID
+    p64 = _params(head_dim=64)
+    assert L.pkv_verify(None, ctypes.byref(p64), ptr, ptr, ptr, ptr, 8, ptr, ptr, 4, 2, 100, ptr,
+                        ptr, 1 << 20) == lib.PKV_ERR_UNSUPPORTED

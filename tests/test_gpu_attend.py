@@ -265,3 +265,64 @@ def test_inactive_sequence_gives_zeros_and_bad_table_gives_nan(gpu):
              dpos2.ptr, 1, B, 127, out.ptr, ws.ptr, ws.nbytes)
     o = out.numpy()
     assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[0])) and np.all(np.isfinite(o[2]))
+
+
+@pytest.mark.parametrize("geom,window,kv_dtype", [
+    ((16, 8, 256), 0, F32),      # two query groups of 4 (8 rows per kv head each)
+    ((16, 8, 256), 1024, F32),   # sliding window
+    ((16, 2, 512), 0, BF16),     # 8 q heads per kv head: one query per group
+], ids=["s256-f32", "s256-window", "g512-bf16"])
+def test_verify_per_sequence_query_counts(gpu, geom, window, kv_dtype):
+    # pkv_verify: every sequence its own draft length (the engine's verify_b = drafts + 1,
+    # fewer after an early stop), including none. Rows past a sequence's count keep what
+    # the caller left there; an invalid count gives NaN rows.
+    print(f"[verify] per-sequence q_len {geom} window={window} {kv_dtype}", flush=True)
+    hq, hkv, d = geom
+    rng = np.random.default_rng(hq + hkv + d + window)
+    bs, B, qmax = 16, 8, 5
+    q_lens = np.array([1, 5, 3, 0, 4, 2, 5, 7], np.int32)  # the last one is invalid (> 5)
+    ctx = rng.integers(300, 2500, B)
+    kvs = hkv * d
+    blocks_per = [(int(c) + qmax + bs - 1) // bs for c in ctx]
+    nb = sum(blocks_per) + 8
+    stride = max(blocks_per) + 2
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((B, stride), np.int32)
+    lens = np.zeros(B, np.int32)
+    off = 0
+    for s in range(B):
+        tables[s, :blocks_per[s]] = perm[off:off + blocks_per[s]]
+        lens[s] = blocks_per[s]
+        off += blocks_per[s]
+    k = rng.standard_normal(nb * bs * kvs, dtype=np.float32)
+    v = rng.standard_normal(nb * bs * kvs, dtype=np.float32)
+    if kv_dtype == BF16:
+        k, v = O.to_bf16(k), O.to_bf16(v)
+    q = rng.standard_normal((B, qmax, hq, d), dtype=np.float32)
+    pos = np.asarray(ctx, np.int32)
+    p = make_params(LayerSpec(hq, hkv, d, window, kv_dtype), bs, nb, 0.0625)
+    import ctypes
+    max_pos = int(pos.max()) + qmax - 1
+    ws_bytes = lib.load().pkv_workspace_size(ctypes.byref(p), B, qmax, max_pos)
+    ws = hip.DeviceArray((ws_bytes,), np.uint8, zero=True)
+    dk, dv = hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(v)
+    dt, dq = hip.DeviceArray.from_numpy(tables), hip.DeviceArray.from_numpy(q)
+    dpos, dql = hip.DeviceArray.from_numpy(pos), hip.DeviceArray.from_numpy(q_lens)
+    sentinel = np.full((B, qmax, hq, d), 12345.0, np.float32)
+    out = hip.DeviceArray.from_numpy(sentinel)
+    lib.call("pkv_verify", None, ctypes.byref(p), dq.ptr, dk.ptr, dv.ptr, dt.ptr, stride,
+             dpos.ptr, dql.ptr, qmax, B, max_pos, out.ptr, ws.ptr, ws.nbytes)
+    got = out.numpy()
+    for s in range(B - 1):
+        ql = int(q_lens[s])
+        assert np.all(got[s, ql:] == 12345.0), f"sequence {s}: rows past its count written"
+        if ql == 0:
+            continue
+        args = (q[s:s + 1, :ql], k, v, tables[s:s + 1], lens[s:s + 1], pos[s:s + 1], ql, hq,
+                hkv, d, bs, window)
+        ref = O.attend(*args, scale=0.0625)
+        exact = None if kv_dtype == BF16 else O.attend_f64(
+            q[s:s + 1, :ql], k, v, tables[s:s + 1], pos[s:s + 1], ql, hq, hkv, d, bs, window,
+            scale=0.0625)
+        parity.check(got[s:s + 1, :ql], ref, exact, bf16=kv_dtype == BF16, what=f"sequence {s}")
+    assert np.all(np.isnan(got[B - 1])), "an invalid count gives NaN rows"
