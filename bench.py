@@ -591,6 +591,7 @@ def bench_config5(args, log):
                 _roofline(nbytes, float(dur.mean()), "stream_attend_kernel<256, float, 4> (2 waves per kv head) + "
                           "stream_merge_kernel<256, double>", flops=flops),
                 {"verify_attend_us": round(float(dur.mean()) * 1e3, 2)})
+    res["roofline"]["traffic"] = _traffic_from_profiles("verify_mtp_cfg5_traffic.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
 
@@ -710,6 +711,7 @@ def bench_producer(args, log):
     dc_ms, dc_dur, dc_bytes, dc_ok, dec = shape_leg(32, 1, dec_pos, F32, F32, args.steps,
                                                     args.warmup, 201)
     roof = _roofline(pf_bytes, pf_dur, "alloc_kernel + qkv_append_kernel<256, 2>")
+    roof["traffic"] = _traffic_from_profiles("producer_qkv_append_traffic.md")
     res = _line("producer step (rms_norm + RoPE + KV append) tokens/s, 4 x 2048-token prefill "
                 "chunks", 4 * 2048 * args.steps / (pf_ms / 1e3), "tokens/s", args.steps,
                 args.warmup, pf_ms / args.steps, "f32 in, bf16 out",
@@ -869,6 +871,7 @@ def bench_lsa(args, log):
                                    "expand_plus_attend_us": round(dur_xa * 1e3, 2),
                                    "lists_equal_host_expand": device_lists_equal,
                                    "chained_max_rel_diff": float(f"{chained_diff:.3g}")}})
+    res["roofline"]["traffic"] = _traffic_from_profiles("lsa_sparse_stream_traffic.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
 
@@ -945,6 +948,7 @@ def bench_wo(args, log):
                  "sliding_4096": {"us_per_call": round(sl["dur"] * 1e3, 2),
                                   "gbs": round(sl["nbytes"] / (sl["dur"] / 1e3) / 1e9, 1),
                                   "bytes_per_call": int(sl["nbytes"])}})
+    res["roofline"]["traffic"] = _traffic_from_profiles("wo_q4_matmul_traffic.md")
     if args.cpu_seconds > 0:
         n, el = 0, 0.0
         errs = []
