@@ -32,7 +32,7 @@ for _p in (REPO, os.path.join(REPO, "llm-mojo_amd")):
 
 METRIC = "paged decode attn tokens/s + achieved HBM GB/s (% peak) at B=32, 1 GPU"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, AMD published
-PEAK_FP64_VALU_TFLOPS = 78.6  # MI355X vector fp64, AMD published
+PEAK_FP64_MFMA_TFLOPS = 78.6  # MI355X dense fp64 matrix, AMD published
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, AMD published
 
 
@@ -293,10 +293,10 @@ def _roofline(nbytes, dur_ms, kernel, flops=None):
     r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
          "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernel,
          "avg_launch_us": round(dur_ms * 1e3, 2), "algorithmic_bytes_per_launch": int(nbytes)}
-    if flops is not None:  # the fp32-pool arithmetic runs in double on the vector ALUs
+    if flops is not None:  # the fp32-pool verify runs its dot products on the fp64 MFMA
         tf = flops / (dur_ms / 1e3) / 1e12
-        r["fp64_vector_tflops"] = round(tf, 2)
-        r["fp64_vector_frac"] = round(tf / PEAK_FP64_VALU_TFLOPS, 4)
+        r["fp64_mfma_tflops"] = round(tf, 2)
+        r["fp64_mfma_frac"] = round(tf / PEAK_FP64_MFMA_TFLOPS, 4)
     return r
 
 
@@ -588,7 +588,7 @@ def bench_config5(args, log):
                 "BASELINE config 5: 16 sequences, ctx U[512,4096], 2 global layers 16q/8kv/256 "
                 "fp32, block 16; per iteration 4 MTP reads at pos-1 per layer, 4-token verify "
                 "append + causal attention, accept U{0..4}, rollback; 32-iteration schedule",
-                _roofline(nbytes, float(dur.mean()), "stream_attend_kernel<256, float, 4> (2 waves per kv head) + "
+                _roofline(nbytes, float(dur.mean()), "stream_mfma_kernel<2, 1, paged> (fp64 MFMA) + "
                           "stream_merge_kernel<256, double>", flops=flops),
                 {"verify_attend_us": round(float(dur.mean()) * 1e3, 2)})
     res["roofline"]["traffic"] = _traffic_from_profiles("verify_mtp_cfg5_traffic.md")

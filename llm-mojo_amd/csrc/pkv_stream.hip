@@ -37,6 +37,8 @@
 // ~1e-7 absolute error of its own and the parity bound leaves no room for a second
 // error of that size. On CDNA3/4 a non-packed double FMA issues at the fp32 rate.
 // bf16 pools accumulate in fp32.
+// fp32 pools with 5..8 query rows per KV head (verify) run stream_mfma_kernel instead:
+// the same plan, pieces and partials, with QK^T and PV on the fp64 4x4x4 MFMA.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -372,34 +374,21 @@ __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
     if (lane == 0) s_pre[batch] = carry;
 }
 
-// R query rows per wave; WPH waves per KV head split the head's rows (WPH = 2 gives two
-// waves of R rows each, reading the same K/V: the second read of a row slice hits the cache).
-// ADDR: kAddrPaged, kAddrRing (key t at row ring_base + t % ring_size) or kAddrSparse.
-template <int D, typename KV, int R, int WPH, int ADDR>
-__global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamArgs a) {
-    using Acc = typename SKV<KV>::Acc;
-    constexpr int kElt = SKV<KV>::kElt;
-    constexpr int EPL = D / kSW;                // elements per lane per token
-    constexpr int NWD = EPL * kElt / 4;         // 32-bit words per lane per token
-    constexpr int U = batch_tokens<D, KV, R>(); // tokens per batch
+// Key ranges of the launch, laid end to end: s_pre[s] = first key of sequence s in the
+// concatenation (s_pre[batch] = total), s_lo[s] = its first key position, or -1
+// (inactive: zeros), -2 (contract violation: NaN rows), -3 (no query of it in this
+// launch). Workgroup (0, 0) also writes the merge plan and fills the rows of inactive and
+// invalid sequences. Returns `per`, the keys of one workgroup.
+template <int D, int ADDR>
+__device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo) {
     constexpr bool RING = ADDR == kAddrRing;
     constexpr bool SPARSE = ADDR == kAddrSparse;
-    constexpr int NV = U * R;                   // dots per batch
-    static_assert(NV <= kSW && (NV & (NV - 1)) == 0, "dots per batch: power of two <= 64");
-    constexpr int REP = kSW / NV;               // lanes holding the same reduced dot
-    constexpr int ROWB = R * REP;               // lane offset of the first token bit
-
-    extern __shared__ int smem[];
-    int* s_pre = smem;                  // [batch + 1]
-    int* s_lo = smem + a.batch + 1;     // [batch]: window start, -1 inactive, -2 bad
-
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
     const int wave = ufirst(tid / kSW);
     const int nthr = blockDim.x;
     const int w = blockIdx.y;
     const int B = a.batch;
-
     for (int i = tid; i < B; i += nthr) {
         int n = 0, lo = -1;
         if constexpr (SPARSE) {  // the list's indices; an empty list gives zeros
@@ -464,6 +453,38 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             for (int i = tid; i < nrow * D; i += nthr) o[i] = fill;
         }
     }
+    return per;
+}
+
+// R query rows per wave; WPH waves per KV head split the head's rows (WPH = 2 gives two
+// waves of R rows each, reading the same K/V: the second read of a row slice hits the cache).
+// ADDR: kAddrPaged, kAddrRing (key t at row ring_base + t % ring_size) or kAddrSparse.
+template <int D, typename KV, int R, int WPH, int ADDR>
+__global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamArgs a) {
+    using Acc = typename SKV<KV>::Acc;
+    constexpr int kElt = SKV<KV>::kElt;
+    constexpr int EPL = D / kSW;                // elements per lane per token
+    constexpr int NWD = EPL * kElt / 4;         // 32-bit words per lane per token
+    constexpr int U = batch_tokens<D, KV, R>(); // tokens per batch
+    constexpr bool RING = ADDR == kAddrRing;
+    constexpr bool SPARSE = ADDR == kAddrSparse;
+    constexpr int NV = U * R;                   // dots per batch
+    static_assert(NV <= kSW && (NV & (NV - 1)) == 0, "dots per batch: power of two <= 64");
+    constexpr int REP = kSW / NV;               // lanes holding the same reduced dot
+    constexpr int ROWB = R * REP;               // lane offset of the first token bit
+
+    extern __shared__ int smem[];
+    int* s_pre = smem;                  // [batch + 1]
+    int* s_lo = smem + a.batch + 1;     // [batch]: window start, -1 inactive, -2 bad
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kSW - 1);
+    const int wave = ufirst(tid / kSW);
+    const int w = blockIdx.y;
+    const int B = a.batch;
+
+    const int per = stream_setup<D, ADDR>(a, s_pre, s_lo);
+    const int total = ufirst(s_pre[B]);
     const int k0 = w * per;
     if (k0 >= total) return;
     const int k1 = min(total, k0 + per);
@@ -680,6 +701,336 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     }
 }
 
+// ---- fp64 MFMA path: fp32 pools, head_dim 256, 3..8 query rows per KV head ------------
+//
+// v_mfma_f64_4x4x4_4b computes four independent 4x4x4 double products per instruction
+// at the full fp64 rate. Lane l = 4b + x + 16y holds block b's elements (b = lane bits
+// 2-3); inside a block (layouts checked on the device) A[i][k] sits at x = i, y = k,
+// B[k][j] at x = j, y = k, and C[i][j] at x = j, y = i. One wave per KV head; its query
+// rows form RG groups of 4 (row 4rg + x of lane x).
+//   S^T = K Q^T for each group of 4 tokens tg and row group rg: A = K (x = token, y = d
+//     slot), B = Q (x = row, y = d slot). Over the 16 steps (q, e) block b contracts
+//     d = 64q + 16b + 4y + e, so the four blocks hold partial sums over disjoint d, added
+//     by two DPP rotations. Lane (b, x, y) then holds S[row 4rg + x][token 4tg + y] --
+//     the B operand of PV as it stands.
+//   O^T += V^T P^T: A = V (x = d slot, y = token), B = P; tile (rg, q, e) of lane
+//     (b, x, y) accumulates O[4rg + x][64q + 16b + 4y + e].
+// Each load is 16 bytes of one token's row, so a load instruction reads 4 tokens x 256
+// contiguous bytes. Products of fp32 values are exact in double and every sum is a
+// double sum, as in the vector path; the matrix cores take the 2 x rows x 256
+// multiply-adds per token off the vector ALUs, and the dot products need no cross-lane
+// reduction beyond the block sum.
+typedef __attribute__((address_space(3))) void lds_void;
+// s_waitcnt with only lgkmcnt = 0 (vmcnt and expcnt at their maxima).
+constexpr int kLgkm0 = 0xC07F;
+// LDS of the MFMA kernel: s_pre / s_lo, then one staging area per wave.
+__host__ __device__ constexpr size_t mfma_stage_offset(int batch) {
+    return ((size_t)(2 * batch + 1) * sizeof(int) + 15) & ~(size_t)15;
+}
+constexpr int kSlot = 1024 + 16;  // one token's 1 KiB slice plus bank padding
+__host__ __device__ constexpr size_t mfma_stage_bytes(int tg) { return (size_t)tg * 8 * kSlot; }
+
+__device__ inline double mfma4(double a, double b, double c) {
+    return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
+}
+// Sum over the four blocks (lane bits 2-3) in every lane.
+__device__ inline double block_sum(double v) {
+    v += dpp<ror_ctrl<4>()>(v);
+    return v + dpp<ror_ctrl<8>()>(v);
+}
+
+template <int RG, int TG, int ADDR>
+__global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs a) {
+    constexpr int D = 256;
+    constexpr int U = 4 * TG;  // tokens per batch
+    constexpr bool RING = ADDR == kAddrRing;
+    constexpr bool SPARSE = ADDR == kAddrSparse;
+    extern __shared__ int smem[];
+    int* s_pre = smem;               // [batch + 1]
+    int* s_lo = smem + a.batch + 1;  // [batch]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kSW - 1);
+    const int wave = ufirst(tid / kSW);
+    const int w = blockIdx.y;
+    const int B = a.batch;
+
+    const int per = stream_setup<D, ADDR>(a, s_pre, s_lo);
+    const int total = ufirst(s_pre[B]);
+    const int k0 = w * per;
+    if (k0 >= total) return;
+    const int k1 = min(total, k0 + per);
+    const int g = blockIdx.x * kMaxWaves + wave;  // this wave's KV head
+    if (g >= a.Hkv) return;
+
+    const int rows = a.G * a.q_cnt;
+    const size_t row_bytes = (size_t)a.Hkv * D * 4;
+    const char* kbase = a.k_pool + (size_t)g * D * 4;
+    const char* vbase = a.v_pool + (size_t)g * D * 4;
+    const int x = lane & 3, b = (lane >> 2) & 3, y = lane >> 4;
+    const int kdo = 64 * b + 16 * y;  // bytes of d = 16b + 4y in a 64-d chunk (K operand)
+    const int vdo = 64 * b + 16 * x;  // bytes of d = 16b + 4x (V operand)
+    const int bs_mask = (1 << a.bs_shift) - 1;
+    char* stage = reinterpret_cast<char*>(smem) + mfma_stage_offset(B) + (size_t)wave * mfma_stage_bytes(TG);
+
+    int s = 0;
+    {
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (ufirst(s_pre[mid]) <= k0) lo = mid;
+            else hi = mid - 1;
+        }
+        s = lo;
+    }
+    for (; s < B; ++s) {
+        const int ps = ufirst(s_pre[s]);
+        const int pe = ufirst(s_pre[s + 1]);
+        if (ps >= k1) break;
+        if (pe == ps) continue;
+        const int lo_key = ufirst(s_lo[s]);
+        const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
+        const int tb = lo_key + min(k1, pe) - ps;  // one past the last
+        const bool single = (ps / per) == ((pe - 1) / per);
+        const int pos0 = SPARSE ? 0 : (a.pos ? ufirst(a.pos[s]) : a.pos_scalar);
+        const int rows_s = a.G * seq_queries(a, s);
+
+        // this lane's rows 4rg + x: Q slice (B operand), query position, first key
+        float4 qf[RG][4];  // fp32: converted at each use, which saves registers
+        int pq[RG], wsr[RG];
+        bool live[RG];
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            const int r = 4 * rg + x;
+            live[rg] = r < rows_s;
+            pq[rg] = SPARSE ? INT32_MAX : pos0 + a.j0 + r / a.G;
+            wsr[rg] = SPARSE ? 0 : window_start(pq[rg], a.window);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) qf[rg][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < rows) {
+                const float* qp = a.q + out_row(a, s, g, r) * D + 16 * b + 4 * y;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) qf[rg][q] = *reinterpret_cast<const float4*>(qp + 64 * q);
+            }
+        }
+        double m[RG], l[RG], o[RG][4][4];
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            m[rg] = -INFINITY;
+            l[rg] = 0.0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[rg][q][e] = 0.0;
+        }
+
+        const int32_t* trow = a.tables + (size_t)s * a.table_stride;
+        int64_t rbase = 0;  // ring mode: first row of the sequence's ring
+        int r0 = 0;         // ring mode: ring row of key ta
+        if constexpr (RING) {
+            rbase = a.pos ? (int64_t)ufirst(trow[0]) * a.ring_size : a.ring_base;
+            r0 = ta % a.ring_size;
+        }
+        const int kbeg = SPARSE ? ufirst(a.key_off[s]) : 0;
+        const int last_page = (tb - 1) >> a.bs_shift;
+        int pgbase = -kSW;  // page index (sparse: list index) held by lane 0 of vpg
+        int vpg = 0;
+        bool bad = false;
+
+        // Batch staging: each token's K and V slices go from global memory straight into
+        // this wave's LDS slots (one 1 KiB row per slot, slots kSlot bytes apart), so the
+        // next batch's loads are in flight while the current one is computed from registers.
+        // The operand reads take 16 bytes of token 4tg + x (K) or 4tg + y (V); the 16-byte
+        // slot padding puts the 16 lanes of each read phase on distinct banks.
+        auto issue = [&](int t, char* buf) {
+            const int tl = min(t + U - 1, tb - 1);
+            if (SPARSE && tl - pgbase >= kSW) {  // pool rows of the next 64 listed keys
+                pgbase = t;
+                int row = 0;
+                if (t + lane < tb) {
+                    const int key = a.keys[kbeg + t + lane];
+                    const int blk = key >> a.bs_shift;
+                    const int phys = (key >= 0 && blk < a.table_stride) ? trow[blk] : -1;
+                    if (phys < 0 || phys >= a.num_blocks) bad = true;
+                    else row = (phys << a.bs_shift) | (key & bs_mask);
+                }
+                vpg = row;
+            }
+            if (ADDR == kAddrPaged && (tl >> a.bs_shift) - pgbase >= kSW) {  // next 64 page ids
+                pgbase = t >> a.bs_shift;
+                int pg = 0;
+                if (pgbase + lane <= last_page) {
+                    pg = trow[pgbase + lane];
+                    if (pg < 0 || pg >= a.num_blocks) {
+                        bad = true;
+                        pg = 0;
+                    }
+                }
+                vpg = pg;
+            }
+            // One token's slice (64 lanes x 16 bytes, contiguous) per load; the address is
+            // wave-uniform: page id by readlane, offsets in scalar registers.
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const int tt = min(t + j, tb - 1);  // tokens past the piece re-read its last row
+                size_t off;
+                if constexpr (RING) {
+                    off = (size_t)ring_key_row(rbase, r0, tt - ta, a.ring_size) * row_bytes;
+                } else if constexpr (SPARSE) {
+                    off = (size_t)(uint32_t)__builtin_amdgcn_readlane(vpg, tt - pgbase) * row_bytes;
+                } else {
+                    const int pg = __builtin_amdgcn_readlane(vpg, (tt >> a.bs_shift) - pgbase);
+                    off = (((size_t)pg << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
+                }
+                __builtin_amdgcn_global_load_lds(uniform_ptr(kbase + off) + 16 * lane,
+                                                 (lds_void*)(buf + (2 * j) * kSlot), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(uniform_ptr(vbase + off) + 16 * lane,
+                                                 (lds_void*)(buf + (2 * j + 1) * kSlot), 16, 0, 0);
+            }
+        };
+
+        issue(ta, stage);
+        for (int t = ta; t < tb; t += U) {
+            __builtin_amdgcn_s_waitcnt(0);  // this batch's slices are in LDS
+            float4 kw[TG][4], vw[TG][4];
+#pragma unroll
+            for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    kw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + x)) * kSlot + kdo + 256 * q);
+                    vw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + y) + 1) * kSlot + vdo + 256 * q);
+                }
+            __builtin_amdgcn_s_waitcnt(kLgkm0);  // read out before the slots are refilled
+            if (t + U < tb) issue(t + U, stage);
+
+            // S^T, then the block sums
+            double sc[TG][RG];
+#pragma unroll
+            for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+                for (int rg = 0; rg < RG; ++rg) sc[tg][rg] = 0.0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    double qd[RG];
+#pragma unroll
+                    for (int rg = 0; rg < RG; ++rg)
+                        qd[rg] = (double)reinterpret_cast<const float*>(&qf[rg][q])[e];
+#pragma unroll
+                    for (int tg = 0; tg < TG; ++tg) {
+                        const double kd = (double)reinterpret_cast<const float*>(&kw[tg][q])[e];
+#pragma unroll
+                        for (int rg = 0; rg < RG; ++rg) sc[tg][rg] = mfma4(kd, qd[rg], sc[tg][rg]);
+                    }
+                }
+            // online softmax per row; p holds the weights, the B operand of PV
+            double p[TG][RG], scl[RG];
+            bool moved_any = false;
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                bool ok[TG];
+                double mb = -INFINITY;
+#pragma unroll
+                for (int tg = 0; tg < TG; ++tg) {
+                    const int tok = t + 4 * tg + y;
+                    ok[tg] = live[rg] && tok < tb && tok <= pq[rg] && tok >= wsr[rg];
+                    const double v = block_sum(sc[tg][rg]) * (double)a.scale;
+                    p[tg][rg] = v;
+                    if (ok[tg]) mb = fmax(mb, v);
+                }
+                mb = allreduce_hi<16>(mb, OpMax());
+                const double m_new = fmax(m[rg], mb);
+                double lb = 0.0;
+#pragma unroll
+                for (int tg = 0; tg < TG; ++tg) {
+                    const double pw = ok[tg] ? exp_acc(p[tg][rg] - m_new) : 0.0;
+                    p[tg][rg] = pw;
+                    lb += pw;
+                }
+                lb = allreduce_hi<16>(lb, OpSum());
+                const bool moved = m_new != m[rg];
+                double f = 1.0;
+                if (moved) f = exp_acc(m[rg] - m_new);  // m = -inf gives 0
+                scl[rg] = f;
+                l[rg] = l[rg] * f + lb;
+                m[rg] = m_new;
+                moved_any = moved_any || moved;
+            }
+            if (__any(moved_any)) {
+#pragma unroll
+                for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[rg][q][e] *= scl[rg];
+            }
+            // PV
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int tg = 0; tg < TG; ++tg) {
+                        const double vd = (double)reinterpret_cast<const float*>(&vw[tg][q])[e];
+#pragma unroll
+                        for (int rg = 0; rg < RG; ++rg) o[rg][q][e] = mfma4(vd, p[tg][rg], o[rg][q][e]);
+                    }
+        }
+        bad = __any(bad);
+
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            // keep the last accumulations ahead of the stores' branches
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(o[rg][q][e]));
+        }
+        if (single) {
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                const int r = 4 * rg + x;
+                if (r < rows_s) {
+                    const double inv = 1.0 / (l[rg] + 1e-10);
+                    float* op = a.out + out_row(a, s, g, r) * D + 16 * b + 4 * y;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        float4 v;
+                        v.x = bad ? __builtin_nanf("") : (float)(o[rg][q][0] * inv);
+                        v.y = bad ? __builtin_nanf("") : (float)(o[rg][q][1] * inv);
+                        v.z = bad ? __builtin_nanf("") : (float)(o[rg][q][2] * inv);
+                        v.w = bad ? __builtin_nanf("") : (float)(o[rg][q][3] * inv);
+                        *reinterpret_cast<float4*>(op + 64 * q) = v;
+                    }
+                }
+            }
+        } else {
+            const size_t slot = (size_t)(w + s) * a.rows_seq;
+            double* po = static_cast<double*>(a.part_o);
+            double* pml = static_cast<double*>(a.part_ml);
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                const int r = 4 * rg + x;
+                if (r < rows) {
+                    const int row = (r / a.G) * a.Hq + g * a.G + r % a.G;
+                    double* dst = po + (slot + row) * D + 16 * b + 4 * y;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        double2* d2 = reinterpret_cast<double2*>(dst + 64 * q);
+                        d2[0] = make_double2(o[rg][q][0], o[rg][q][1]);
+                        d2[1] = make_double2(o[rg][q][2], o[rg][q][3]);
+                    }
+                    if (b == 0 && y == 0) {
+                        pml[(slot + row) * 2 + 0] = bad ? __builtin_nan("") : m[rg];
+                        pml[(slot + row) * 2 + 1] = l[rg];
+                    }
+                }
+            }
+        }
+    }
+}
+
 // Combines the pieces of every sequence that spans more than one workgroup:
 //   out = sum_c o_c e^(m_c - M) / (sum_c l_c e^(m_c - M) + 1e-10),  M = max_c m_c,
 // the reference's softmax(x)_i = e^(x_i - max) / (sum + 1e-10). One workgroup per
@@ -843,6 +1194,42 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
 }
 
 template <int D, typename KV, int R, int WPH = 1>
+int32_t launch_r(StreamArgs a, hipStream_t st);
+constexpr size_t kMfmaLdsMax = 160 * 1024;  // LDS of one CU
+
+template <int RG, int TG, int ADDR>
+int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
+    const int waves = a.Hkv < kMaxWaves ? a.Hkv : kMaxWaves;
+    const int threads = waves * kSW;
+    const size_t lds = mfma_stage_offset(a.batch) + (size_t)waves * mfma_stage_bytes(TG);
+    if (lds > kMfmaLdsMax) return launch_r<256, float, 4, 2>(a, st);  // very large batches
+    const void* fn = reinterpret_cast<const void*>(&stream_mfma_kernel<RG, TG, ADDR>);
+    // Above 64 KiB of dynamic LDS a kernel must opt in (once per kernel and device).
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLdsMax) !=
+        hipSuccess)
+        return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
+    const int slots = fill_workgroups(fn, threads, lds);
+    if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
+    const int groups = (a.Hkv + kMaxWaves - 1) / kMaxWaves;
+    a.nwg = slots / groups > 0 ? slots / groups : 1;
+    dim3 grid(groups, a.nwg);
+    hipLaunchKernelGGL((stream_mfma_kernel<RG, TG, ADDR>), grid, dim3(threads), lds, st, a);
+    hipLaunchKernelGGL((stream_merge_kernel<256, double>), dim3(a.rows_seq, a.batch),
+                       dim3(kMergeNT), 0, st, a);
+    return PKV_OK;
+}
+
+#ifndef PKV_MFMA_TG
+#define PKV_MFMA_TG 1
+#endif
+template <int RG>
+int32_t launch_mfma(StreamArgs a, hipStream_t st) {
+    if (a.keys) return launch_mfma_addr<RG, PKV_MFMA_TG, kAddrSparse>(a, st);
+    return a.ring_size > 0 ? launch_mfma_addr<RG, PKV_MFMA_TG, kAddrRing>(a, st)
+                           : launch_mfma_addr<RG, PKV_MFMA_TG, kAddrPaged>(a, st);
+}
+
+template <int D, typename KV, int R, int WPH>
 int32_t launch_r(StreamArgs a, hipStream_t st) {
     if (a.keys) return launch_addr<D, KV, R, WPH, kAddrSparse>(a, st);
     return a.ring_size > 0 ? launch_addr<D, KV, R, WPH, kAddrRing>(a, st)
@@ -856,6 +1243,9 @@ int32_t launch_rows(StreamArgs a, int D, int rows, hipStream_t st) {
     if (D == 256) {
         if (rows <= 1) return launch_r<256, KV, 1>(a, st);
         if (rows <= 2) return launch_r<256, KV, 2>(a, st);
+        if constexpr (sizeof(KV) == 4) {  // fp32 pools: the fp64 matrix cores
+            if (rows > 4) return launch_mfma<2>(a, st);
+        }
         if (rows <= 4) return launch_r<256, KV, 4>(a, st);
         return launch_r<256, KV, 4, 2>(a, st);
     }

@@ -68,7 +68,8 @@ def _run(p, q, k, v, tables, keys, off, max_keys, B, hq, d):
     ((16, 2, 512), F32, 64, 16),     # the model's global layers, LSA's small window
     ((16, 2, 512), BF16, 128, 256),
     ((16, 8, 256), F32, 512, 1024),  # lists longer than one 256-key chunk (merge path)
-], ids=["g512-f32", "g512-bf16", "s256-long"])
+    ((16, 2, 256), F32, 256, 128),   # 8 rows per kv head at head_dim 256: the fp64 MFMA kernel
+], ids=["g512-f32", "g512-bf16", "s256-long", "g256-f32-mfma"])
 def test_sparse_lists_match_oracle(gpu, geom, kv_dtype, top_k, window):
     print(f"[sparse] {geom} {kv_dtype} top_k={top_k} window={window}", flush=True)
     rng = np.random.default_rng(top_k + window)
@@ -89,11 +90,12 @@ def test_sparse_lists_match_oracle(gpu, geom, kv_dtype, top_k, window):
     parity.check(got, ref, exact, bf16=kv_dtype == BF16, what="sparse")
 
 
-def test_sparse_empty_bad_and_overlong_lists(gpu):
+@pytest.mark.parametrize("d", [512, 256], ids=["d512", "d256-mfma"])
+def test_sparse_empty_bad_and_overlong_lists(gpu, d):
     # An empty list gives zeros; a key past the table or a list longer than max_keys NaN.
-    print("[sparse] empty / bad key / overlong", flush=True)
+    print(f"[sparse] empty / bad key / overlong, head_dim {d}", flush=True)
     rng = np.random.default_rng(3)
-    hq, hkv, d = 16, 2, 512
+    hq, hkv = 16, 2
     B = 4
     ctx = np.array([100, 100, 100, 100])
     bs, nb, stride, tables, k, v = _case(rng, B, ctx, hkv, d, F32)
