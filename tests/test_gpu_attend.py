@@ -221,6 +221,54 @@ def test_verify_query_groups(gpu, geom, q_len, window, kv_dtype):
     _batched_case(rng, 5, q_len, ctx, *geom, 16, window, kv_dtype, 0.0625)
 
 
+@pytest.mark.parametrize("hq,hkv,q_len,window", [
+    (32, 16, 4, 0),     # 16 kv heads: two workgroup head groups
+    (8, 8, 8, 0),       # G = 1: 8 queries per kv head
+    (24, 8, 2, 0),      # G = 3: 6 rows (a partly filled row group)
+    (16, 4, 2, 0),      # G = 4
+    (16, 8, 3, 600),    # 6 rows with a window
+], ids=["hkv16", "g1-q8", "g3-q2", "g4-q2", "q3-window"])
+def test_verify_fp64_mfma_geometries(gpu, hq, hkv, q_len, window):
+    # fp32 pools, head_dim 256, 5..8 query rows per kv head: stream_mfma_kernel
+    print(f"[attend] fp64 MFMA verify {hq}q/{hkv}kv q_len={q_len} window={window}", flush=True)
+    rng = np.random.default_rng(hq * 7 + hkv + q_len)
+    ctx = rng.integers(100, 1800, 5)
+    ctx[0] = 0
+    _batched_case(rng, 5, q_len, ctx, hq, hkv, 256, 16, window, F32, 0.0625)
+
+
+def test_verify_inactive_and_bad_table_mfma(gpu):
+    # The contract paths of the fp64 MFMA verify kernel (16/8/256, 4 queries = 8 rows per
+    # kv head): an inactive sequence gives zeros, a table entry outside the pool NaN, a
+    # call past max_pos NaN; the other sequences stay finite.
+    print("[attend] MFMA verify inactive / bad table", flush=True)
+    import ctypes
+    rng = np.random.default_rng(31)
+    B, hq, hkv, d, bs, nb, stride, ql = 3, 16, 8, 256, 16, 64, 8, 4
+    p = make_params(LayerSpec(hq, hkv, d), bs, nb, 0.0625)
+    tables = rng.integers(0, nb, (B, stride)).astype(np.int32)
+    tables[2, 3] = nb + 5  # out of the pool
+    k = hip.DeviceArray.from_numpy(rng.standard_normal(nb * bs * hkv * d, dtype=np.float32))
+    q = hip.DeviceArray.from_numpy(rng.standard_normal((B, ql, hq, d), dtype=np.float32))
+    out = hip.DeviceArray((B, ql, hq, d), np.float32)
+    ws_bytes = lib.load().pkv_workspace_size(ctypes.byref(p), B, ql, 127)
+    ws = hip.DeviceArray((ws_bytes,), np.uint8, zero=True)
+    dtab = hip.DeviceArray.from_numpy(tables)
+    dpos = hip.DeviceArray.from_numpy(np.array([40, -1, 60], np.int32))
+    lib.call("pkv_attend", None, ctypes.byref(p), q.ptr, k.ptr, k.ptr, dtab.ptr, stride,
+             dpos.ptr, ql, B, 127, out.ptr, ws.ptr, ws.nbytes)
+    o = out.numpy()
+    assert np.all(np.isfinite(o[0]))
+    assert np.all(o[1] == 0.0)
+    assert np.all(np.isnan(o[2]))
+    dtab2 = hip.DeviceArray.from_numpy(np.clip(tables, 0, nb - 1))
+    dpos2 = hip.DeviceArray.from_numpy(np.array([40, 125, 0], np.int32))  # 125 + 3 > 127
+    lib.call("pkv_attend", None, ctypes.byref(p), q.ptr, k.ptr, k.ptr, dtab2.ptr, stride,
+             dpos2.ptr, ql, B, 127, out.ptr, ws.ptr, ws.nbytes)
+    o = out.numpy()
+    assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[0])) and np.all(np.isfinite(o[2]))
+
+
 def test_gqa8_d512(gpu):
     rng = np.random.default_rng(12)
     ctx = rng.integers(1, 4000, 4)
