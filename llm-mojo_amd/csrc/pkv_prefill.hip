@@ -15,9 +15,10 @@
 //     needs two cross-lane steps (permlane16 / permlane32 swaps);
 //   P = exp2(S * scale * log2 e - m), split P = P_hi + P_lo (both bf16; the residual of a
 //     single bf16 rounding would break the 2e-2 output bound near zero);
-//   O^T += V^T P^T (A = V^T from LDS, B = P_hi then P_lo straight from the S^T registers):
-//     the keys of a 32-key step are taken in the order the S^T registers hold them, and
-//     V^T is stored in LDS with the same permutation, so each operand is one 16-byte read.
+//   O^T += V^T P^T (A = V^T, B = P_hi then P_lo straight from the S^T registers): the keys
+//     of a 32-key step are taken in the order the S^T registers hold them, four
+//     consecutive keys at a time, which is what one ds_read_b64_tr_b16 gathers from V
+//     kept in its natural [key][dim] layout (two such reads per operand).
 // Accumulation is fp32 throughout; the output is O / (l + 1e-10) (the reference's
 // softmax denominator, attention.mojo:151-162).
 //
@@ -40,16 +41,15 @@ constexpr int kD = 256;             // head_dim of this kernel
 constexpr int kKT = 64;             // keys per tile
 constexpr int kNT = 512;            // eight waves
 constexpr float kLog2e = 1.4426950408889634f;
-// LDS tiles, double-buffered (bf16 elements). K: [key][256] rows of 512 B whose 16-byte
-// chunk c sits at chunk c ^ (key & 15): the 16 keys of an operand read land on distinct
-// banks whether the LDS serves 8 lanes over 32 banks or 16 lanes over 64 per cycle.
-// V^T: [dim][64 keys] rows of 128 B; keys are permuted inside 32-key groups (vperm) and
-// chunk c of row d sits at chunk c ^ (((d >> 3) ^ d) & 7), which keeps the operand reads
-// conflict-free; the transposed staging writes (8 bytes per lane) conflict 2-way. A
-// conflict-free staging order (pairing lanes with permlane32 so each writes 16-byte
-// chunks) measured slower: its extra permutes cost more than the conflicts.
+// LDS tiles, double-buffered (bf16 elements), both filled straight from global memory
+// (global_load_lds), rows of 512 B:
+//   K: [key][256]; its 16-byte chunk c sits at chunk c ^ (key & 15): the 16 keys of an
+//     operand read land on distinct banks.
+//   V: [key][256]; its 32-byte chunk c (dims 16c .. 16c+15) sits at chunk c ^ (key & 15):
+//     a transposed read takes the same 32-byte chunk of 16 keys, which then lands on
+//     distinct banks.
 constexpr int kKTile = kKT * kD;    // elements per K buffer (32 KiB)
-constexpr int kVTile = kD * kKT;    // elements per V^T buffer (32 KiB)
+constexpr int kVTile = kKT * kD;    // elements per V buffer (32 KiB)
 
 struct PrefillArgs {
     const uint16_t* q;  // bf16 [rows][Hq][D]
@@ -71,13 +71,8 @@ struct PrefillArgs {
     float* out;  // fp32 [rows][Hq][D]
 };
 
-// Position of key k (0..63) of a tile inside its V^T row. Within a 32-key step, lane
-// group grp of the S^T output holds keys 16b + 4grp + r (b = 0, 1; r = 0..3); they sit at
-// positions 8grp + 4b + r, i.e. key bits [4 | 3:2 | 1:0] -> position bits [2 | 4:3 | 1:0].
-__device__ inline int vperm(int k) {
-    return (k & ~31) | (((k >> 2) & 3) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
-}
-__device__ inline int vswz(int d) { return ((d >> 3) ^ d) & 7; }
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
 
 __device__ inline float swap32_max(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -97,6 +92,15 @@ __device__ inline float swap16_sum(float x) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16 (checked on the device): inside each 16-lane group, output lane j
+// element e is element j % 4 of what input lane 4e + j / 4 addressed. With input lane a
+// addressing dims 4(a % 4) .. +3 of key k0 + a / 4, output lane j holds dim j of keys
+// k0 .. k0 + 3.
+__device__ inline s16x4 read_tr(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
 
 template <int G>
 __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
@@ -192,33 +196,18 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
                                              (lds_void*)(dst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
         }
     };
-    // V tile t: this thread's unit = 4 consecutive keys x 8 dims, staged through
-    // registers and written transposed.
-    uint4 vreg[4];
-    const int v_kg = tid >> 5, v_dc = tid & 31;
-    auto load_v = [&](int t) {
+    // V tile t -> sV[t % 2] the same way, under the 32-byte chunk swizzle: LDS 16-byte
+    // position p of key row k holds global 16-byte chunk 2 * ((p / 2) ^ (k & 15)) + p % 2.
+    auto issue_v = [&](int t) {
+        uint16_t* dst = sV + (t & 1) * kVTile;
         const int64_t* offs = s_off + (t & 3) * kKT;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            vreg[j] = *reinterpret_cast<const uint4*>(a.v_pool + offs[4 * v_kg + j] + 8 * v_dc);
-    };
-    auto store_v = [&](int t) {
-        uint16_t* dst = sV + (t & 1) * kVTile;
-        const int kp = vperm(4 * v_kg);  // 4-aligned: the 4 keys stay contiguous
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int d = 8 * v_dc + e;
-            // dim e of keys j = 0..3: 16-bit half (e & 1) of word e / 2 of vreg[j]
-            auto word = [&](int j) -> uint32_t {
-                const uint4& r = vreg[j];
-                return (e >> 1) == 0 ? r.x : (e >> 1) == 1 ? r.y : (e >> 1) == 2 ? r.z : r.w;
-            };
-            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            uint2 pk;
-            pk.x = __builtin_amdgcn_perm(word(1), word(0), sel);
-            pk.y = __builtin_amdgcn_perm(word(3), word(2), sel);
-            const int col = (((kp >> 3) ^ vswz(d)) << 3) | (kp & 7);
-            *reinterpret_cast<uint2*>(&dst[d * kKT + col]) = pk;
+        for (int j = 0; j < 4; ++j) {
+            const int key = wave * 8 + 2 * j + (lane >> 5);
+            const int p16 = lane & 31;
+            const int c = ((((p16 >> 1) ^ (key & 15)) << 1) | (p16 & 1));
+            __builtin_amdgcn_global_load_lds(a.v_pool + offs[key] + 8 * c,
+                                             (lds_void*)(dst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
         }
     };
 
@@ -246,8 +235,7 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     stage_rows(2);
     __syncthreads();
     issue_k(0);
-    load_v(0);
-    store_v(0);
+    issue_v(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -256,7 +244,7 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         const bool more = t + 1 < ntiles;
         if (more) {
             issue_k(t + 1);
-            load_v(t + 1);
+            issue_v(t + 1);
         }
         const uint16_t* cK = sK + (t & 1) * kKTile;
         const uint16_t* cV = sV + (t & 1) * kVTile;
@@ -333,11 +321,16 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
             for (int u = 0; u < 16; ++u) o[u] *= alpha;
         }
         // O^T += V^T P^T: 16 d-tiles x 2 steps of 32 keys, hi then lo; the V operand of
-        // (step ks, d-tile u) is dims 16u + l16 at positions 32ks + 8grp .. +7.
+        // (step ks, d-tile u) is dims 16u + l16 of keys 32ks + 4grp + 0..3 and
+        // 32ks + 16 + 4grp + 0..3 (elements 0..3 and 4..7), two transposed reads.
         auto vop = [&](int ks, int u) -> bf16x8 {
-            const int d = 16 * u + l16;
-            const int ch = (4 * ks + grp) ^ vswz(d);
-            return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cV[d * kKT + 8 * ch]));
+            const int kr = 32 * ks + 4 * grp + (l16 >> 2);  // key this lane addresses
+            const int dq = 4 * (l16 & 3);                    // its dims within the 16-dim tile
+            const s16x4 lo = read_tr(&cV[kr * kD + ((u ^ (kr & 15)) << 4) + dq]);
+            const int kr2 = kr + 16;
+            const s16x4 hi = read_tr(&cV[kr2 * kD + ((u ^ (kr2 & 15)) << 4) + dq]);
+            const s16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            return __builtin_bit_cast(bf16x8, v);
         };
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -352,7 +345,6 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
                 o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, pl[ks], o[u], 0, 0, 0);
             }
         }
-        if (more) store_v(t + 1);
         stage_rows(t + 3);
         __builtin_amdgcn_s_waitcnt(0);  // tile t+1's direct-to-LDS K loads have landed
         __syncthreads();
