@@ -172,6 +172,28 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
                    const int32_t* pos, int32_t batch, int32_t max_pos, float* out,
                    void* workspace, size_t workspace_bytes);
 
+/* Fused decode/verify step of one layer: pkv_append, then pkv_attend over the same pos
+ * (queries at positions pos[s] .. pos[s] + q_len - 1), as the engine's per-layer step
+ * writes the new tokens' K/V into the paged cache and attends over it
+ * (model_speculative_moe_batched.mojo:1996, :2625, :3111 write sites; :3090-3123 verify).
+ * Block tables, table lengths, free list, status, every pool byte and out are those of the
+ * two separate calls, with one exception: a sequence whose allocation fails
+ * (PKV_SEQ_OUT_OF_BLOCKS) attends positions its append did not write, through table
+ * entries past its length; if such an entry names another sequence's block, the fused
+ * launch may read that row before or after this call's append writes it.
+ * When one launch of the stream kernel's vector path covers the call (paged pools,
+ * head_dim 256 or 512, G * q_len <= 8 on the vector kernel, every kv head in one
+ * workgroup), that launch also copies the appended rows into the pool and reads them from
+ * k_new / v_new, saving the scatter launch; otherwise the append runs whole first. Arguments as in pkv_append and pkv_attend; the attention's arguments are
+ * checked before anything is launched. No reference counterpart as one call. */
+int32_t pkv_append_attend(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
+                          int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
+                          int32_t* free_list, int32_t* free_count, const int32_t* pos,
+                          const int32_t* tok_off, int32_t max_new, const void* k_new,
+                          const void* v_new, int32_t total_rows, int32_t* status, const float* q,
+                          int32_t q_len, int32_t batch, int32_t max_pos, float* out,
+                          void* workspace, size_t workspace_bytes);
+
 /* K2'' -- verify attention with a query count per sequence. The engine verifies each
  * sequence's own draft: verify_b = drafts + 1 tokens (model_speculative_moe_batched.mojo
  * :3005), fewer when drafting stopped early at a terminal token (:2990-2993), so counts

@@ -662,7 +662,7 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
                     const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                     const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
                     const int32_t* q_lens, int32_t batch, int32_t max_pos, float* out,
-                    void* workspace, size_t workspace_bytes) {
+                    void* workspace, size_t workspace_bytes, const NewRows* nr = nullptr) {
     int32_t rc = validate_params(p);
     if (rc != PKV_OK) return rc;
     if (batch <= 0 || q_len <= 0 || table_stride <= 0 || max_pos < 0)
@@ -677,7 +677,7 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     if (stream_eligible(p, G) && workspace_bytes >= stream_layout(p, batch, q_len).total) {
         rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
                            ring_base, q_len, q_lens, batch, max_pos, nullptr, nullptr, 0, out,
-                           workspace, st);
+                           workspace, st, nr);
         if (rc != PKV_OK) return rc;
         return check_launch("pkv_attend");
     }
@@ -843,6 +843,39 @@ int32_t pkv_attend(void* stream, const pkv_params* p, const float* q, const void
     if (!pos) return pkv::fail(PKV_ERR_INVALID, "pos is NULL");
     return pkv::attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0, 0,
                             q_len, nullptr, batch, max_pos, out, workspace, workspace_bytes);
+}
+
+int32_t pkv_append_attend(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
+                          int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
+                          int32_t* free_list, int32_t* free_count, const int32_t* pos,
+                          const int32_t* tok_off, int32_t max_new, const void* k_new,
+                          const void* v_new, int32_t total_rows, int32_t* status, const float* q,
+                          int32_t q_len, int32_t batch, int32_t max_pos, float* out,
+                          void* workspace, size_t workspace_bytes) {
+    using namespace pkv;
+    clear_error();
+    int32_t rc = validate_params(p);
+    if (rc != PKV_OK) return rc;
+    // The attention's arguments are checked before anything is launched.
+    if (!q || !out || !workspace || !pos) return fail(PKV_ERR_INVALID, "null device pointer");
+    if (q_len <= 0 || max_pos < 0 || batch <= 0 || batch > 4096)
+        return fail(PKV_ERR_INVALID, "q_len must be positive, max_pos >= 0, 0 < batch <= 4096");
+    if (workspace_bytes < pkv_workspace_size(p, batch, q_len, max_pos))
+        return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_workspace_size()");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // The stream kernel takes the appended rows itself when one vector-kernel launch covers
+    // the call; otherwise the append copies them first.
+    const bool fuse = stream_takes_new_rows(p, q_len) &&
+                      workspace_bytes >= stream_layout(p, batch, q_len).total;
+    rc = append_launch(st, p, k_pool, v_pool, block_tables, table_stride, table_lens, free_list,
+                       free_count, pos, tok_off, max_new, k_new, v_new, total_rows, batch, status,
+                       !fuse);
+    if (rc != PKV_OK) return rc;
+    NewRows nr{static_cast<const char*>(k_new), static_cast<const char*>(v_new), tok_off,
+               static_cast<char*>(k_pool), static_cast<char*>(v_pool), status};
+    return attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0, 0, q_len,
+                       nullptr, batch, max_pos, out, workspace, workspace_bytes,
+                       fuse ? &nr : nullptr);
 }
 
 int32_t pkv_verify(void* stream, const pkv_params* p, const float* q, const void* k_pool,

@@ -53,6 +53,30 @@ StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len);
 // True when the stream kernel covers this geometry: head_dim 256 or 512 with
 // G = num_heads / num_kv_heads <= 8 (any number of queries: launched in groups).
 bool stream_eligible(const pkv_params* p, int32_t G);
+// The appended rows of a fused append + attention (pkv_append_attend). The attention
+// launch copies row r of sequence s (tok_off[s] <= r < tok_off[s + 1], position
+// pos[s] + r - tok_off[s]) into the pool, with scatter_kernel's checks, and reads those
+// positions from k_new / v_new instead of the pool. k_new == NULL: no appended rows.
+struct NewRows {
+    const char* k_new;
+    const char* v_new;
+    const int32_t* tok_off;  // [batch + 1]
+    char* k_dst;             // the pools, written
+    char* v_dst;
+    int32_t* status;         // per sequence, from the block allocation
+};
+// True when stream_attend takes the appended rows itself for q_len queries: paged pools
+// and one launch on the vector kernel.
+bool stream_takes_new_rows(const pkv_params* p, int32_t q_len);
+// Validates a paged or ring append and launches it (pkv_state.hip): the block allocation,
+// then, with scatter, the row copies.
+int32_t append_launch(hipStream_t st, const pkv_params* p, void* k_pool, void* v_pool,
+                      int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
+                      int32_t* free_list, int32_t* free_count, const int32_t* pos,
+                      const int32_t* tok_off, int32_t max_new, const void* k_new,
+                      const void* v_new, int32_t total_rows, int32_t batch, int32_t* status,
+                      bool scatter);
+
 // pos == NULL: one sequence at pos_scalar; in ring mode its ring starts at row
 // ring_base (otherwise ring slot block_tables[s * table_stride] starts at row
 // slot * ring_size). keys != NULL: sparse mode, sequence s attends the key positions
@@ -63,7 +87,7 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
                       const int32_t* q_lens, int32_t batch, int32_t max_pos, const int32_t* keys,
                       const int32_t* key_off, int32_t max_keys, float* out, void* workspace,
-                      hipStream_t st);
+                      hipStream_t st, const NewRows* nr = nullptr);
 
 __host__ __device__ inline int32_t window_start(int32_t pos, int32_t window) {
     if (window <= 0) return 0;

@@ -557,17 +557,13 @@ __global__ __launch_bounds__(kNT) void rollback_kernel(RollbackArgs a) {
 }
 
 }  // namespace
-}  // namespace pkv
 
-extern "C" {
-
-int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
-                   int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
-                   int32_t* free_list, int32_t* free_count, const int32_t* pos,
-                   const int32_t* tok_off, int32_t max_new, const void* k_new,
-                   const void* v_new, int32_t total_rows, int32_t batch, int32_t* status) {
-    using namespace pkv;
-    clear_error();
+int32_t append_launch(hipStream_t st, const pkv_params* p, void* k_pool, void* v_pool,
+                      int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
+                      int32_t* free_list, int32_t* free_count, const int32_t* pos,
+                      const int32_t* tok_off, int32_t max_new, const void* k_new,
+                      const void* v_new, int32_t total_rows, int32_t batch, int32_t* status,
+                      bool scatter) {
     int32_t rc = validate_params(p);
     if (rc != PKV_OK) return rc;
     if (batch <= 0 || max_new <= 0 || table_stride <= 0 || total_rows <= 0)
@@ -601,11 +597,27 @@ int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool
     // Tokens per scatter workgroup: ~64 KiB of K+V copies each (4 tokens at 8 x 256 fp32).
     const int tpw = (64 * 1024) / (2 * a.row_bytes);
     a.tok_per_wg = tpw < 1 ? 1 : tpw;
-    hipStream_t st = static_cast<hipStream_t>(stream);
     if (!ring) hipLaunchKernelGGL(alloc_kernel, dim3(1), dim3(kNT), 0, st, a);
-    dim3 grid((max_new + a.tok_per_wg - 1) / a.tok_per_wg, batch);
-    hipLaunchKernelGGL(scatter_kernel, grid, dim3(kNT), 0, st, a);
+    if (scatter) {
+        dim3 grid((max_new + a.tok_per_wg - 1) / a.tok_per_wg, batch);
+        hipLaunchKernelGGL(scatter_kernel, grid, dim3(kNT), 0, st, a);
+    }
     return check_launch("pkv_append");
+}
+
+}  // namespace pkv
+
+extern "C" {
+
+int32_t pkv_append(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
+                   int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
+                   int32_t* free_list, int32_t* free_count, const int32_t* pos,
+                   const int32_t* tok_off, int32_t max_new, const void* k_new,
+                   const void* v_new, int32_t total_rows, int32_t batch, int32_t* status) {
+    pkv::clear_error();
+    return pkv::append_launch(static_cast<hipStream_t>(stream), p, k_pool, v_pool, block_tables,
+                              table_stride, table_lens, free_list, free_count, pos, tok_off,
+                              max_new, k_new, v_new, total_rows, batch, status, true);
 }
 
 int32_t pkv_append_qkv(void* stream, const pkv_params* p, int32_t is_global, void* k_pool,

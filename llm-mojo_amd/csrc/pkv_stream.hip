@@ -343,6 +343,7 @@ struct StreamArgs {
     void* part_ml;     // Acc (m, l) per (slot, row)
     void* part_o;      // Acc [D] per (slot, row)
     float* out;
+    NewRows nr;        // fused append (paged, vector kernel); nr.k_new == NULL: none
 };
 
 // Queries of sequence s in this launch (the rest of its rows are left untouched).
@@ -456,6 +457,57 @@ __device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo) {
     return per;
 }
 
+// Fused append: the appended rows (NewRows) of sequences w, w + nwg, ... go into the pool
+// from workgroup w, the first wave of each kv head copying that head's slice, with the
+// checks of scatter_kernel (pkv_state.hip): sequences whose allocation failed or at a
+// negative position are skipped, and a table entry outside the pool skips its row and
+// reports PKV_SEQ_BAD_BLOCK. The launch has one head group, so each sequence's status is
+// read and written by one workgroup only, reads first.
+template <int D, typename KV, int WPH>
+__device__ inline void copy_new_rows(const StreamArgs& a, int wave, int lane) {
+    constexpr int kElt = SKV<KV>::kElt;
+    constexpr int kVec = D * kElt / 16;  // 16-byte vectors per head slice
+    __shared__ int s_bad;
+    const int g = wave / WPH;
+    const bool copier = wave % WPH == 0 && g < a.Hkv;
+    const size_t row_bytes = (size_t)a.Hkv * D * kElt;
+    const size_t head_off = (size_t)g * D * kElt;
+    const int bs_mask = (1 << a.bs_shift) - 1;
+    for (int s = blockIdx.y; s < a.batch; s += a.nwg) {
+        const bool ok = a.nr.status[s] == PKV_SEQ_OK;
+        if (threadIdx.x == 0) s_bad = 0;
+        __syncthreads();  // every read of status[s] before its write below
+        const int p0 = a.pos[s];
+        const int r0 = a.nr.tok_off[s];
+        const int n = a.nr.tok_off[s + 1] - r0;
+        if (copier && ok && p0 >= 0 && n > 0) {
+            const int32_t* table = a.tables + (size_t)s * a.table_stride;
+            for (int b = 0; b < n; ++b) {
+                const int p = p0 + b;
+                const int phys = table[p >> a.bs_shift];
+                if (phys < 0 || phys >= a.num_blocks) {
+                    s_bad = 1;
+                    continue;
+                }
+                const size_t dst = (((size_t)phys << a.bs_shift) | (size_t)(p & bs_mask)) * row_bytes + head_off;
+                const size_t src = ((size_t)r0 + b) * row_bytes + head_off;
+                const uint4* ks = reinterpret_cast<const uint4*>(a.nr.k_new + src);
+                const uint4* vs = reinterpret_cast<const uint4*>(a.nr.v_new + src);
+                uint4* kd = reinterpret_cast<uint4*>(a.nr.k_dst + dst);
+                uint4* vd = reinterpret_cast<uint4*>(a.nr.v_dst + dst);
+                for (int i = lane; i < kVec; i += kSW) {
+                    const uint4 kv = ks[i];
+                    const uint4 vv = vs[i];
+                    kd[i] = kv;
+                    vd[i] = vv;
+                }
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0 && s_bad) a.nr.status[s] = PKV_SEQ_BAD_BLOCK;
+    }
+}
+
 // R query rows per wave; WPH waves per KV head split the head's rows (WPH = 2 gives two
 // waves of R rows each, reading the same K/V: the second read of a row slice hits the cache).
 // ADDR: kAddrPaged, kAddrRing (key t at row ring_base + t % ring_size) or kAddrSparse.
@@ -484,6 +536,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     const int B = a.batch;
 
     const int per = stream_setup<D, ADDR>(a, s_pre, s_lo);
+    if (ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0) copy_new_rows<D, KV, WPH>(a, wave, lane);
     const int total = ufirst(s_pre[B]);
     const int k0 = w * per;
     if (k0 >= total) return;
@@ -569,6 +622,17 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         int pgbase = -kSW;  // page index held by lane 0 of vpg
         int vpg = 0;
         bool bad = false;
+        // Fused append: positions [pn_lo, pn_hi) come from k_new / v_new (row r0 + t - pos).
+        int pn_lo = INT32_MAX, pn_hi = INT32_MIN, nr0 = 0;
+        if (ADDR == kAddrPaged && a.nr.k_new) {
+            const int r0 = ufirst(a.nr.tok_off[s]);
+            const int n = ufirst(a.nr.tok_off[s + 1]) - r0;
+            if (ufirst(a.nr.status[s]) == PKV_SEQ_OK && pos0 >= 0 && n > 0) {
+                pn_lo = pos0;
+                pn_hi = pos0 + n;
+                nr0 = r0;
+            }
+        }
 
         for (int t = ta; t < tb; t += U) {
             const int tl = min(t + U - 1, tb - 1);
@@ -599,20 +663,35 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             // K and V rows of the batch, all in flight together (tokens past the piece
             // re-read its last row and are masked).
             uint32_t kw[U][NWD], vw[U][NWD];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int tt = min(t + u, tb - 1);
-                size_t off;
+            auto row_off = [&](int tt) -> size_t {
                 if constexpr (RING) {
-                    off = (size_t)ring_key_row(rbase, r0, tt - ta, a.ring_size) * row_bytes;
+                    return (size_t)ring_key_row(rbase, r0, tt - ta, a.ring_size) * row_bytes;
                 } else if constexpr (SPARSE) {
-                    off = (size_t)(uint32_t)__builtin_amdgcn_readlane(vpg, tt - pgbase) * row_bytes;
+                    return (size_t)(uint32_t)__builtin_amdgcn_readlane(vpg, tt - pgbase) * row_bytes;
                 } else {
                     const int page = __builtin_amdgcn_readlane(vpg, (tt >> a.bs_shift) - pgbase);
-                    off = (((size_t)page << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
+                    return (((size_t)page << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
                 }
-                load_words<NWD>(uniform_ptr(kbase + off) + lane_off, kw[u]);
-                load_words<NWD>(uniform_ptr(vbase + off) + lane_off, vw[u]);
+            };
+            if (ADDR == kAddrPaged && t + U > pn_lo && t < pn_hi) {
+                // the batch holding appended rows (fused append): those come from k_new / v_new
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int tt = min(t + u, tb - 1);
+                    const bool fresh = tt >= pn_lo && tt < pn_hi;
+                    const size_t off = fresh ? (size_t)(nr0 + (tt - pn_lo)) * row_bytes : row_off(tt);
+                    const char* kb = fresh ? a.nr.k_new + (size_t)g * D * kElt : kbase;
+                    const char* vb = fresh ? a.nr.v_new + (size_t)g * D * kElt : vbase;
+                    load_words<NWD>(uniform_ptr(kb + off) + lane_off, kw[u]);
+                    load_words<NWD>(uniform_ptr(vb + off) + lane_off, vw[u]);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const size_t off = row_off(min(t + u, tb - 1));
+                    load_words<NWD>(uniform_ptr(kbase + off) + lane_off, kw[u]);
+                    load_words<NWD>(uniform_ptr(vbase + off) + lane_off, vw[u]);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);  // keep all 2U loads ahead of the math
             // scores
@@ -1273,12 +1352,26 @@ bool stream_eligible(const pkv_params* p, int32_t G) {
     return (p->head_dim == 256 || p->head_dim == 512) && G >= 1 && G <= 8;
 }
 
+bool stream_takes_new_rows(const pkv_params* p, int32_t q_len) {
+    const int G = p->num_heads / p->num_kv_heads;
+    if (p->ring_size > 0 || !stream_eligible(p, G)) return false;
+    const int rows = G * q_len;
+    if (rows > 8) return false;  // one launch (no query groups)
+    const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
+    if (p->head_dim == 256 && !bf16 && rows > 4) return false;  // the fp64 MFMA kernel
+    // one head group: every kv head's waves in one workgroup
+    int wph = 1;
+    if (p->head_dim == 256) wph = (!bf16 || rows <= 4) ? 1 : 2;
+    else wph = rows <= 2 ? 1 : (rows <= 4 ? 2 : 4);
+    return p->num_kv_heads * wph <= kMaxWaves;
+}
+
 int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const void* v_pool, const int32_t* block_tables, int32_t table_stride,
                       const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
                       const int32_t* q_lens, int32_t batch, int32_t max_pos, const int32_t* keys,
                       const int32_t* key_off, int32_t max_keys, float* out, void* workspace,
-                      hipStream_t st) {
+                      hipStream_t st, const NewRows* nr) {
     const int G = p->num_heads / p->num_kv_heads;
     if (!stream_eligible(p, G)) return fail(PKV_ERR_UNSUPPORTED, "stream path: geometry");
     StreamLayout lay = stream_layout(p, batch, q_len);
@@ -1311,6 +1404,11 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.part_ml = ws + lay.ml_off;
     a.part_o = ws + lay.o_off;
     a.out = out;
+    if (nr) {
+        if (!stream_takes_new_rows(p, q_len))
+            return fail(PKV_ERR_UNSUPPORTED, "stream path: appended rows need one vector-kernel launch");
+        a.nr = *nr;
+    }
     const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
     // Queries in groups of at most 8 query rows per kv head, one launch pair each; the
     // launches share the workspace in stream order.

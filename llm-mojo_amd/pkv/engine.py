@@ -236,6 +236,25 @@ class PagedKVCache:
                  self.max_pos if max_pos is None else max_pos, _ptr(out), self.workspace.ptr,
                  self.workspace.nbytes)
 
+    def append_attend(self, layer: int, pos, tok_off, k_new, v_new, max_new: int,
+                      total_rows: int, q, q_len: int, out, batch: int | None = None,
+                      max_pos: int | None = None):
+        """append() then attend() over the same pos in one call (pkv_append_attend): where
+        the stream kernel's vector path covers the call, its launch also writes the new
+        rows into the pool, saving the scatter launch. Same results as the two calls.
+        Returns the device status array."""
+        b = batch or self.max_seqs
+        p = self.params[layer]
+        tables, stride = self._tables_of(layer)
+        lib.call("pkv_append_attend", self._stream(), ctypes.byref(p), self.k_pools[layer].ptr,
+                 self.v_pools[layer].ptr, tables, stride, self.table_lens.ptr,
+                 self.free_list.ptr, self.free_count.ptr, self._ints(pos, self._i32_a, b),
+                 self._ints(tok_off, self._i32_b, b + 1), max_new, _ptr(k_new), _ptr(v_new),
+                 total_rows, self.status.ptr, _ptr(q), q_len, b,
+                 self.max_pos if max_pos is None else max_pos, _ptr(out), self.workspace.ptr,
+                 self.workspace.nbytes)
+        return self.status
+
     def verify(self, layer: int, q, pos, q_lens, max_q_len: int, out, batch: int | None = None,
                max_pos: int | None = None):
         """Verify attention with a query count per sequence (pkv_verify): q / out device

@@ -64,6 +64,8 @@ PROTOTYPES = {
                                  _vp, _sz]),
     "pkv_verify": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp,
                           _vp, _sz]),
+    "pkv_append_attend": (_i32, [_vp, _PP, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32,
+                                 _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _sz]),
     "pkv_q4_matmul_workspace_size": (_sz, [_i32, _i32, _i32]),
     "pkv_q4_matmul": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _sz]),
     "pkv_lsa_max_keys": (_i32, [_i32, _i32, _i32]),

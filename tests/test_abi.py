@@ -167,3 +167,24 @@ def test_verify_rejections_before_launch():
     p64 = _params(head_dim=64)
     assert L.pkv_verify(None, ctypes.byref(p64), ptr, ptr, ptr, ptr, 8, ptr, ptr, 4, 2, 100, ptr,
                         ptr, 1 << 20) == lib.PKV_ERR_UNSUPPORTED
+
+
+def test_append_attend_rejections_before_launch():
+    # The fused step checks the attention's arguments, then the append's, before any launch.
+    L = lib.load()
+    p = _params()
+    ptr = 16
+    ws = L.pkv_workspace_size(ctypes.byref(p), 4, 1, 100)
+
+    def call(q=ptr, q_len=1, ws_bytes=ws, k_new=ptr, status=ptr, batch=4, max_pos=100):
+        return L.pkv_append_attend(None, ctypes.byref(p), ptr, ptr, ptr, 8, ptr, ptr, ptr, ptr,
+                                   ptr, 1, k_new, ptr, 4, status, q, q_len, batch, max_pos, ptr,
+                                   ptr, ws_bytes)
+
+    assert call(q=None) == lib.PKV_ERR_INVALID
+    assert call(q_len=0) == lib.PKV_ERR_INVALID
+    assert call(max_pos=-1) == lib.PKV_ERR_INVALID
+    assert call(batch=5000) == lib.PKV_ERR_INVALID
+    assert call(ws_bytes=ws - 1) == lib.PKV_ERR_WORKSPACE
+    assert call(k_new=None) == lib.PKV_ERR_INVALID
+    assert call(status=None) == lib.PKV_ERR_INVALID
