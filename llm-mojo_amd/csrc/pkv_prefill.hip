@@ -50,6 +50,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 //     distinct banks.
 constexpr int kKTile = kKT * kD;    // elements per K buffer (32 KiB)
 constexpr int kVTile = kKT * kD;    // elements per V buffer (32 KiB)
+constexpr int kVAhead = 6;          // PV operands requested ahead of the matrix cores
+// __builtin_amdgcn_sched_group_barrier instruction classes
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 
 struct PrefillArgs {
     const uint16_t* q;  // bf16 [rows][Hq][D]
@@ -182,32 +186,33 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
             s_off[(t & 3) * kKT + tid] = (int64_t)row * (int64_t)row_elems + (int64_t)head_off;
         }
     };
-    // K tile t -> sK[t % 2] straight from global memory into LDS: each wave instruction
-    // fills two key rows (1 KiB); lane i loads the global chunk that belongs at chunk
-    // i % 32 of its row under the swizzle. Eight waves x 4 instructions = 64 rows.
-    auto issue_k = [&](int t) {
-        uint16_t* dst = sK + (t & 1) * kKTile;
+    // K and V tiles t -> sK[t % 2], sV[t % 2] straight from global memory into LDS: each
+    // wave instruction fills two key rows (1 KiB), eight waves x 4 instructions = 64 rows.
+    // The wave's four key offsets are read from s_off once, for K and V both. Lane i loads
+    // the global chunk that belongs at 16-byte position i % 32 of its row: for K that is
+    // chunk (i % 32) ^ (key & 15); for V, LDS position p of key row k holds global chunk
+    // 2 * ((p / 2) ^ (k & 15)) + p % 2 (the 32-byte chunk swizzle).
+    auto issue_kv = [&](int t) {
+        uint16_t* kdst = sK + (t & 1) * kKTile;
+        uint16_t* vdst = sV + (t & 1) * kVTile;
         const int64_t* offs = s_off + (t & 3) * kKT;
+        int64_t ko[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ko[j] = offs[wave * 8 + 2 * j + (lane >> 5)];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int key = wave * 8 + 2 * j + (lane >> 5);
             const int c = (lane & 31) ^ (key & 15);
-            __builtin_amdgcn_global_load_lds(a.k_pool + offs[key] + 8 * c,
-                                             (lds_void*)(dst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.k_pool + ko[j] + 8 * c,
+                                             (lds_void*)(kdst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
         }
-    };
-    // V tile t -> sV[t % 2] the same way, under the 32-byte chunk swizzle: LDS 16-byte
-    // position p of key row k holds global 16-byte chunk 2 * ((p / 2) ^ (k & 15)) + p % 2.
-    auto issue_v = [&](int t) {
-        uint16_t* dst = sV + (t & 1) * kVTile;
-        const int64_t* offs = s_off + (t & 3) * kKT;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int key = wave * 8 + 2 * j + (lane >> 5);
             const int p16 = lane & 31;
             const int c = ((((p16 >> 1) ^ (key & 15)) << 1) | (p16 & 1));
-            __builtin_amdgcn_global_load_lds(a.v_pool + offs[key] + 8 * c,
-                                             (lds_void*)(dst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.v_pool + ko[j] + 8 * c,
+                                             (lds_void*)(vdst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
         }
     };
 
@@ -234,23 +239,20 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     stage_rows(1);
     stage_rows(2);
     __syncthreads();
-    issue_k(0);
-    issue_v(0);
+    issue_kv(0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     for (int t = 0; t < ntiles; ++t) {
         const int kb = kb0 + t * kKT;
-        const bool more = t + 1 < ntiles;
-        if (more) {
-            issue_k(t + 1);
-            issue_v(t + 1);
-        }
+        if (t + 1 < ntiles) issue_kv(t + 1);
         const uint16_t* cK = sK + (t & 1) * kKTile;
         const uint16_t* cV = sV + (t & 1) * kVTile;
 
-        // S^T = K Q^T: four 16-key sub-tiles (independent accumulators), K operands read
-        // one step ahead.
+        // S^T = K Q^T: four 16-key sub-tiles (independent accumulators). The K operands of
+        // 32-dim step c + 2 are requested while step c runs on the matrix cores; the
+        // scheduling groups below keep that order (the compiler otherwise waits for each
+        // read right after issuing it).
         f32x4 st[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) st[u] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -259,19 +261,28 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
             const int ch = (4 * c + grp) ^ (key & 15);
             return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cK[key * kD + 8 * ch]));
         };
-        bf16x8 ka[2][4];
+        bf16x8 ka[3][4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) ka[0][u] = kop(u, 0);
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ka[c][u] = kop(u, c);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            if (c + 1 < 8) {
+            if (c + 2 < 8) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) ka[(c + 1) & 1][u] = kop(u, c + 1);
+                for (int u = 0; u < 4; ++u) ka[(c + 2) % 3][u] = kop(u, c + 2);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[c & 1][u], qreg[c], st[u], 0, 0, 0);
+                st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[c % 3][u], qreg[c], st[u], 0, 0, 0);
         }
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+#pragma unroll
+        for (int c = 0; c < 6; ++c) {
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
         // Tiles that straddle a row's causal edge or window start get -inf outside
         // [window_start(qpos), qpos]; st[u][r] is key kb + 16u + 4grp + r. Rows past the
         // chunk are never written, so they need no mask.
@@ -300,19 +311,26 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         const float m_use = m_new == -INFINITY ? 0.f : m_new;
         // v_exp_f32 directly: results below 2^-126 flush to zero, immaterial next to the
         // row sum. P = P_hi + P_lo, both bf16, packed as the B operand of each 32-key step:
-        // element e of step ks is sub-tile 2ks + e/4, register e % 4.
+        // element e of step ks is sub-tile 2ks + e/4, register e % 4. P_hi is p truncated
+        // to bf16 (its top 16 bits, so two of them pack with one permute) and P_lo the exact
+        // remainder p - P_hi rounded to nearest: |p - P_hi - P_lo| <= 2^-16 p.
         float lsum[2] = {0.f, 0.f};
         bf16x8 ph[2], pl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float x = st[2 * ks + (e >> 2)][e & 3];
-                const float p = __builtin_amdgcn_exp2f(fmaf(x, a.scale_log2, -m_use));
-                lsum[e & 1] += p;
-                const __bf16 h = (__bf16)p;
-                ph[ks][e] = h;
-                pl[ks][e] = (__bf16)(p - (float)h);
+            for (int e = 0; e < 8; e += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(st[2 * ks + (e >> 2)][e & 3], a.scale_log2, -m_use));
+                const float p1 =
+                    __builtin_amdgcn_exp2f(fmaf(st[2 * ks + (e >> 2)][(e & 3) + 1], a.scale_log2, -m_use));
+                lsum[0] += p0;
+                lsum[1] += p1;
+                const uint32_t u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
+                const uint32_t hp = (u0 >> 16) | (u1 & 0xffff0000u);
+                ph[ks][e] = __builtin_bit_cast(__bf16, (uint16_t)hp);
+                ph[ks][e + 1] = __builtin_bit_cast(__bf16, (uint16_t)(hp >> 16));
+                pl[ks][e] = (__bf16)(p0 - __uint_as_float(u0 & 0xffff0000u));
+                pl[ks][e + 1] = (__bf16)(p1 - __uint_as_float(u1 & 0xffff0000u));
             }
         l = l * alpha + (lsum[0] + lsum[1]);
         m = m_new;
@@ -332,18 +350,28 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
             const s16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
             return __builtin_bit_cast(bf16x8, v);
         };
+        // The 32 (step, d-tile) operands run as one pipeline, kVAhead operands requested
+        // ahead of the matrix cores (across the step boundary too), and the scheduling
+        // groups interleave each operand's two reads with two MFMAs.
+        {
+            bf16x8 va[kVAhead];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            bf16x8 va[4];
+            for (int i = 0; i < kVAhead; ++i) va[i] = vop(i / 16, i % 16);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) va[u] = vop(ks, u);
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const bf16x8 cur = va[u & 3];
-                if (u + 4 < 16) va[u & 3] = vop(ks, u + 4);
+            for (int i = 0; i < 32; ++i) {
+                const int ks = i / 16, u = i % 16;
+                const bf16x8 cur = va[i % kVAhead];
+                if (i + kVAhead < 32) va[i % kVAhead] = vop((i + kVAhead) / 16, (i + kVAhead) % 16);
                 o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, ph[ks], o[u], 0, 0, 0);
                 o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, pl[ks], o[u], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kVAhead, 1);
+#pragma unroll
+            for (int i = 0; i < 32 - kVAhead; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 1);
+                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+            }
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kVAhead, 1);
         }
         stage_rows(t + 3);
         __builtin_amdgcn_s_waitcnt(0);  // tile t+1's direct-to-LDS K loads have landed
