@@ -84,8 +84,11 @@ __device__ inline bf16x8 weights_bf16(uint32_t w) {
 // block. (With a runtime tile count a chain ended in a branch and the first register of
 // its result was read in the target block without the MFMA's wait states: a wrong,
 // varying value in every fourth row.)
+// Up to two column tiles the kernel fits 80 VGPRs, which keeps three workgroups per CU
+// resident (six waves per SIMD): the 704 workgroups of an 8192 -> 2816 call then run in
+// one round instead of two.
 template <int TILES, int KB>
-__global__ __launch_bounds__(kQ4Waves * 64) void q4_matmul_kernel(Q4Args a) {
+__global__ __launch_bounds__(kQ4Waves * 64, TILES <= 2 ? 6 : 1) void q4_matmul_kernel(Q4Args a) {
     constexpr int NT = kQ4Waves * 64;
     constexpr int BPW = KB / kQ4WK;  // blocks per wave
     // x slice in B-operand order: slot ((ct * KB + b) * 2 + h) * 64 + lane holds inputs
