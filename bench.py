@@ -998,8 +998,8 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures the paged KV path on one GPU only: every GPU box here has "
-              "one GPU and this path has no multi-GPU leg (sharding is design-only, see "
-              "DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "one GPU and this path has no multi-GPU leg (splitting sequences or heads "
+              "across GPUs is not built). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     def log(msg):
