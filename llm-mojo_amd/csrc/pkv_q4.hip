@@ -36,6 +36,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kQ4WR = 2;                       // row halves per workgroup
 constexpr int kQ4WK = 4;                       // K quarters per workgroup
@@ -98,7 +99,8 @@ __global__ __launch_bounds__(kQ4Waves * 64, TILES <= 2 ? 6 : 1) void q4_matmul_k
     constexpr int kRed = kQ4WR * 2 * kQ4ATiles * TILES * 64;  // f32x4 per pair of quarters
     static_assert(kRed * 16 <= kSlots * 16, "quarter sums fit the x slice");
     __shared__ uint4 s_x[kSlots];
-    __shared__ float s_sc[kQ4Waves][BPW][64];
+    __shared__ uint4 s_w[kQ4Rows * KB];                                  // weights, see below
+    __shared__ __attribute__((aligned(16))) float s_sc[KB][kQ4Rows];     // scales [block][row]
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -115,7 +117,7 @@ __global__ __launch_bounds__(kQ4Waves * 64, TILES <= 2 ? 6 : 1) void q4_matmul_k
     const int kb0 = wk * BPW;                      // this wave's first block in the split
     const int blk0 = split * KB;
 
-    // Requests first: x staging, scales (lane = row), weights.
+    // Requests first: x staging, weights (straight to LDS), scales.
     constexpr int kStage = TILES * 16 * KB * 8 / NT;  // float4 per thread
     static_assert(kStage * NT == TILES * 16 * KB * 8, "whole float4 per thread");
     float4 xs[kStage];
@@ -127,24 +129,28 @@ __global__ __launch_bounds__(kQ4Waves * 64, TILES <= 2 ? 6 : 1) void q4_matmul_k
         if (col < a.batch && blk0 + b < a.nb)
             xs[i] = *reinterpret_cast<const float4*>(a.x + (size_t)col * a.c_in + (size_t)(blk0 + b) * 32 + 4 * m);
     }
-    float sc[BPW];
+    // Weights: the workgroup's rows x KB blocks (each row's KB * 16 contiguous bytes) go
+    // straight into LDS, 16 bytes per lane; row r's block b sits at position b ^ (r % 8)
+    // of its LDS row, so the 4-byte A-operand reads of 16 rows spread over the banks. Rows
+    // and blocks outside the matrix load a valid chunk and are replaced by zero weights
+    // when read.
+    constexpr int kWChunks = kQ4Rows * KB / (kQ4Waves * 64);  // DMA instructions per wave
+    static_assert(kWChunks * kQ4Waves * 64 == kQ4Rows * KB && KB == 8, "whole chunks per wave");
 #pragma unroll
-    for (int bb = 0; bb < BPW; ++bb) {
-        const int row = row0 + lane, b = blk0 + kb0 + bb;
-        sc[bb] = (row < a.c_out && b < a.nb) ? a.scales[(size_t)row * a.nb + b] : 0.f;
+    for (int j = 0; j < kWChunks; ++j) {
+        const int pos = (wave * kWChunks + j) * 64 + lane;
+        const int r = pos / KB, b = (pos % KB) ^ (r & 7);
+        const bool in = grow0 + r < a.c_out && blk0 + b < a.nb;
+        const uint8_t* src = in ? a.w + (size_t)(grow0 + r) * (a.c_in / 2) + (size_t)(blk0 + b) * 16 : a.w;
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(s_w + (wave * kWChunks + j) * 64), 16, 0, 0);
     }
-    uint32_t wv[kQ4ATiles][BPW];
+    // Scales: eight lanes read a row's KB consecutive scales; stored [block][row].
+    constexpr int kScPer = kQ4Rows * KB / NT;
+    float sc[kScPer];
 #pragma unroll
-    for (int t = 0; t < kQ4ATiles; ++t) {
-        const int row = row0 + 16 * t + (lane & 15);
-#pragma unroll
-        for (int bb = 0; bb < BPW; ++bb) {
-            const int b = blk0 + kb0 + bb;
-            wv[t][bb] = 0x88888888u;  // zeros after the offset (outside the matrix)
-            if (row < a.c_out && b < a.nb)
-                wv[t][bb] = *reinterpret_cast<const uint32_t*>(a.w + (size_t)row * (a.c_in / 2) +
-                                                               (size_t)b * 16 + g * 4);
-        }
+    for (int i = 0; i < kScPer; ++i) {
+        const int e = tid + i * NT, r = e / KB, b = e % KB;
+        sc[i] = (grow0 + r < a.c_out && blk0 + b < a.nb) ? a.scales[(size_t)(grow0 + r) * a.nb + blk0 + b] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < kStage; ++i) {
@@ -154,8 +160,24 @@ __global__ __launch_bounds__(kQ4Waves * 64, TILES <= 2 ? 6 : 1) void q4_matmul_k
         s_x[((ct * KB + b) * 2 + h) * 64 + l] = *reinterpret_cast<const uint4*>(&xs[i]);
     }
 #pragma unroll
-    for (int bb = 0; bb < BPW; ++bb) s_sc[wave][bb][lane] = sc[bb];
+    for (int i = 0; i < kScPer; ++i) {
+        const int e = tid + i * NT;
+        s_sc[e % KB][e / KB] = sc[i];
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's weight chunks have landed
     __syncthreads();
+    uint32_t wv[kQ4ATiles][BPW];
+#pragma unroll
+    for (int t = 0; t < kQ4ATiles; ++t) {
+        const int r = wr * kQ4ATiles * 16 + 16 * t + (lane & 15);  // row in the workgroup
+#pragma unroll
+        for (int bb = 0; bb < BPW; ++bb) {
+            const int b = kb0 + bb;
+            const uint32_t v = reinterpret_cast<const uint32_t*>(s_w)[(r * KB + (b ^ (r & 7))) * 4 + g];
+            // zeros after the offset outside the matrix
+            wv[t][bb] = (grow0 + r < a.c_out && blk0 + b < a.nb) ? v : 0x88888888u;
+        }
+    }
 
     f32x4 acc[kQ4ATiles][TILES];
 #pragma unroll
@@ -184,7 +206,8 @@ __global__ __launch_bounds__(kQ4Waves * 64, TILES <= 2 ? 6 : 1) void q4_matmul_k
 #pragma unroll
         for (int t = 0; t < kQ4ATiles; ++t) {
             const bf16x8 A = weights_bf16(wv[t][bb]);
-            const f32x4 s4 = *reinterpret_cast<const f32x4*>(&s_sc[wave][bb][16 * t + 4 * g]);
+            const f32x4 s4 =
+                *reinterpret_cast<const f32x4*>(&s_sc[kb0 + bb][wr * kQ4ATiles * 16 + 16 * t + 4 * g]);
 #pragma unroll
             for (int ct = 0; ct < TILES; ++ct) {
                 f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
