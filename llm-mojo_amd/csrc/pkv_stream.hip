@@ -1007,36 +1007,54 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                     }
                 }
             // online softmax per row; p holds the weights, the B operand of PV
-            double p[TG][RG], scl[RG];
+            double p[TG][RG], scl[RG], m_new[RG];
+            bool ok[TG][RG];
             bool moved_any = false;
 #pragma unroll
             for (int rg = 0; rg < RG; ++rg) {
-                bool ok[TG];
                 double mb = -INFINITY;
 #pragma unroll
                 for (int tg = 0; tg < TG; ++tg) {
                     const int tok = t + 4 * tg + y;
-                    ok[tg] = live[rg] && tok < tb && tok <= pq[rg] && tok >= wsr[rg];
+                    ok[tg][rg] = live[rg] && tok < tb && tok <= pq[rg] && tok >= wsr[rg];
                     const double v = block_sum(sc[tg][rg]) * (double)a.scale;
                     p[tg][rg] = v;
-                    if (ok[tg]) mb = fmax(mb, v);
+                    if (ok[tg][rg]) mb = fmax(mb, v);
                 }
                 mb = allreduce_hi<16>(mb, OpMax());
-                const double m_new = fmax(m[rg], mb);
+                m_new[rg] = fmax(m[rg], mb);
+            }
+            // Every block holds the same scores. With two row groups, blocks of even index
+            // take row group 0's exponentials and odd ones row group 1's, and a rotation by
+            // one block (4 lanes, the opposite parity) hands each lane the other half.
+#pragma unroll
+            for (int tg = 0; tg < TG; ++tg) {
+                if constexpr (RG == 2) {
+                    const bool odd = b & 1;
+                    const double e = (odd ? ok[tg][1] : ok[tg][0])
+                                         ? exp_acc(odd ? p[tg][1] - m_new[1] : p[tg][0] - m_new[0])
+                                         : 0.0;
+                    const double other = dpp<ror_ctrl<4>()>(e);
+                    p[tg][0] = odd ? other : e;
+                    p[tg][1] = odd ? e : other;
+                } else {
+#pragma unroll
+                    for (int rg = 0; rg < RG; ++rg)
+                        p[tg][rg] = ok[tg][rg] ? exp_acc(p[tg][rg] - m_new[rg]) : 0.0;
+                }
+            }
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
                 double lb = 0.0;
 #pragma unroll
-                for (int tg = 0; tg < TG; ++tg) {
-                    const double pw = ok[tg] ? exp_acc(p[tg][rg] - m_new) : 0.0;
-                    p[tg][rg] = pw;
-                    lb += pw;
-                }
+                for (int tg = 0; tg < TG; ++tg) lb += p[tg][rg];
                 lb = allreduce_hi<16>(lb, OpSum());
-                const bool moved = m_new != m[rg];
+                const bool moved = m_new[rg] != m[rg];
                 double f = 1.0;
-                if (moved) f = exp_acc(m[rg] - m_new);  // m = -inf gives 0
+                if (moved) f = exp_acc(m[rg] - m_new[rg]);  // m = -inf gives 0
                 scl[rg] = f;
                 l[rg] = l[rg] * f + lb;
-                m[rg] = m_new;
+                m[rg] = m_new[rg];
                 moved_any = moved_any || moved;
             }
             if (__any(moved_any)) {
