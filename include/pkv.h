@@ -351,8 +351,8 @@ size_t pkv_q4_matmul_workspace_size(int32_t c_in, int32_t c_out, int32_t batch);
  * c_in = num_heads * head_dim), out fp32 [batch][c_out]. W is in the reference's Q4_0
  * block-32 form (moe_kernels.mojo:7-57): w_packed uint8 [c_out][c_in / 2] (byte j of a
  * block: element 2j in the low nibble, 2j + 1 in the high one; value nibble - 8) and
- * scales fp32 [c_out][c_in / 32]. c_in % 32 == 0, batch <= 64; w_packed and scales 4-byte,
- * x 16-byte aligned. Products are exact (bf16 matrix cores on a three-way split of x) and
+ * scales fp32 [c_out][c_in / 32]. c_in % 32 == 0, batch <= 64; w_packed and x 16-byte,
+ * scales 4-byte aligned (the weights are read in 16-byte chunks). Products are exact (bf16 matrix cores on a three-way split of x) and
  * sums are fp32. One or two launches. */
 int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales, const float* x,
                       int32_t c_in, int32_t c_out, int32_t batch, float* out, void* workspace,

@@ -317,9 +317,9 @@ int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales
     if (batch > kQ4MaxBatch) return fail(PKV_ERR_UNSUPPORTED, "pkv_q4_matmul: batch must be <= 64");
     if (!w_packed || !scales || !x || !out || !workspace)
         return fail(PKV_ERR_INVALID, "pkv_q4_matmul: null device pointer");
-    if ((reinterpret_cast<uintptr_t>(w_packed) & 3) || (reinterpret_cast<uintptr_t>(x) & 15) ||
+    if ((reinterpret_cast<uintptr_t>(w_packed) & 15) || (reinterpret_cast<uintptr_t>(x) & 15) ||
         (reinterpret_cast<uintptr_t>(scales) & 3))
-        return fail(PKV_ERR_INVALID, "pkv_q4_matmul: w_packed / scales need 4-byte, x 16-byte alignment");
+        return fail(PKV_ERR_INVALID, "pkv_q4_matmul: w_packed and x need 16-byte, scales 4-byte alignment");
     if (workspace_bytes < pkv_q4_matmul_workspace_size(c_in, c_out, batch))
         return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_q4_matmul_workspace_size()");
     Q4Args a{};

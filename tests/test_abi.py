@@ -117,10 +117,11 @@ def test_ring_mode_rejections():
 
 def test_q4_matmul_rejections_before_launch():
     L = lib.load()
-    assert L.pkv_q4_matmul(None, 4, 4, 16, 100, 8, 1, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID
-    assert L.pkv_q4_matmul(None, 4, 4, 16, 128, 8, 65, 16, 16, 1 << 20) == lib.PKV_ERR_UNSUPPORTED
-    assert L.pkv_q4_matmul(None, 4, 4, 16, 4096, 8, 8, 16, 16, 16) == lib.PKV_ERR_WORKSPACE
-    assert L.pkv_q4_matmul(None, 4, 4, 8, 4096, 8, 8, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID  # x alignment
+    assert L.pkv_q4_matmul(None, 16, 4, 16, 100, 8, 1, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID
+    assert L.pkv_q4_matmul(None, 16, 4, 16, 128, 8, 65, 16, 16, 1 << 20) == lib.PKV_ERR_UNSUPPORTED
+    assert L.pkv_q4_matmul(None, 16, 4, 16, 4096, 8, 8, 16, 16, 16) == lib.PKV_ERR_WORKSPACE
+    assert L.pkv_q4_matmul(None, 16, 4, 8, 4096, 8, 8, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID  # x alignment
+    assert L.pkv_q4_matmul(None, 4, 4, 16, 4096, 8, 8, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID  # w alignment
     assert L.pkv_q4_matmul_workspace_size(4096, 2816, 32) == 16 * 32 * 2816 * 4
 
 
