@@ -345,7 +345,8 @@ def q4_matmul(w_packed, scales, x, out, c_in: int, c_out: int, batch: int, works
               stream: hip.Stream | None = None):
     """Wo projection (q4_matmul_vec, moe_kernels.mojo:59-163) for `batch` vectors: out
     [batch][c_out] = x [batch][c_in] times the Q4_0 matrix (w_packed [c_out][c_in/2] uint8,
-    scales [c_out][c_in/32] fp32); all device arrays. Returns the workspace used."""
+    scales [c_out][c_in/32] fp32); all device arrays, w_packed and x 16-byte aligned (device
+    allocations are). Returns the workspace used."""
     L = lib.load()
     need = L.pkv_q4_matmul_workspace_size(c_in, c_out, batch)
     if need == 0:
