@@ -100,7 +100,12 @@ size_t pkv_workspace_size(const pkv_params* p, int32_t batch, int32_t q_len, int
  * sequence's rows is written and status[s] = PKV_SEQ_OUT_OF_BLOCKS.
  * pos[s] < 0 or n_s <= 0 skips sequence s. A token range outside [0, total_rows) or
  * longer than max_new (which sizes the grid) changes nothing for s and gives
- * PKV_SEQ_BAD_ARGS. tok_off: int32 [batch + 1] (device).
+ * PKV_SEQ_BAD_ARGS. A block the append touches whose table entry (held, or just popped
+ * from the free list) lies outside [0, num_blocks) gives PKV_SEQ_BAD_BLOCK: the rows of
+ * that block are skipped and the others written. A *free_count outside [0, num_blocks]
+ * pops nothing and gives PKV_SEQ_BAD_BLOCK to every sequence that needs a block; such a
+ * sequence writes only the rows of blocks it already holds. tok_off: int32 [batch + 1]
+ * (device).
  * status: int32 [batch] (device), written for every sequence. batch <= 4096.
  * Two launches on `stream`: the allocation (one workgroup) and the row scatter.
  * Ring pools (ring_size > 0): one launch, the scatter; token p of sequence s goes to
@@ -178,14 +183,18 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
  * (model_speculative_moe_batched.mojo:1996, :2625, :3111 write sites; :3090-3123 verify).
  * Block tables, table lengths, free list, status, every pool byte and out are those of the
  * two separate calls, with one exception: a sequence whose allocation fails
- * (PKV_SEQ_OUT_OF_BLOCKS) attends positions its append did not write, through table
- * entries past its length; if such an entry names another sequence's block, the fused
- * launch may read that row before or after this call's append writes it.
+ * (PKV_SEQ_OUT_OF_BLOCKS, or PKV_SEQ_BAD_BLOCK from a free count out of range) attends
+ * positions its append did not write, through table entries past its length; if such an
+ * entry names another sequence's block, the fused launch may read that row before or
+ * after this call's append writes it.
  * When one launch of the stream kernel's vector path covers the call (paged pools,
  * head_dim 256 or 512, G * q_len <= 8 on the vector kernel, every kv head in one
  * workgroup), that launch also copies the appended rows into the pool and reads them from
- * k_new / v_new, saving the scatter launch; otherwise the append runs whole first. Arguments as in pkv_append and pkv_attend; the attention's arguments are
- * checked before anything is launched. No reference counterpart as one call. */
+ * k_new / v_new, saving the scatter launch; otherwise the append runs whole first.
+ * Arguments as in pkv_append and pkv_attend. Every check of the attention's arguments
+ * (including an unsupported geometry) runs before the append launches anything, so a
+ * call that returns an error has changed no table, free list or pool. No reference
+ * counterpart as one call. */
 int32_t pkv_append_attend(void* stream, const pkv_params* p, void* k_pool, void* v_pool,
                           int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
                           int32_t* free_list, int32_t* free_count, const int32_t* pos,

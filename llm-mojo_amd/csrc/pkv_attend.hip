@@ -655,14 +655,24 @@ int32_t dispatch_rows(const AttendArgs& a, int rows, dim3 grid, hipStream_t st) 
     return PKV_OK;
 }
 
-// pos == NULL: one sequence at pos_scalar (whose ring, in ring mode, starts at row
-// ring_base; block_tables is then not read and may be NULL). q_lens != NULL: sequence s
-// has q_lens[s] <= q_len queries (stream path only).
-int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const void* k_pool,
-                    const void* v_pool, const int32_t* block_tables, int32_t table_stride,
-                    const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
-                    const int32_t* q_lens, int32_t batch, int32_t max_pos, float* out,
-                    void* workspace, size_t workspace_bytes, const NewRows* nr = nullptr) {
+// Rows per kv head the chunk kernel takes: 8, or 16 where a row's lanes number 16 or more
+// (head_dim 64 fp32, head_dim 256).
+bool chunk_rows_ok(const pkv_params* p, int rows) {
+    if (rows <= 8) return true;
+    if (rows > 16) return false;
+    const int ve = p->kv_dtype == PKV_DTYPE_BF16 ? 8 : 4;
+    const int vpr = p->head_dim / ve;
+    const int lpr = vpr < kWave ? vpr : kWave;
+    return p->head_dim <= 256 && lpr >= 16;
+}
+
+// Every check pkv_attend / pkv_verify make, and the kernel they take: *use_stream for the
+// stream kernel, else the chunk kernel with layout *lay. Launches nothing.
+int32_t attend_check(const pkv_params* p, const float* q, const void* k_pool,
+                     const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                     const int32_t* pos, int32_t q_len, const int32_t* q_lens, int32_t batch,
+                     int32_t max_pos, const float* out, const void* workspace,
+                     size_t workspace_bytes, bool* use_stream, AttendLayout* lay) {
     int32_t rc = validate_params(p);
     if (rc != PKV_OK) return rc;
     if (batch <= 0 || q_len <= 0 || table_stride <= 0 || max_pos < 0)
@@ -673,29 +683,54 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     const int G = p->num_heads / p->num_kv_heads;
     const int rows = G * q_len;
     if (batch > 4096) return fail(PKV_ERR_INVALID, "batch must be <= 4096");
-    hipStream_t st = static_cast<hipStream_t>(stream);
     if (stream_eligible(p, G) && workspace_bytes >= stream_layout(p, batch, q_len).total) {
-        rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
-                           ring_base, q_len, q_lens, batch, max_pos, nullptr, nullptr, 0, out,
-                           workspace, st, nr);
-        if (rc != PKV_OK) return rc;
-        return check_launch("pkv_attend");
+        *use_stream = true;
+        return PKV_OK;
     }
+    *use_stream = false;
     if (q_lens) {
         if (!stream_eligible(p, G))
             return fail(PKV_ERR_UNSUPPORTED, "per-sequence query counts need head_dim 256 or 512 "
                                              "and num_heads / num_kv_heads <= 8");
         return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_workspace_size()");
     }
-    if (rows > 16)
+    if (!chunk_rows_ok(p, rows))
         return fail(PKV_ERR_UNSUPPORTED, "this geometry allows at most 16 query rows "
-                                         "(q_len * num_heads / num_kv_heads) per kv head");
-    AttendLayout lay = attend_layout(p, batch, q_len, max_pos);
-    if (lay.chunk > kMaxChunk) return fail(PKV_ERR_UNSUPPORTED, "chunk larger than the kernel's LDS bound");
-    if (workspace_bytes < lay.total)
+                                         "(q_len * num_heads / num_kv_heads) per kv head, 8 at "
+                                         "head_dim 512 or bf16 head_dim 64");
+    *lay = attend_layout(p, batch, q_len, max_pos);
+    if (lay->chunk > kMaxChunk) return fail(PKV_ERR_UNSUPPORTED, "chunk larger than the kernel's LDS bound");
+    if (workspace_bytes < lay->total)
         return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_workspace_size()");
     if (batch > 65535 || p->num_kv_heads > 65535)
         return fail(PKV_ERR_INVALID, "batch and num_kv_heads must be <= 65535");
+    return PKV_OK;
+}
+
+// pos == NULL: one sequence at pos_scalar (whose ring, in ring mode, starts at row
+// ring_base; block_tables is then not read and may be NULL). q_lens != NULL: sequence s
+// has q_lens[s] <= q_len queries (stream path only).
+int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const void* k_pool,
+                    const void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                    const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
+                    const int32_t* q_lens, int32_t batch, int32_t max_pos, float* out,
+                    void* workspace, size_t workspace_bytes, const NewRows* nr = nullptr) {
+    bool use_stream = false;
+    AttendLayout lay{};
+    int32_t rc = attend_check(p, q, k_pool, v_pool, block_tables, table_stride, pos, q_len,
+                              q_lens, batch, max_pos, out, workspace, workspace_bytes,
+                              &use_stream, &lay);
+    if (rc != PKV_OK) return rc;
+    const int G = p->num_heads / p->num_kv_heads;
+    const int rows = G * q_len;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (use_stream) {
+        rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
+                           ring_base, q_len, q_lens, batch, max_pos, nullptr, nullptr, 0, out,
+                           workspace, st, nr);
+        if (rc != PKV_OK) return rc;
+        return check_launch("pkv_attend");
+    }
     AttendArgs a{};
     char* ws = static_cast<char*>(workspace);
     a.q = q;
@@ -856,10 +891,14 @@ int32_t pkv_append_attend(void* stream, const pkv_params* p, void* k_pool, void*
     clear_error();
     int32_t rc = validate_params(p);
     if (rc != PKV_OK) return rc;
-    // The attention's arguments are checked before anything is launched.
-    if (!q || !out || !workspace || !pos) return fail(PKV_ERR_INVALID, "null device pointer");
-    if (q_len <= 0 || max_pos < 0 || batch <= 0 || batch > 4096)
-        return fail(PKV_ERR_INVALID, "q_len must be positive, max_pos >= 0, 0 < batch <= 4096");
+    // Every check of the attention runs before the append launches anything, so a call
+    // that returns an error has changed no table, free list or pool.
+    if (!pos) return fail(PKV_ERR_INVALID, "null device pointer");
+    bool use_stream = false;
+    AttendLayout lay{};
+    rc = attend_check(p, q, k_pool, v_pool, block_tables, table_stride, pos, q_len, nullptr,
+                      batch, max_pos, out, workspace, workspace_bytes, &use_stream, &lay);
+    if (rc != PKV_OK) return rc;
     if (workspace_bytes < pkv_workspace_size(p, batch, q_len, max_pos))
         return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_workspace_size()");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -872,7 +911,7 @@ int32_t pkv_append_attend(void* stream, const pkv_params* p, void* k_pool, void*
                        !fuse);
     if (rc != PKV_OK) return rc;
     NewRows nr{static_cast<const char*>(k_new), static_cast<const char*>(v_new), tok_off,
-               static_cast<char*>(k_pool), static_cast<char*>(v_pool), status};
+               static_cast<char*>(k_pool), static_cast<char*>(v_pool), status, table_lens};
     return attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0, 0, q_len,
                        nullptr, batch, max_pos, out, workspace, workspace_bytes,
                        fuse ? &nr : nullptr);

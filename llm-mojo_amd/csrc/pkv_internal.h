@@ -42,14 +42,17 @@ AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, in
 //   plan   int32 [batch + 2]       per, then the key prefix of every sequence
 //   part_ml                        double (m, l) per (slot, row)
 //   part_o                         double [head_dim] per (slot, row)
-// slots = kMaxSlots + batch, rows = num_heads * q_len.
+// slots = min(nwg_cap, kStreamMaxSlots) + batch, rows = num_heads * q_len: piece (w, s) of
+// workgroup w < nwg <= nwg_cap and sequence s uses slot w + s.
+constexpr int kStreamMaxSlots = 1024;  // workgroups along the keys, at most
 struct StreamLayout {
     size_t plan_off;
     size_t ml_off;
     size_t o_off;
     size_t total;
 };
-StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len);
+StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len,
+                           int32_t nwg_cap = kStreamMaxSlots);
 // True when the stream kernel covers this geometry: head_dim 256 or 512 with
 // G = num_heads / num_kv_heads <= 8 (any number of queries: launched in groups).
 bool stream_eligible(const pkv_params* p, int32_t G);
@@ -60,10 +63,11 @@ bool stream_eligible(const pkv_params* p, int32_t G);
 struct NewRows {
     const char* k_new;
     const char* v_new;
-    const int32_t* tok_off;  // [batch + 1]
-    char* k_dst;             // the pools, written
+    const int32_t* tok_off;     // [batch + 1]
+    char* k_dst;                // the pools, written
     char* v_dst;
-    int32_t* status;         // per sequence, from the block allocation
+    const int32_t* status;      // per sequence, from the block allocation (read only)
+    const int32_t* table_lens;  // after the allocation (read only)
 };
 // True when stream_attend takes the appended rows itself for q_len queries: paged pools
 // and one launch on the vector kernel.
@@ -87,7 +91,8 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
                       const int32_t* q_lens, int32_t batch, int32_t max_pos, const int32_t* keys,
                       const int32_t* key_off, int32_t max_keys, float* out, void* workspace,
-                      hipStream_t st, const NewRows* nr = nullptr);
+                      hipStream_t st, const NewRows* nr = nullptr,
+                      int32_t nwg_cap = kStreamMaxSlots);
 
 __host__ __device__ inline int32_t window_start(int32_t pos, int32_t window) {
     if (window <= 0) return 0;

@@ -130,10 +130,15 @@ __device__ inline int append_need(const AppendArgs& a, int s, int len) {
 // One workgroup. Sequence s (index order) takes the free-list entries
 // free_list[fc - 1 - pref[s] - j], j < granted[s]: the LIFO pops of a serial pass.
 // A sequence that runs the list dry keeps what it popped (status OUT_OF_BLOCKS).
+// This kernel writes every sequence's final status: a block the append touches whose
+// table entry (held, or just popped) lies outside the pool gives BAD_BLOCK, as does a
+// free count outside [0, num_blocks] for a sequence that needs blocks. The row copies
+// after it only read status, so no two workgroups of a launch share a status word.
 __global__ __launch_bounds__(kNT) void alloc_kernel(AppendArgs a) {
     __shared__ int s_tmp[kNT];
     __shared__ int s_len[kMaxBatch];
     __shared__ int s_need[kMaxBatch];
+    __shared__ int s_code[kMaxBatch];
     __shared__ int s_pref[kMaxBatch + 1];
     const int tid = threadIdx.x;
     int fc = *a.free_count;
@@ -144,7 +149,7 @@ __global__ __launch_bounds__(kNT) void alloc_kernel(AppendArgs a) {
         const int need = append_need(a, s, len);
         s_len[s] = len;
         s_need[s] = need > 0 ? need : 0;
-        a.status[s] = need < 0 ? need : PKV_SEQ_OK;
+        s_code[s] = need < 0 ? need : PKV_SEQ_OK;
     }
     __syncthreads();
     const int total = lds_prefix(s_need, s_pref, a.batch, s_tmp);
@@ -157,13 +162,38 @@ __global__ __launch_bounds__(kNT) void alloc_kernel(AppendArgs a) {
     }
     for (int s = tid; s < a.batch; s += kNT) {
         const int need = s_need[s];
-        if (need == 0) continue;
+        int code = s_code[s];
         const int avail = fc - s_pref[s];
-        const int granted = avail <= 0 ? 0 : (avail < need ? avail : need);
+        const int granted = need == 0 || avail <= 0 ? 0 : (avail < need ? avail : need);
         if (granted > 0) a.table_lens[s] = s_len[s] + granted;
-        if (granted < need) a.status[s] = fc_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_OUT_OF_BLOCKS;
+        if (granted < need) code = fc_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_OUT_OF_BLOCKS;
+        const int p = a.pos[s];
+        const int n = a.tok_off[s + 1] - a.tok_off[s];
+        if (code == PKV_SEQ_OK && p >= 0 && n > 0) {
+            // Every block the rows land in: held entries from the table, new ones from the
+            // free list (the entries the loop above writes, read at their source).
+            const int32_t* table = a.tables + (size_t)s * a.table_stride;
+            const int len = s_len[s];
+            const int b1 = (int)(((long long)p + n - 1) / a.bs);
+            for (int blk = p / a.bs; blk <= b1; ++blk) {
+                const int e = blk < len ? table[blk] : a.free_list[fc - 1 - s_pref[s] - (blk - len)];
+                if (e < 0 || e >= a.num_blocks) {
+                    code = PKV_SEQ_BAD_BLOCK;
+                    break;
+                }
+            }
+        }
+        a.status[s] = code;
     }
     if (tid == 0 && !fc_bad) *a.free_count = fc - popped;
+}
+
+// Paged pools: whether the rows of sequence s with status `st` (from alloc_kernel) are
+// copied -- OK, or BAD_BLOCK where each row is then written only if its block is held
+// (index < table_lens[s], a length within [0, table_stride]) and its entry lies in the
+// pool.
+__device__ inline bool paged_rows_written(int st) {
+    return st == PKV_SEQ_OK || st == PKV_SEQ_BAD_BLOCK;
 }
 
 // grid = (ceil(max_new / tok_per_wg), batch). Copies this workgroup's tokens of one
@@ -180,7 +210,7 @@ __global__ __launch_bounds__(kNT) void scatter_kernel(AppendArgs a) {
         const int st = ring_append_status(a, s);
         if (blockIdx.x == 0 && tid == 0) a.status[s] = st;
         if (st != PKV_SEQ_OK) return;
-    } else if (a.status[s] != PKV_SEQ_OK) {
+    } else if (!paged_rows_written(a.status[s])) {
         return;
     }
     const int p0 = a.pos[s];
@@ -192,17 +222,17 @@ __global__ __launch_bounds__(kNT) void scatter_kernel(AppendArgs a) {
     const int tok_end = min(n, (int)blockIdx.x * a.tok_per_wg + a.tok_per_wg);
     const int vec_per_row = a.row_bytes / 16;
     const int32_t* table = a.tables + (size_t)s * a.table_stride;
+    const int held = ring ? 0 : a.table_lens[s];
+    if (!ring && held > a.table_stride) return;  // a length outside the table: BAD_BLOCK
     for (int b = tok_begin; b < tok_end; ++b) {
         const int p = p0 + b;
         size_t row;
         if (ring) {
             row = (size_t)table[0] * a.ring_size + (size_t)(p % a.ring_size);
         } else {
-            const int phys = table[p / a.bs];
-            if (phys < 0 || phys >= a.num_blocks) {
-                if (tid == 0) a.status[s] = PKV_SEQ_BAD_BLOCK;
-                continue;
-            }
+            const int blk = p / a.bs;
+            const int phys = blk < held ? table[blk] : -1;
+            if (phys < 0 || phys >= a.num_blocks) continue;  // reported by alloc_kernel
             row = (size_t)phys * a.bs + (size_t)(p % a.bs);
         }
         const uint4* ks = reinterpret_cast<const uint4*>(a.k_new + ((size_t)row0 + b) * a.row_bytes);
@@ -401,14 +431,17 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
     // ring_size tokens of the call (earlier ones would be overwritten within it).
     if (tid == 0) {
         long long prow = -1;
-        if (st == PKV_SEQ_OK && !(ring && b < n - ap.ring_size)) {
+        const bool write = ring ? st == PKV_SEQ_OK && b >= n - ap.ring_size : paged_rows_written(st);
+        if (write) {
             const int32_t* table = ap.tables + (size_t)s * ap.table_stride;
             if (ring) {
                 prow = (long long)table[0] * ap.ring_size + p % ap.ring_size;
             } else {
-                const int phys = table[p / ap.bs];
-                if (phys < 0 || phys >= ap.num_blocks) ap.status[s] = PKV_SEQ_BAD_BLOCK;
-                else prow = (long long)phys * ap.bs + p % ap.bs;
+                // a block outside the pool or not held skips the row (alloc_kernel reported it)
+                const int blk = p / ap.bs;
+                const int held = ap.table_lens[s];
+                const int phys = blk < held && held <= ap.table_stride ? table[blk] : -1;
+                if (phys >= 0 && phys < ap.num_blocks) prow = (long long)phys * ap.bs + p % ap.bs;
             }
         }
         s_prow = prow;

@@ -341,6 +341,7 @@ struct StreamArgs {
     int32_t max_pos;   // last query position the caller sized for
     int32_t batch;
     int32_t nwg;       // P: workgroups along the keys
+    int32_t nwg_cap;   // at most this many (the workspace holds nwg_cap + batch slots)
     int32_t rows_seq;  // Hq * q_cnt: workspace rows per sequence
     int32_t* plan;     // [0] = per, [1 + s] = key prefix of sequence s (s <= batch)
     void* part_ml;     // Acc (m, l) per (slot, row)
@@ -462,52 +463,46 @@ __device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo) {
 
 // Fused append: the appended rows (NewRows) of sequences w, w + nwg, ... go into the pool
 // from workgroup w, the first wave of each kv head copying that head's slice, with the
-// checks of scatter_kernel (pkv_state.hip): sequences whose allocation failed or at a
-// negative position are skipped, and a table entry outside the pool skips its row and
-// reports PKV_SEQ_BAD_BLOCK. The launch has one head group, so each sequence's status is
-// read and written by one workgroup only, reads first.
+// checks of scatter_kernel (pkv_state.hip): a sequence is copied when the block
+// allocation gave it OK or BAD_BLOCK, and a row whose block is not held or whose table
+// entry lies outside the pool is skipped. Status, table lengths and table entries are
+// final before this launch (the allocation is its own launch) and are only read here.
 template <int D, typename KV, int WPH>
 __device__ inline void copy_new_rows(const StreamArgs& a, int wave, int lane) {
     constexpr int kElt = SKV<KV>::kElt;
     constexpr int kVec = D * kElt / 16;  // 16-byte vectors per head slice
-    __shared__ int s_bad;
     const int g = wave / WPH;
-    const bool copier = wave % WPH == 0 && g < a.Hkv;
+    if (wave % WPH != 0 || g >= a.Hkv) return;
     const size_t row_bytes = (size_t)a.Hkv * D * kElt;
     const size_t head_off = (size_t)g * D * kElt;
     const int bs_mask = (1 << a.bs_shift) - 1;
     for (int s = blockIdx.y; s < a.batch; s += a.nwg) {
-        const bool ok = a.nr.status[s] == PKV_SEQ_OK;
-        if (threadIdx.x == 0) s_bad = 0;
-        __syncthreads();  // every read of status[s] before its write below
         const int p0 = a.pos[s];
         const int r0 = a.nr.tok_off[s];
         const int n = a.nr.tok_off[s + 1] - r0;
-        if (copier && ok && p0 >= 0 && n > 0) {
-            const int32_t* table = a.tables + (size_t)s * a.table_stride;
-            for (int b = 0; b < n; ++b) {
-                const int p = p0 + b;
-                const int phys = table[p >> a.bs_shift];
-                if (phys < 0 || phys >= a.num_blocks) {
-                    s_bad = 1;
-                    continue;
-                }
-                const size_t dst = (((size_t)phys << a.bs_shift) | (size_t)(p & bs_mask)) * row_bytes + head_off;
-                const size_t src = ((size_t)r0 + b) * row_bytes + head_off;
-                const uint4* ks = reinterpret_cast<const uint4*>(a.nr.k_new + src);
-                const uint4* vs = reinterpret_cast<const uint4*>(a.nr.v_new + src);
-                uint4* kd = reinterpret_cast<uint4*>(a.nr.k_dst + dst);
-                uint4* vd = reinterpret_cast<uint4*>(a.nr.v_dst + dst);
-                for (int i = lane; i < kVec; i += kSW) {
-                    const uint4 kv = ks[i];
-                    const uint4 vv = vs[i];
-                    kd[i] = kv;
-                    vd[i] = vv;
-                }
+        const int st = a.nr.status[s];
+        if ((st != PKV_SEQ_OK && st != PKV_SEQ_BAD_BLOCK) || p0 < 0 || n <= 0) continue;
+        const int32_t* table = a.tables + (size_t)s * a.table_stride;
+        const int held = a.nr.table_lens[s];
+        if (held > a.table_stride) continue;  // a length outside the table: BAD_BLOCK
+        for (int b = 0; b < n; ++b) {
+            const int p = p0 + b;
+            const int blk = p >> a.bs_shift;
+            const int phys = blk < held ? table[blk] : -1;
+            if (phys < 0 || phys >= a.num_blocks) continue;
+            const size_t dst = (((size_t)phys << a.bs_shift) | (size_t)(p & bs_mask)) * row_bytes + head_off;
+            const size_t src = ((size_t)r0 + b) * row_bytes + head_off;
+            const uint4* ks = reinterpret_cast<const uint4*>(a.nr.k_new + src);
+            const uint4* vs = reinterpret_cast<const uint4*>(a.nr.v_new + src);
+            uint4* kd = reinterpret_cast<uint4*>(a.nr.k_dst + dst);
+            uint4* vd = reinterpret_cast<uint4*>(a.nr.v_dst + dst);
+            for (int i = lane; i < kVec; i += kSW) {
+                const uint4 kv = ks[i];
+                const uint4 vv = vs[i];
+                kd[i] = kv;
+                vd[i] = vv;
             }
         }
-        __syncthreads();
-        if (threadIdx.x == 0 && s_bad) a.nr.status[s] = PKV_SEQ_BAD_BLOCK;
     }
 }
 
@@ -630,7 +625,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         if (ADDR == kAddrPaged && a.nr.k_new) {
             const int r0 = ufirst(a.nr.tok_off[s]);
             const int n = ufirst(a.nr.tok_off[s + 1]) - r0;
-            if (ufirst(a.nr.status[s]) == PKV_SEQ_OK && pos0 >= 0 && n > 0) {
+            const int st = ufirst(a.nr.status[s]);
+            if ((st == PKV_SEQ_OK || st == PKV_SEQ_BAD_BLOCK) && pos0 >= 0 && n > 0) {
                 pn_lo = pos0;
                 pn_hi = pos0 + n;
                 nr0 = r0;
@@ -1241,7 +1237,7 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
 
 // ---- host -------------------------------------------------------------------------
 
-constexpr int kMaxSlots = 1024;  // workgroups along the keys, at most (merge LDS bound)
+constexpr int kMaxSlots = kStreamMaxSlots;  // workgroups along the keys, at most (merge LDS bound)
 
 struct Occ {
     std::mutex mu;
@@ -1285,6 +1281,7 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     // covers ceil(total / nwg) keys.
     const int groups = (a.Hkv * WPH + kMaxWaves - 1) / kMaxWaves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
+    if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
     dim3 grid(groups, a.nwg);
     hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, ADDR>), grid, dim3(threads), lds, st,
                        a);
@@ -1312,6 +1309,7 @@ int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
     const int groups = (a.Hkv + kMaxWaves - 1) / kMaxWaves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
+    if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
     dim3 grid(groups, a.nwg);
     hipLaunchKernelGGL((stream_mfma_kernel<RG, TG, ADDR>), grid, dim3(threads), lds, st, a);
     hipLaunchKernelGGL((stream_merge_kernel<256, double>), dim3(a.rows_seq, a.batch),
@@ -1357,11 +1355,11 @@ int32_t launch_rows(StreamArgs a, int D, int rows, hipStream_t st) {
 
 }  // namespace
 
-StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len) {
+StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len, int32_t nwg_cap) {
     StreamLayout L{};
     auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t rows = (size_t)p->num_heads * q_len;
-    const size_t slots = (size_t)kMaxSlots + batch;
+    const size_t slots = (size_t)(nwg_cap < kMaxSlots ? nwg_cap : kMaxSlots) + batch;
     L.plan_off = 0;
     L.ml_off = align((size_t)(batch + 2) * sizeof(int32_t));
     L.o_off = L.ml_off + align(slots * rows * 2 * sizeof(double));
@@ -1392,10 +1390,11 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
                       const int32_t* pos, int32_t pos_scalar, int64_t ring_base, int32_t q_len,
                       const int32_t* q_lens, int32_t batch, int32_t max_pos, const int32_t* keys,
                       const int32_t* key_off, int32_t max_keys, float* out, void* workspace,
-                      hipStream_t st, const NewRows* nr) {
+                      hipStream_t st, const NewRows* nr, int32_t nwg_cap) {
     const int G = p->num_heads / p->num_kv_heads;
     if (!stream_eligible(p, G)) return fail(PKV_ERR_UNSUPPORTED, "stream path: geometry");
-    StreamLayout lay = stream_layout(p, batch, q_len);
+    if (nwg_cap < 1) return fail(PKV_ERR_WORKSPACE, "stream path: no room for one workgroup's partials");
+    StreamLayout lay = stream_layout(p, batch, q_len, nwg_cap);
     StreamArgs a{};
     char* ws = static_cast<char*>(workspace);
     a.q = q;
@@ -1421,6 +1420,7 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.ring_base = ring_base;
     a.max_pos = max_pos;
     a.batch = batch;
+    a.nwg_cap = nwg_cap < kMaxSlots ? nwg_cap : kMaxSlots;
     a.plan = reinterpret_cast<int32_t*>(ws + lay.plan_off);
     a.part_ml = ws + lay.ml_off;
     a.part_o = ws + lay.o_off;

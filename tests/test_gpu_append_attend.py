@@ -105,3 +105,36 @@ def test_append_attend_matches_append_then_attend(gpu, geom, kv_dtype, q_len):
         pos = np.where(pos >= 0, pos + q_len, pos).astype(np.int32)
     fused.free()
     sep.free()
+
+
+def test_append_attend_unsupported_geometry_changes_nothing(gpu):
+    """A geometry the attention has no kernel for (32 q heads over 2 kv heads with 2
+    queries: 32 rows per kv head) is refused before the append launches: tables, table
+    lengths, the free list and every pool byte are unchanged."""
+    print("[append_attend] unsupported geometry 32q/2kv q_len 2", flush=True)
+    rng = np.random.default_rng(5)
+    spec = LayerSpec(32, 2, 256, window=0)
+    B, nb, stride, q_len = 3, 16, 8, 2
+    c = PagedKVCache([spec], block_size=BS, num_blocks=nb, max_seqs=B, max_blocks_per_seq=stride,
+                     max_q_len=q_len, max_pos=stride * BS - 1, scale=0.0625)
+    kp = rng.standard_normal(c.k_pools[0].shape, dtype=np.float32)
+    vp = rng.standard_normal(c.v_pools[0].shape, dtype=np.float32)
+    c.k_pools[0].upload(kp)
+    c.v_pools[0].upload(vp)
+    before = c.snapshot()
+    pos = np.array([16, 5, 31], np.int32)  # 16 and 31 + 1 open new blocks
+    tok_off = (np.arange(B + 1) * q_len).astype(np.int32)
+    rows = B * q_len
+    dk = hip.DeviceArray.from_numpy(rng.standard_normal((rows, spec.kv_stride), dtype=np.float32))
+    dv = hip.DeviceArray.from_numpy(rng.standard_normal((rows, spec.kv_stride), dtype=np.float32))
+    dq = hip.DeviceArray.from_numpy(rng.standard_normal((B, q_len, 32, 256), dtype=np.float32))
+    out = hip.DeviceArray((B, q_len, 32, 256), np.float32)
+    with pytest.raises(lib.PkvError) as ei:
+        c.append_attend(0, pos, tok_off, dk, dv, q_len, rows, dq, q_len, out)
+    assert ei.value.code == lib.PKV_ERR_UNSUPPORTED
+    after = c.snapshot()
+    for key in ("tables", "table_lens", "free_list", "free_count"):
+        _same(np.asarray(after[key]), np.asarray(before[key]), key)
+    _same(c.k_pools[0].numpy(), kp, "K pool")
+    _same(c.v_pools[0].numpy(), vp, "V pool")
+    c.free()

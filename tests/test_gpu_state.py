@@ -133,3 +133,92 @@ def test_config1_append_into_new_block(gpu):
     assert st.table_lens[0] == 33 and st.tables[0, 32] == free[-1]
     _compare(cache, st)
     cache.free()
+
+
+@pytest.mark.parametrize("entry", ["append", "append_attend"])
+def test_bad_table_entry_skips_only_its_rows(gpu, entry):
+    """A 40-token append (ten scatter workgroups of 4 tokens at 8 KiB rows) over three
+    blocks, the middle one's table entry outside the pool: status BAD_BLOCK, the rows of
+    that block are skipped and every other row is written, whichever workgroup copies it.
+    The allocation and the other sequences follow the oracle bit-exactly. The oracle runs
+    the same call with a spare in-pool block in place of the bad entry; the device pools
+    must equal the oracle's everywhere except that spare block, which stays untouched.
+    append_attend: the fused launch copies the rows and attends (outputs against pkv_append
+    + pkv_attend)."""
+    print(f"[state] bad table entry, {entry}", flush=True)
+    rng = np.random.default_rng(11)
+    bs, nb, stride, nseq = 16, 14, 6, 3
+    spare = nb - 1  # in the pool, in no table and not on the free list
+    spec = LayerSpec(16, 8, 256)
+    kvs = spec.kv_stride
+    tables = np.zeros((nseq, stride), np.int32)
+    tables[0, :2] = [4, 9]
+    tables[1, :1] = [2]
+    tables[2, :2] = [7, 0]
+    lens = np.array([2, 1, 2], np.int32)
+    free = np.array([1, 3, 5, 6, 8, 10, 11, 12], np.int32)
+    dev_tables = tables.copy()
+    dev_tables[0, 1] = nb + 3  # outside the pool
+    tables[0, 1] = spare
+    pos = np.array([5, 3, 30], np.int32)
+    n_new = np.array([40, 6, 5], np.int32)  # blocks 0-2 of seq 0, block 0 of 1, 1-2 of 2
+    off = O.ragged_tok_off(n_new)
+    rows = int(off[-1])
+    k = rng.standard_normal((rows, kvs), dtype=np.float32)
+    v = rng.standard_normal((rows, kvs), dtype=np.float32)
+    kp = rng.standard_normal(nb * bs * kvs, dtype=np.float32)
+    vp = rng.standard_normal(nb * bs * kvs, dtype=np.float32)
+
+    def device_cache():
+        c = PagedKVCache([spec], block_size=bs, num_blocks=nb, max_seqs=nseq,
+                         max_blocks_per_seq=stride, max_pos=stride * bs - 1, scale=0.0625)
+        c.tables.upload(dev_tables)
+        c.table_lens.upload(lens)
+        fl = np.zeros(nb, np.int32)
+        fl[:free.size] = free
+        c.free_list.upload(fl)
+        c.free_count.upload(np.array([free.size], np.int32))
+        c.k_pools[0].upload(kp.reshape(c.k_pools[0].shape))
+        c.v_pools[0].upload(vp.reshape(c.v_pools[0].shape))
+        return c
+
+    st = O.CacheState(1, kvs, bs, nb, nseq, stride, alloc_pools=False)
+    st.k_pools[0], st.v_pools[0] = kp.copy(), vp.copy()
+    st.tables[:] = tables
+    st.table_lens[:] = lens
+    st.bm.free_list[:free.size] = free
+    st.bm.count[0] = free.size
+    ref = st.append(0, pos, off, k, v, int(n_new.max()))
+    dk, dv = hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(v)
+    a = device_cache()
+    got = a.append(0, pos, off, dk, dv, int(n_new.max()), rows).numpy()
+    q = rng.standard_normal((nseq, 1, 16, 256), dtype=np.float32)
+    dq = hip.DeviceArray.from_numpy(q)
+    if entry == "append_attend":
+        out_ref = hip.DeviceArray((nseq, 1, 16, 256), np.float32)
+        a.attend(0, dq, pos, 1, out_ref)
+        out = hip.DeviceArray((nseq, 1, 16, 256), np.float32)
+        b = device_cache()
+        got_b = b.append_attend(0, pos, off, dk, dv, int(n_new.max()), rows, dq, 1, out).numpy()
+        np.testing.assert_array_equal(got_b, got)
+        np.testing.assert_array_equal(out.numpy(), out_ref.numpy())  # block 0 only: no NaN
+        a.free()
+        a = b
+    assert list(got) == [lib.PKV_SEQ_BAD_BLOCK, lib.PKV_SEQ_OK, lib.PKV_SEQ_OK]
+    assert list(ref) == [0, 0, 0]
+    snap = a.snapshot()
+    exp_tables = st.tables.copy()
+    exp_tables[0, 1] = nb + 3
+    np.testing.assert_array_equal(snap["tables"], exp_tables)
+    np.testing.assert_array_equal(snap["table_lens"], st.table_lens)
+    np.testing.assert_array_equal(snap["free_list"], st.free_list)
+    row_elems = bs * kvs
+    for name, dev, exp, init in (("K", a.k_pools[0], st.k_pools[0], kp),
+                                 ("V", a.v_pools[0], st.v_pools[0], vp)):
+        g = dev.numpy().reshape(-1)
+        sl = slice(spare * row_elems, (spare + 1) * row_elems)
+        np.testing.assert_array_equal(g[sl], init[sl], err_msg=f"{name}: the bad block's rows")
+        e = exp.copy()
+        e[sl] = init[sl]
+        np.testing.assert_array_equal(g, e, err_msg=f"{name} pool")
+    a.free()
