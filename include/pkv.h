@@ -203,6 +203,26 @@ int32_t pkv_append_attend(void* stream, const pkv_params* p, void* k_pool, void*
                           int32_t q_len, int32_t batch, int32_t max_pos, float* out,
                           void* workspace, size_t workspace_bytes);
 
+/* Bytes of the device scratch pkv_attend_noalloc uses on each GPU (held from its first
+ * call on that GPU until the process ends). */
+#define PKV_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* pkv_attend without a workspace argument. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. Same arguments, results and
+ * contract as pkv_attend (decode, verify with q_len queries, MTP reads, ring pools),
+ * for head_dim 256 or 512 with num_heads / num_kv_heads <= 8; other geometries give
+ * PKV_ERR_UNSUPPORTED. The split-K partials live in a library-owned device array of
+ * PKV_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, whose address is looked up on the first
+ * call on each device; the call allocates nothing. A call whose partials cannot fit
+ * (batch + 1 slots of num_heads * q_len rows of (head_dim + 2) doubles) gives
+ * PKV_ERR_WORKSPACE. Every call on one GPU shares that array: calls that overlap on a
+ * GPU (other streams, other host threads) race, so order them on one stream. */
+int32_t pkv_attend_noalloc(void* stream, const pkv_params* p, const float* q,
+                           const void* k_pool, const void* v_pool, const int32_t* block_tables,
+                           int32_t table_stride, const int32_t* pos, int32_t q_len,
+                           int32_t batch, int32_t max_pos, float* out);
+
 /* K2'' -- verify attention with a query count per sequence. The engine verifies each
  * sequence's own draft: verify_b = drafts + 1 tokens (model_speculative_moe_batched.mojo
  * :3005), fewer when drafting stopped early at a terminal token (:2990-2993), so counts

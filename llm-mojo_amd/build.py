@@ -33,7 +33,7 @@ HIP_FLAGS = [
     f"-I{os.path.join(REPO, 'include')}",
 ]
 SOURCES = ["pkv_common.cpp", "pkv_state.hip", "pkv_attend.hip", "pkv_stream.hip",
-           "pkv_prefill.hip", "pkv_q4.hip", "pkv_lsa.hip"]
+           "pkv_prefill.hip", "pkv_q4.hip", "pkv_lsa.hip", "pkv_noalloc.hip"]
 
 
 def _run(cmd: list[str]) -> None:

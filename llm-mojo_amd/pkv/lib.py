@@ -52,6 +52,8 @@ PROTOTYPES = {
                           _vp, _i32, _i32, _vp]),
     "pkv_attend": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp,
                           _sz]),
+    "pkv_attend_noalloc": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32,
+                                  _vp]),
     "pkv_decode": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _sz]),
     "pkv_rollback": (_i32, [_vp, _PP, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp]),
     "pkv_prefill": (_i32, [_vp, _PP, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),

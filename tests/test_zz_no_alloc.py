@@ -1,0 +1,105 @@
+"""pkv_attend_noalloc (no workspace argument; partials in the library's 64 MiB device
+scratch) against pkv_attend with a caller workspace, through the C ABI: the same kernels
+on the same inputs give bit-identical outputs. Two calls in a row, the second with a
+smaller batch and shorter contexts (the scratch keeps the first call's contents, which
+must not leak into the second), then a 4-query verify on the fp64 MFMA kernel, and
+parity of the no-allocation outputs against the oracle. A call whose partials cannot fit
+the scratch is refused with PKV_ERR_WORKSPACE before anything is launched."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pkv import F32, LayerSpec, PagedKVCache, hip, lib
+from pkv.engine import make_params
+from tests import parity
+
+pytestmark = pytest.mark.gpu
+
+BS = 16
+
+
+def _noalloc(cache, q, pos, q_len, out, batch, max_pos):
+    p = cache.params[0]
+    lib.call("pkv_attend_noalloc", None, ctypes.byref(p), q.ptr, cache.k_pools[0].ptr,
+             cache.v_pools[0].ptr, cache.tables.ptr, cache.table_stride,
+             cache._ints(pos, cache._i32_a, batch), q_len, batch, max_pos, out.ptr)
+
+
+def _setup(rng, B, ctx, max_q_len):
+    spec = LayerSpec(16, 8, 256, window=0, kv_dtype=F32)
+    stride = int((ctx.max() + max_q_len + BS - 1) // BS) + 1
+    lens = ((ctx + max_q_len + BS - 1) // BS).astype(np.int32)
+    nb = int(lens.sum()) + 4
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((B, stride), np.int32)
+    o = 0
+    for s in range(B):
+        tables[s, :lens[s]] = perm[o:o + lens[s]]
+        o += lens[s]
+    cache = PagedKVCache([spec], block_size=BS, num_blocks=nb, max_seqs=B,
+                         max_blocks_per_seq=stride, max_q_len=max_q_len,
+                         max_pos=stride * BS - 1, scale=0.0625)
+    cache.tables.upload(tables)
+    cache.table_lens.upload(lens)
+    kp = rng.standard_normal(cache.k_pools[0].shape, dtype=np.float32)
+    vp = rng.standard_normal(cache.v_pools[0].shape, dtype=np.float32)
+    cache.k_pools[0].upload(kp)
+    cache.v_pools[0].upload(vp)
+    return cache, tables, lens, kp.reshape(-1), vp.reshape(-1)
+
+
+def _pair(cache, q, pos, q_len, batch, what):
+    print(f"[no_alloc] {what}: batch {batch}, q_len {q_len}", flush=True)
+    dq = hip.DeviceArray.from_numpy(q)
+    shape = (batch, q_len, 16, 256)
+    out_ws = hip.DeviceArray(shape, np.float32)
+    out_na = hip.DeviceArray(shape, np.float32)
+    max_pos = int(pos.max()) + q_len - 1
+    cache.attend(0, dq, pos, q_len, out_ws, batch=batch, max_pos=max_pos)
+    _noalloc(cache, dq, pos, q_len, out_na, batch, max_pos)
+    a, b = out_ws.numpy(), out_na.numpy()
+    assert np.array_equal(a, b), f"{what}: outputs differ from pkv_attend's"
+    return b
+
+
+def test_noalloc_matches_attend_twice_then_verify(gpu):
+    rng = np.random.default_rng(77)
+    B = 32
+    ctx = rng.integers(100, 3000, B).astype(np.int32)
+    cache, tables, lens, kp, vp = _setup(rng, B, ctx, 4)
+    # call 1: 32 decode queries
+    q1 = rng.standard_normal((B, 1, 16, 256), dtype=np.float32)
+    got1 = _pair(cache, q1, ctx, 1, B, "call 1")
+    ref = O.attend(q1, kp, vp, tables, lens, ctx, 1, 16, 8, 256, BS, 0, scale=0.0625,
+                   nthreads=O.max_threads(), par=1)
+    exact = O.attend_f64(q1, kp, vp, tables, ctx, 1, 16, 8, 256, BS, 0, scale=0.0625)
+    parity.check(got1, ref, exact, what="no-alloc call 1")
+    # call 2: a smaller input -- 5 sequences, shorter contexts
+    pos2 = (ctx[:5] // 3).astype(np.int32)
+    q2 = rng.standard_normal((5, 1, 16, 256), dtype=np.float32)
+    got2 = _pair(cache, q2, pos2, 1, 5, "call 2")
+    ref = O.attend(q2, kp, vp, tables[:5], lens[:5], pos2, 1, 16, 8, 256, BS, 0, scale=0.0625)
+    exact = O.attend_f64(q2, kp, vp, tables[:5], pos2, 1, 16, 8, 256, BS, 0, scale=0.0625)
+    parity.check(got2, ref, exact, what="no-alloc call 2")
+    # call 3: a 4-query verify (8 rows per kv head: the fp64 MFMA kernel)
+    q3 = rng.standard_normal((16, 4, 16, 256), dtype=np.float32)
+    got3 = _pair(cache, q3, ctx[:16], 4, 16, "call 3 (verify)")
+    ref = O.attend(q3, kp, vp, tables[:16], lens[:16], ctx[:16], 4, 16, 8, 256, BS, 0,
+                   scale=0.0625, nthreads=O.max_threads(), par=1)
+    exact = O.attend_f64(q3, kp, vp, tables[:16], ctx[:16], 4, 16, 8, 256, BS, 0, scale=0.0625)
+    parity.check(got3, ref, exact, what="no-alloc call 3")
+    cache.free()
+
+
+def test_noalloc_refuses_partials_beyond_the_scratch(gpu):
+    # 16 q heads at head_dim 512 with 16 queries: 256 rows of 514 doubles per slot, ~1 MiB,
+    # so 64 sequences need more than the 64 MiB scratch holds.
+    print("[no_alloc] oversized call is refused", flush=True)
+    p = make_params(LayerSpec(16, 2, 512), BS, 64)
+    buf = hip.DeviceArray((1024,), np.uint8, zero=True)
+    rc = lib.load().pkv_attend_noalloc(None, ctypes.byref(p), buf.ptr, buf.ptr, buf.ptr,
+                                       buf.ptr, 4, buf.ptr, 16, 64, 63, buf.ptr)
+    assert rc == lib.PKV_ERR_WORKSPACE, rc
+    buf.free()
