@@ -179,11 +179,44 @@ def run_gpu(sched, data, steps, warmup, log):
                 outs=first_outs, status=status)
 
 
-def run_cpu(sched, data, seconds, nthreads, log):
-    """Reference CPU path (oracle) on the first steps of the same schedule: the engine's
-    append and paged_attention_layer per sequence, head-pair tasks on `nthreads` threads
-    (attention.mojo:276-287), sequences one after another (…batched.mojo:2951)."""
+def host_cpu_info():
+    """The GPU box host's CPU as the baseline record states it: model name, logical CPUs
+    (os.cpu_count / nproc), physical cores (distinct (socket, core) pairs of
+    /proc/cpuinfo, as lscpu counts them) and the OpenMP thread share of this job."""
+    model, cores = None, set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return {"model": model, "logical_cpus": os.cpu_count(),
+            "physical_cores": len(cores) or None,
+            "omp_num_threads": int(omp) if omp and omp.isdigit() else None}
+
+
+def run_cpu(sched, data, seconds, nthreads, log, par=0):
+    """Reference CPU path (oracle) on the steps of the same schedule, up to `seconds` of
+    work: the engine's append and paged_attention_layer per sequence. par 0 is the
+    reference's own dispatch: head-pair tasks on `nthreads` threads (attention.mojo:276-287),
+    sequences one after another (…batched.mojo:2951). par 3 is the all-cores batched mode:
+    every (sequence, head pair) task of a step on `nthreads` threads at once."""
     from oracle import oracle as O
+    O.use_host_build()
 
     B = sched.B
     st = O.CacheState(2, sched.kv_stride, sched.BS, sched.num_blocks, B, sched.table_stride,
@@ -216,10 +249,10 @@ def run_cpu(sched, data, seconds, nthreads, log):
             o = O.attend(qh[j, layer], st.k_pools[layer], st.v_pools[layer], st.tables,
                          st.table_lens, sched.pos[j], 1, sched.HQ, sched.HKV, sched.D, sched.BS,
                          sched.WINDOW if layer == 0 else 0, scale=sched.SCALE,
-                         nthreads=nthreads, par=0)
+                         nthreads=nthreads, par=par)
             step_out.append(o)
         elapsed += time.perf_counter() - t0
-        if j < 2:  # float64 attention of the same inputs (outside the timed sample)
+        if j < 2 and par == 0:  # float64 attention of the same inputs (outside the sample)
             for layer in range(2):
                 exact.append((j, layer, O.attend_f64(
                     qh[j, layer], st.k_pools[layer], st.v_pools[layer], st.tables,
@@ -229,7 +262,7 @@ def run_cpu(sched, data, seconds, nthreads, log):
         done += 1
         if elapsed >= seconds:
             break
-    log(f"cpu baseline: {done} steps in {elapsed:.1f}s on {nthreads} threads")
+    log(f"cpu baseline (par {par}): {done} steps in {elapsed:.1f}s on {nthreads} threads")
     return dict(steps=done, seconds=elapsed, outs=outs, exact=exact)
 
 
@@ -349,6 +382,7 @@ def bench_config1(args, log):
                 {"attend_us": round(dur * 1e3, 2)})
     if args.cpu_seconds > 0:
         from oracle import oracle as O
+        O.use_host_build()
 
         st = O.CacheState(1, w.kv_stride, w.BS, w.num_blocks, 1, w.table_stride,
                           alloc_pools=False)
@@ -368,7 +402,7 @@ def bench_config1(args, log):
             el += time.perf_counter() - t
             n += 1
         res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "steps/s",
-                               "cores": args.cpu_threads, "kind": "port",
+                               "cores": args.cpu_threads, "kind": "port", "host": host_cpu_info(),
                                "sample": f"{n} steps (append + paged_attention_layer, "
                                          f"{args.cpu_threads} head-pair tasks)"}
         res["parity_sample_max_rel_err"] = float(f"{O.max_rel_err(got, ref):.3g}")
@@ -418,6 +452,7 @@ def bench_config3(args, log):
     res["roofline"]["traffic"] = _traffic_from_profiles("stream_attend_bf16_cfg3_profile.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
+        O.use_host_build()
 
         k, v, q = d["k"].numpy().reshape(-1), d["v"].numpy().reshape(-1), d["q"].numpy()
         tables = np.ascontiguousarray(w.tables0)
@@ -429,7 +464,7 @@ def bench_config3(args, log):
             el += time.perf_counter() - t
             n += 1
         res["cpu_baseline"] = {"value": round(w.B * n / el, 3), "unit": "tokens/s",
-                               "cores": args.cpu_threads, "kind": "port",
+                               "cores": args.cpu_threads, "kind": "port", "host": host_cpu_info(),
                                "sample": f"{n} attention steps (8 sequences in turn, "
                                          f"{args.cpu_threads} head-pair tasks per call; the "
                                          f"pre-append pools, so the 32768th key differs)"}
@@ -489,6 +524,7 @@ def bench_config4(args, log):
                 {"prefill_us": round(dur * 1e3, 2), "prefixes": w.prefix.tolist()})
     if args.cpu_seconds > 0:
         from oracle import oracle as O
+        O.use_host_build()
 
         k, v = d["k"].numpy().reshape(-1), d["v"].numpy().reshape(-1)
         kn = d["k_new"].numpy().reshape(-1, w.kv_stride)
@@ -514,7 +550,7 @@ def bench_config4(args, log):
             errs.append(O.max_rel_err(got[n], ref[0, 0]))
             n += 1
         res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s",
-                               "cores": args.cpu_threads, "kind": "port",
+                               "cores": args.cpu_threads, "kind": "port", "host": host_cpu_info(),
                                "sample": f"first {n} chunk queries of sequence 0 (prefix "
                                          f"{int(w.prefix[0])}), one paged_attention_layer call "
                                          f"each, {args.cpu_threads} head-pair tasks"}
@@ -601,6 +637,7 @@ def bench_config5(args, log):
     res["roofline"]["traffic"] = _traffic_from_profiles("verify_mtp_cfg5_traffic.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
+        O.use_host_build()
 
         st = O.CacheState(L, w.kv_stride, w.BS, w.num_blocks, B, w.table_stride,
                           alloc_pools=False)
@@ -646,7 +683,7 @@ def bench_config5(args, log):
             if el >= args.cpu_seconds:
                 break
         res["cpu_baseline"] = {"value": round(B * DR * n / el, 2), "unit": "tokens/s",
-                               "cores": args.cpu_threads, "kind": "port",
+                               "cores": args.cpu_threads, "kind": "port", "host": host_cpu_info(),
                                "sample": f"first {n} iterations of the schedule (MTP reads, "
                                          f"appends, verify as {DR} sequential "
                                          f"paged_attention_layer calls per sequence, rollback)"}
@@ -733,6 +770,7 @@ def bench_producer(args, log):
                                   "pools": "fp32"}})
     if args.cpu_seconds > 0:
         from oracle import oracle as O
+        O.use_host_build()
 
         c = dec["cache"]
         q, k, v = dec["q"].numpy(), dec["k"].numpy(), dec["v"].numpy()
@@ -752,7 +790,7 @@ def bench_producer(args, log):
             n += 1
         ex_q, _, _ = O.producer_f64(dec["pos"], off, q, k, v, qw, kw, 1, HQ, HKV, D, False)
         res["cpu_baseline"] = {"value": round(32 * n / el, 2), "unit": "tokens/s",
-                               "cores": 1, "kind": "port",
+                               "cores": 1, "kind": "port", "host": host_cpu_info(),
                                "sample": f"{n} decode-shape calls (32 tokens each) of the "
                                          f"oracle's per-token rms_norm / apply_rope_qk / "
                                          f"append, one thread"}
@@ -881,6 +919,7 @@ def bench_lsa(args, log):
     res["roofline"]["traffic"] = _traffic_from_profiles("lsa_sparse_stream_traffic.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
+        O.use_host_build()
 
         k = cache.k_pools[0].numpy().reshape(-1)
         v = cache.v_pools[0].numpy().reshape(-1)
@@ -897,7 +936,7 @@ def bench_lsa(args, log):
                                     HKV, D, BS, scale=0.0625)
         ref = np.concatenate(refs)
         res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "tokens/s",
-                               "cores": args.cpu_threads, "kind": "port",
+                               "cores": args.cpu_threads, "kind": "port", "host": host_cpu_info(),
                                "sample": f"first {n} sequences, one lsa_sparse_paged_attention "
                                          f"call each on {args.cpu_threads} head-pair threads"}
         res["parity_sample"] = {"sequences": n,
@@ -914,6 +953,8 @@ def bench_wo(args, log):
     from pkv import hip, q4_matmul, synth
 
     from oracle import oracle as O
+
+    O.use_host_build()
 
     B, C_OUT = 32, 2816
     stream = hip.Stream()
@@ -969,7 +1010,7 @@ def bench_wo(args, log):
                          float(np.max(np.abs(ref - exact)))))
             n += 1
         res["cpu_baseline"] = {"value": round(n / el, 2), "unit": "sequences/s", "cores": 1,
-                               "kind": "port",
+                               "kind": "port", "host": host_cpu_info(),
                                "sample": f"{n} q4_matmul_vec calls (8192 -> 2816), one thread"}
         res["parity_sample"] = {"max_abs_err_vs_cpu_fp32": float(f"{max(e[0] for e in errs):.3g}"),
                                 "max_abs_err_vs_float64": float(f"{max(e[1] for e in errs):.3g}"),
@@ -986,7 +1027,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU-baseline sample (0 disables it)")
     ap.add_argument("--cpu-threads", type=int, default=8,
-                    help="threads for the reference CPU path (8 = its Hq/2 head-pair tasks)")
+                    help="threads of the reference-faithful CPU mode (8 = its Hq/2 head-pair "
+                         "tasks); the all-cores mode uses the job's OpenMP share of the host")
     ap.add_argument("--quiet", action="store_true")
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="BASELINE.json configuration (2, the default, is the headline)")
@@ -1066,17 +1108,35 @@ def main() -> int:
         "append_status_ok": bool(np.all(g["status"] == 0)),
     }
     if args.cpu_seconds > 0:
-        c = run_cpu(sched, data, args.cpu_seconds, args.cpu_threads, log)
         from oracle import oracle as O
 
+        lib_path = O.use_host_build()
+        host = host_cpu_info()
+        all_threads = host["omp_num_threads"] or os.cpu_count() or 1
+        all_threads = min(all_threads, os.cpu_count() or all_threads)
+        c = run_cpu(sched, data, args.cpu_seconds / 2, args.cpu_threads, log, par=0)
+        cb = run_cpu(sched, data, args.cpu_seconds / 2, all_threads, log, par=3)
         errs = [O.max_rel_err(g["outs"][j, layer], c["outs"][j][layer])
                 for j in range(min(c["steps"], steps)) for layer in range(2)]
+        same = all(np.array_equal(c["outs"][j][layer], cb["outs"][j][layer])
+                   for j in range(min(c["steps"], cb["steps"])) for layer in range(2))
+        faithful = round(sched.B * c["steps"] / c["seconds"], 2)
+        batched = round(sched.B * cb["steps"] / cb["seconds"], 2)
         result["cpu_baseline"] = {
-            "value": round(sched.B * c["steps"] / c["seconds"], 2), "unit": "tokens/s",
-            "cores": args.cpu_threads, "kind": "port",
-            "sample": f"first {c['steps']} steps of the same 64-step schedule (both layers, "
-                      f"appends + attention), reference-faithful: sequences in turn, "
-                      f"{args.cpu_threads} head-pair tasks per call"}
+            "value": batched, "unit": "tokens/s", "cores": all_threads, "kind": "port",
+            "sample": f"first {cb['steps']} steps of the same 64-step schedule (both layers, "
+                      f"appends + attention), all-cores batched: every (sequence, head pair) "
+                      f"task of a step on {all_threads} threads; the oracle's "
+                      f"{os.path.basename(lib_path)} build",
+            "host": host,
+            "modes": {
+                "reference_faithful": {
+                    "value": faithful, "threads": args.cpu_threads, "steps": c["steps"],
+                    "how": f"sequences in turn, {args.cpu_threads} head-pair tasks per call "
+                           f"(attention.mojo:276-287)"},
+                "all_cores_batched": {"value": batched, "threads": all_threads,
+                                      "steps": cb["steps"],
+                                      "outputs_equal_reference_faithful": bool(same)}}}
         if errs:
             result["parity_sample_max_rel_err"] = float(f"{max(errs):.3g}")
             # The fp32 reference path is itself an approximation: on these long contexts it

@@ -12,10 +12,37 @@ import os
 import numpy as np
 
 ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(ORACLE_DIR, "libpkv_oracle.so")
+# PKV_ORACLE_LIB selects another build of the same source (the sanitizer build of
+# `make -C oracle sanitize`, or the AVX-512 build the benchmark times).
+LIB_PATH = os.environ.get("PKV_ORACLE_LIB") or os.path.join(ORACLE_DIR, "libpkv_oracle.so")
+LIB_V4_PATH = os.path.join(ORACLE_DIR, "libpkv_oracle_v4.so")
 
 F32, BF16 = 0, 1
 _lib = None
+
+
+def host_has_avx512() -> bool:
+    """True when this host's CPU runs x86-64-v4 code (AVX-512 F, BW, CD, DQ, VL)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags
+    except OSError:
+        pass
+    return False
+
+
+def use_host_build() -> str:
+    """Loads the build for this host's ISA level (the AVX-512 one where the CPU has it and
+    it is built) before the first oracle call; returns the path in use. The builds differ
+    only in vector width: every restated loop keeps its own summation order."""
+    global LIB_PATH
+    if _lib is None and "PKV_ORACLE_LIB" not in os.environ and host_has_avx512() \
+            and os.path.exists(LIB_V4_PATH):
+        LIB_PATH = LIB_V4_PATH
+    return LIB_PATH
 
 
 def _L():

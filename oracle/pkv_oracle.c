@@ -227,16 +227,13 @@ static void eval_head_range(const float* q, const void* k_pool, const void* v_po
  * (the reference's debug_assert, :271).
  * nthreads > 1 runs the head-pair tasks on OpenMP threads, mirroring the
  * reference's parallelize over num_heads // 2 tasks (:276-287).            */
-int pkvo_paged_attention_layer(const float* q, const void* k_pool, const void* v_pool, int dtype,
-                               const int64_t* block_table, int64_t table_len, int64_t block_size,
-                               int64_t pos, int64_t num_heads, int64_t num_kv_heads,
-                               int64_t head_dim, int64_t window, float* scores, int64_t* rows,
-                               float* attn_out, int64_t ring_size, int64_t ring_base, int nthreads) {
-    int64_t kv_stride = num_kv_heads * head_dim;
-    int64_t ratio = num_heads / num_kv_heads;
+/* Key rows of paged_attention_layer (attention.mojo:258-274): rows[i] = pool offset of
+ * key start_t + i. Returns n, or -1 / -2 as pkvo_paged_attention_layer. */
+static int64_t pal_rows(const int64_t* block_table, int64_t table_len, int64_t block_size,
+                        int64_t pos, int64_t kv_stride, int64_t window, int64_t* rows,
+                        int64_t ring_size, int64_t ring_base) {
     int64_t start_t = pkvo_window_start(pos, window);
     int64_t n = pos + 1 - start_t;
-
     if (ring_size > 0) {
         if (n > ring_size) return -1;
         for (int64_t i = 0; i < n; ++i) {
@@ -250,8 +247,26 @@ int pkvo_paged_attention_layer(const float* q, const void* k_pool, const void* v
             rows[i] = (block_table[t / block_size] * block_size + t % block_size) * kv_stride;
         }
     }
+    return n < 0 ? 0 : n;
+}
 
-    if (n >= 64 && num_heads >= 4 && (num_heads % 2 == 0) && (ratio % 2 == 0)) {
+/* The head-pair dispatch condition of attention.mojo:276. */
+static int pal_pairs(int64_t n, int64_t num_heads, int64_t ratio) {
+    return n >= 64 && num_heads >= 4 && (num_heads % 2 == 0) && (ratio % 2 == 0);
+}
+
+int pkvo_paged_attention_layer(const float* q, const void* k_pool, const void* v_pool, int dtype,
+                               const int64_t* block_table, int64_t table_len, int64_t block_size,
+                               int64_t pos, int64_t num_heads, int64_t num_kv_heads,
+                               int64_t head_dim, int64_t window, float* scores, int64_t* rows,
+                               float* attn_out, int64_t ring_size, int64_t ring_base, int nthreads) {
+    int64_t kv_stride = num_kv_heads * head_dim;
+    int64_t ratio = num_heads / num_kv_heads;
+    int64_t n = pal_rows(block_table, table_len, block_size, pos, kv_stride, window, rows,
+                         ring_size, ring_base);
+    if (n < 0) return (int)n;
+
+    if (pal_pairs(n, num_heads, ratio)) {
         int64_t num_pairs = num_heads / 2;
 #pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static, 1) if (nthreads > 1)
         for (int64_t t = 0; t < num_pairs; ++t) {
@@ -984,10 +999,77 @@ void pkvo_rollback(int32_t block_size, int32_t* tables, int32_t table_stride, in
  * par: 0 = serial over sequences, head-pair tasks on `nthreads` threads
  *      (reference-faithful); 1 = sequences spread over `nthreads` threads;
  *      2 = (sequence, query) pairs spread over `nthreads` threads (the calls are
- *      independent once the keys are in the pool; used for long prefill chunks).
+ *      independent once the keys are in the pool; used for long prefill chunks);
+ *      3 = every core on (sequence, query, head pair) items: the batched CPU mode, whose
+ *      items are the reference's head-pair tasks of every call at once (a call below
+ *      the head-pair condition of attention.mojo:276 is one item). Every mode computes
+ *      each head with the same arithmetic, so all give the same bits.
  * ring_size > 0: ring pools; tables[s * table_stride] is sequence s's ring slot and
  * the call passes ring_base = slot * ring_size (…batched.mojo:648). Returns -1 when a
  * query's window exceeds the ring (the reference aborts, attention.mojo:265-266). */
+/* pkvo_attend's par = 3: items (s, j, pair) over all threads. Item (s, j, t) computes the
+ * key rows of query j of sequence s, then head pair t as paged_attention_layer's task t
+ * does; when the call takes the serial path (attention.mojo:283-287) item t = 0 runs it
+ * and the others do nothing. */
+static int attend_pairs(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        int32_t block_size, int32_t window, float q_scale, const float* q,
+                        const void* k_pool, const void* v_pool, const int32_t* tables,
+                        int32_t table_stride, const int32_t* table_lens, const int32_t* pos,
+                        int32_t q_len, int32_t batch, float* out, int nthreads, int32_t ring_size,
+                        int64_t max_n) {
+    const int64_t hd = (int64_t)num_heads * head_dim;
+    const int64_t ratio = num_heads / num_kv_heads;
+    const int64_t kv_stride = (int64_t)num_kv_heads * head_dim;
+    const int64_t pairs = num_heads / 2 > 0 ? num_heads / 2 : 1;
+    const int64_t items = (int64_t)batch * q_len * pairs;
+    int err = 0;
+#pragma omp parallel num_threads(nthreads > 0 ? nthreads : 1) if (nthreads > 1)
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)(num_heads * (max_n + 1)));
+        int64_t* rows = (int64_t*)malloc(sizeof(int64_t) * (size_t)(max_n + 1));
+        int64_t* tab = (int64_t*)malloc(sizeof(int64_t) * (size_t)(table_stride > 0 ? table_stride : 1));
+        float* qs = (float*)malloc(sizeof(float) * (size_t)hd);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t it = 0; it < items; ++it) {
+            const int32_t s = (int32_t)(it / ((int64_t)q_len * pairs));
+            const int32_t j = (int32_t)((it / pairs) % q_len);
+            const int64_t t = it % pairs;
+            const float* qj = q + ((int64_t)s * q_len + j) * hd;
+            float* oj = out + ((int64_t)s * q_len + j) * hd;
+            if (pos[s] < 0) {
+                if (t == 0)
+                    for (int64_t i = 0; i < hd; ++i) oj[i] = 0.0f;
+                continue;
+            }
+            for (int32_t i = 0; i < table_stride; ++i) tab[i] = tables[(int64_t)s * table_stride + i];
+            for (int64_t i = 0; i < hd; ++i) qs[i] = qj[i] * q_scale;
+            const int64_t ring_base = ring_size > 0 ? tab[0] * ring_size : 0;
+            const int64_t n = pal_rows(tab, ring_size > 0 ? 0 : table_lens[s], block_size,
+                                       (int64_t)pos[s] + j, kv_stride, window, rows, ring_size,
+                                       ring_base);
+            if (n < 0) {
+#pragma omp atomic write
+                err = (int)n;
+                continue;
+            }
+            if (pal_pairs(n, num_heads, ratio)) {
+                const int64_t h_start = t * 2;
+                eval_head_range(qs, k_pool, v_pool, dtype, rows, scores, oj, n,
+                                (h_start / ratio) * head_dim, h_start, h_start + 2, head_dim);
+            } else if (t == 0) {
+                for (int64_t g = 0; g < num_kv_heads; ++g)
+                    eval_head_range(qs, k_pool, v_pool, dtype, rows, scores, oj, n, g * head_dim,
+                                    g * ratio, g * ratio + ratio, head_dim);
+            }
+        }
+        free(scores);
+        free(rows);
+        free(tab);
+        free(qs);
+    }
+    return err;
+}
+
 int pkvo_attend(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                 int32_t block_size, int32_t window, float q_scale, const float* q,
                 const void* k_pool, const void* v_pool, const int32_t* tables,
@@ -1001,6 +1083,10 @@ int pkvo_attend(int dtype, int32_t num_heads, int32_t num_kv_heads, int32_t head
     }
     int64_t hd = (int64_t)num_heads * head_dim;
     int err = 0;
+    if (par == 3)
+        return attend_pairs(dtype, num_heads, num_kv_heads, head_dim, block_size, window, q_scale,
+                            q, k_pool, v_pool, tables, table_stride, table_lens, pos, q_len,
+                            batch, out, nthreads, ring_size, max_n);
     int outer = (par >= 1 && nthreads > 1) ? nthreads : 1;
     int inner = (par >= 1) ? 1 : nthreads;
     /* par 2: one work item per (sequence, query); otherwise one per sequence. */

@@ -237,3 +237,26 @@ def test_batched_f64_oracle_agrees_with_per_token_f64():
     r32 = O.attend(q, fx.k_pool, fx.v_pool, tables, np.array([160], np.int32),
                    np.array([1500], np.int32), 3, 16, 8, 256, BLOCK_SIZE, 1024, scale=0.0625)
     assert O.max_rel_err(r32, ex) < 1e-4
+
+
+@pytest.mark.parametrize("geom", [(16, 8, 256), (16, 2, 512), (6, 3, 64), (5, 5, 64)],
+                         ids=["16q8kv", "16q2kv", "ratio2-odd-pairs", "odd-heads"])
+def test_every_parallel_mode_gives_the_same_bits(geom):
+    """par 0 (reference-faithful: head-pair tasks per call), 1 (sequences over threads),
+    2 ((sequence, query) items) and 3 (every core on (sequence, query, head pair) items,
+    the batched CPU baseline) compute each head with the same arithmetic: identical bits,
+    including calls below the head-pair condition (n < 64, odd ratio or head count),
+    windows and an inactive sequence."""
+    hq, hkv, d = geom
+    fx = Fixture(hq, hkv, d, seed=21, k_scale=0.25)
+    tables = np.stack([fx.table, fx.table[::-1], fx.table, fx.table[::-1]]).astype(np.int32)
+    lens = np.full(4, 160, np.int32)
+    pos = np.array([700, 30, -1, 2000], np.int32)  # 30: n < 64 -> the serial path
+    q = np.random.default_rng(2).standard_normal((4, 2, hq, d)).astype(np.float32)
+    outs = [O.attend(q, fx.k_pool, fx.v_pool, tables, lens, pos, 2, hq, hkv, d, BLOCK_SIZE, w,
+                     scale=0.0625, nthreads=4, par=par)
+            for w in (0, 512) for par in (0, 1, 2, 3)]
+    for i in range(1, 4):
+        np.testing.assert_array_equal(outs[i], outs[0])
+        np.testing.assert_array_equal(outs[4 + i], outs[4])
+    assert np.all(outs[0][2] == 0.0)
