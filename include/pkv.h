@@ -370,7 +370,8 @@ int32_t pkv_paged_attention_layer(void* stream, const float* q, const void* k_po
                                   int32_t num_blocks, int32_t kv_dtype, void* workspace,
                                   size_t workspace_bytes);
 
-/* Bytes of workspace pkv_q4_matmul needs (split-K partials); 0 on invalid sizes. */
+/* Bytes of workspace pkv_q4_matmul needs (split-K partials and per-row-group arrival
+ * counts); 0 on invalid sizes. */
 size_t pkv_q4_matmul_workspace_size(int32_t c_in, int32_t c_out, int32_t batch);
 
 /* Wo projection after attention -- batched Q4_0 matrix-vector products.
@@ -381,8 +382,11 @@ size_t pkv_q4_matmul_workspace_size(int32_t c_in, int32_t c_out, int32_t batch);
  * block-32 form (moe_kernels.mojo:7-57): w_packed uint8 [c_out][c_in / 2] (byte j of a
  * block: element 2j in the low nibble, 2j + 1 in the high one; value nibble - 8) and
  * scales fp32 [c_out][c_in / 32]. c_in % 32 == 0, batch <= 64; w_packed and x 16-byte,
- * scales 4-byte aligned (the weights are read in 16-byte chunks). Products are exact (bf16 matrix cores on a three-way split of x) and
- * sums are fp32. One or two launches. */
+ * scales 4-byte aligned (the weights are read in 16-byte chunks). Products are exact (bf16
+ * matrix cores on a three-way split of x) and sums are fp32, added in a fixed order. The
+ * workspace (16-byte aligned) must be zero-filled before its first use; every call leaves
+ * its counters at zero again, so one workspace serves any sequence of calls on a stream.
+ * One launch. */
 int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales, const float* x,
                       int32_t c_in, int32_t c_out, int32_t batch, float* out, void* workspace,
                       size_t workspace_bytes);

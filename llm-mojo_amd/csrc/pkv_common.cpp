@@ -2,7 +2,11 @@
 // layout, and the single-sequence paged_attention_layer drop-in.
 #include <hip/hip_runtime.h>
 
+#include <map>
+#include <mutex>
 #include <string>
+#include <tuple>
+#include <utility>
 
 #include "pkv_internal.h"
 
@@ -25,6 +29,39 @@ int32_t check_launch(const char* what) {
     if (e != hipSuccess)
         return fail(PKV_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
     return PKV_OK;
+}
+
+namespace {
+struct Occ {
+    std::mutex mu;
+    std::map<std::tuple<const void*, int, int, size_t>, int> blocks;  // -> workgroups
+};
+Occ& occ() {
+    static Occ o;
+    return o;
+}
+}  // namespace
+
+int device_fill_workgroups(const void* fn, int threads, size_t lds, int cap) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    Occ& o = occ();
+    std::lock_guard<std::mutex> lk(o.mu);
+    auto key = std::make_tuple(fn, dev, threads, lds);
+    auto it = o.blocks.find(key);
+    int p = 0;
+    if (it != o.blocks.end()) {
+        p = it->second;
+    } else {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return -1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess)
+            return -1;
+        p = cus * (per_cu > 0 ? per_cu : 1);
+        o.blocks.emplace(key, p);
+    }
+    return p > cap ? cap : p;
 }
 
 int32_t validate_params(const pkv_params* p) {

@@ -19,6 +19,11 @@ void clear_error();
 int32_t fail(int32_t code, const std::string& msg);
 int32_t check_launch(const char* what);
 
+// Workgroups of `threads` threads and `lds` bytes of dynamic LDS of kernel `fn` that are
+// resident on the current device at once (CUs x occupancy), at most `cap`; -1 if the
+// runtime query fails. Cached per (kernel, device, shape).
+int device_fill_workgroups(const void* fn, int threads, size_t lds, int cap);
+
 // Validates the geometry shared by every entry point. Returns PKV_OK or an error code
 // (message set).
 int32_t validate_params(const pkv_params* p);

@@ -7,25 +7,36 @@
 // nibble and 2j + 1 in its high one, value (nibble - 8) * scale.
 //
 // At decode batches this is a skinny GEMM (M = c_out rows, N = batch, K = c_in) whose
-// weights are read once, so it is HBM-bound on the weights; fp32 FMAs on the vector units
-// would take several times the weight-read time, so it runs on the matrix cores:
-//   - one v_mfma_f32_16x16x32_bf16 covers exactly one Q4 block: A = 16 rows x 32 weights
-//     (nibble - 8 is exact in bf16), B = 32 inputs x 16 sequences;
-//   - x is split into three bf16 parts (hi + mid + lo = x exactly: 3 x 8 bits cover fp32's
-//     24-bit significand), so every product is exact and only fp32 accumulation rounds;
-//   - the block's fp32 partial is scaled and accumulated in fp32.
-// Work split: a workgroup owns 128 rows and a split of KB blocks of K. It stages its
-// fp32 x slice in LDS once, in B-operand order; its 8 waves are 2 row halves x 4 K
-// quarters, so each wave takes 64 rows (4 A tiles) over KB / 4 blocks and a B operand,
-// read from LDS and split into parts in registers, feeds 4 A tiles. The K quarters are
-// summed through LDS in a fixed order, (q0 + q1) + (q2 + q3), and the workgroup writes
-// its split's partial; q4_reduce_kernel adds the splits in order (deterministic). A
-// single split writes out directly. Workgroups of one split are placed on one XCD
-// (dispatch is round-robin over the 8 XCDs), so each XCD's L2 holds one slice of x.
+// weights are read once, so it is HBM-bound on the weights; it runs on the matrix cores:
+//   - one v_mfma_f32_16x16x32_bf16 covers exactly one Q4 block: A = 32 inputs of 16
+//     sequences, B = 16 rows x 32 weights (nibble - 8 is exact in bf16);
+//   - x is split into three bf16 parts (hi + mid + lo = x exactly: each part takes the
+//     next 8 significant bits of the 24-bit fp32 significand), so every product is exact
+//     and only the fp32 accumulation rounds;
+//   - the block's fp32 sum is scaled by the row's block scale and accumulated in fp32.
+//
+// Work split: row groups of 64 rows, each split into `splits` runs of `per` consecutive
+// blocks, one workgroup per run, as many runs as keep every workgroup resident (two
+// 8-wave workgroups per CU). Per workgroup:
+//   - its rows' weights and scales go straight into LDS (global_load_lds over
+//     consecutive memory: a row's blocks are contiguous, so whole cache lines are read),
+//     in passes of 8 blocks that are computed as they land;
+//   - the eight waves take the blocks in turn (wave v: blocks v, v + 8, ...); a wave
+//     splits the inputs of its block into three exact bf16 operands once and feeds them
+//     to every row tile of the group;
+//   - the waves' sums are added through LDS in a fixed order. With one run per group the
+//     workgroup writes out directly. Otherwise it writes its partial sums and counts
+//     itself in the group's arrival counter; the last to arrive adds the group's
+//     partials in run order (deterministic) and writes out. The partials are written and
+//     read at system scope (through and past the L2 caches), so no cache write-back or
+//     invalidation is needed; device-scope fences here cost more than the whole product
+//     on this 8-XCD part.
 //
 // MFMA lane layouts (v_mfma_f32_16x16x32_bf16):
 //   A[i][k]: lane i + 16*(k/8), element k%8;   B[k][j]: lane j + 16*(k/8), element k%8;
 //   C[i][j]: lane j + 16*(i/4), register i%4.
+// A block's element e of quarter g (K index 8g + e) is nibble e of dword g of the block
+// (byte 4g + e/2, low nibble for even e), so both operands use the block's own K order.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -36,262 +47,333 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kQ4WR = 2;                       // row halves per workgroup
-constexpr int kQ4WK = 4;                       // K quarters per workgroup
-constexpr int kQ4Waves = kQ4WR * kQ4WK;
-constexpr int kQ4ATiles = 4;                   // 16-row A tiles per wave
-constexpr int kQ4Rows = kQ4WR * kQ4ATiles * 16;  // output rows per workgroup
-constexpr int kQ4KB = 8;                       // Q4 blocks per split
-constexpr int kQ4MaxBatch = 64;                // four column tiles of 16
-constexpr int kQ4Parts = 3;                    // bf16 parts of each input
+constexpr int kQ4Waves = 8;               // waves per workgroup (blocks taken in turn)
+constexpr int kQ4NT = kQ4Waves * 64;
+constexpr int kQ4MaxBatch = 64;           // four column tiles of 16
+constexpr int kQ4MaxWg = 1024;            // workgroups, at most
 
 struct Q4Args {
     const uint8_t* w;     // [c_out][c_in / 2]
     const float* scales;  // [c_out][c_in / 32]
     const float* x;       // [batch][c_in]
     float* out;           // [batch][c_out]
-    float* part;          // [splits][batch][c_out] (splits > 1)
+    float* part;          // [workgroups][batch][rows of a group] (split row groups)
+    int32_t* arrived;     // [groups]: workgroups of the row group done (zero between calls)
     int32_t c_in;
     int32_t c_out;
     int32_t batch;
     int32_t nb;      // blocks per row
-    int32_t groups;  // row groups of kQ4Rows
-    int32_t splits;
+    int32_t groups;  // row groups
+    int32_t splits;  // workgroups per row group (each takes `per` consecutive blocks)
+    int32_t per;
 };
 
-
-__device__ inline bf16x8 as_bf16x8(uint4 v) {
+__device__ inline bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint4 v = make_uint4(a, b, c, d);
     bf16x8 r;
     __builtin_memcpy(&r, &v, 16);
     return r;
 }
 
-// 8 weights (nibbles of w, low first) minus 8, as bf16 bits: small integers, exact.
-__device__ inline bf16x8 weights_bf16(uint32_t w) {
-    uint32_t h[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float a = (float)((int)((w >> (8 * e)) & 15u) - 8);
-        const float b = (float)((int)((w >> (8 * e + 4)) & 15u) - 8);
-        h[e] = (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
-    }
-    return as_bf16x8(make_uint4(h[0], h[1], h[2], h[3]));
+// The upper halves of two fp32 words as one bf16 pair (lo first).
+__device__ inline uint32_t hi_pair(uint32_t lo, uint32_t hi) {
+    return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
 }
 
-// TILES = column tiles of 16 sequences, KB = blocks per split; both compile-time, so the
-// whole body is one basic block: every MFMA result is read by VALU code in the MFMA's own
-// block. (With a runtime tile count a chain ended in a branch and the first register of
-// its result was read in the target block without the MFMA's wait states: a wrong,
-// varying value in every fourth row.)
-// Up to two column tiles the kernel fits 80 VGPRs, which keeps three workgroups per CU
-// resident (six waves per SIMD): the 704 workgroups of an 8192 -> 2816 call then run in
-// one round instead of two.
-template <int TILES, int KB>
-__global__ __launch_bounds__(kQ4Waves * 64, TILES <= 2 ? 6 : 1) void q4_matmul_kernel(Q4Args a) {
-    constexpr int NT = kQ4Waves * 64;
-    constexpr int BPW = KB / kQ4WK;  // blocks per wave
-    // x slice in B-operand order: slot ((ct * KB + b) * 2 + h) * 64 + lane holds inputs
-    // 8 (lane >> 4) + 4h .. +3 of block b of sequence 16 ct + (lane & 15), so a wave's
-    // operand read is 64 consecutive 16-byte slots. Reused for the K-quarter sums.
-    constexpr int kSlots = TILES * KB * 2 * 64;
-    constexpr int kRed = kQ4WR * 2 * kQ4ATiles * TILES * 64;  // f32x4 per pair of quarters
-    static_assert(kRed * 16 <= kSlots * 16, "quarter sums fit the x slice");
-    __shared__ uint4 s_x[kSlots];
-    __shared__ uint4 s_w[kQ4Rows * KB];                                  // weights, see below
-    __shared__ __attribute__((aligned(16))) float s_sc[KB][kQ4Rows];     // scales [block][row]
+// 8 weights of one dword (element e = nibble e, value nibble - 8) as bf16 values of
+// (nibble - 8) / 16, exactly. v_cvt_off_f32_i4 converts bits [3:0] of its operand, read
+// as a signed 4-bit integer, to that integer / 16; with SDWA it reads one byte, so the
+// low nibbles come from the bytes of w ^ 0x88888888 (nibble ^ 8 as a signed 4-bit field
+// is nibble - 8) and the high ones from the same word shifted right by 4. The 1/16 is
+// folded into the block scale (a power of two: the scaled sums round as before).
+template <int BYTE>
+__device__ inline float cvt_off_byte(uint32_t v) {
+    float r;
+    if constexpr (BYTE == 0)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(v));
+    else if constexpr (BYTE == 1)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(v));
+    else if constexpr (BYTE == 2)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(v));
+    else
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ inline bf16x8 unpack_q4(uint32_t w) {
+    const uint32_t lo = w ^ 0x88888888u, hi = lo >> 4;
+    return as_bf16x8(hi_pair(__float_as_uint(cvt_off_byte<0>(lo)), __float_as_uint(cvt_off_byte<0>(hi))),
+                     hi_pair(__float_as_uint(cvt_off_byte<1>(lo)), __float_as_uint(cvt_off_byte<1>(hi))),
+                     hi_pair(__float_as_uint(cvt_off_byte<2>(lo)), __float_as_uint(cvt_off_byte<2>(hi))),
+                     hi_pair(__float_as_uint(cvt_off_byte<3>(lo)), __float_as_uint(cvt_off_byte<3>(hi))));
+}
+constexpr float kQ4Unpack = 16.0f;  // unpack_q4 gives (nibble - 8) / 16
+
+// x = hi + mid + lo exactly: hi is x truncated to bf16; the remainder (at most 16
+// significant bits) is exact in fp32 and is truncated again; the last remainder has at
+// most 8 significant bits and is a bf16 value.
+__device__ inline void split3(const float (&v)[8], bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+    uint32_t h[4], m[4], l[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        uint32_t u[2], r[2], s[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            u[e] = __float_as_uint(v[2 * k + e]);
+            const float r1 = v[2 * k + e] - __uint_as_float(u[e] & 0xffff0000u);
+            r[e] = __float_as_uint(r1);
+            s[e] = __float_as_uint(r1 - __uint_as_float(r[e] & 0xffff0000u));
+        }
+        h[k] = hi_pair(u[0], u[1]);
+        m[k] = hi_pair(r[0], r[1]);
+        l[k] = hi_pair(s[0], s[1]);
+    }
+    hi = as_bf16x8(h[0], h[1], h[2], h[3]);
+    mid = as_bf16x8(m[0], m[1], m[2], m[3]);
+    lo = as_bf16x8(l[0], l[1], l[2], l[3]);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ inline void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+constexpr int kQ4Lds = 128 * 1024;
+constexpr int kQ4MaxPass = 3;  // passes of 8 blocks staged at once (one block per wave each)
+
+// TILES column tiles of 16 sequences; RH row halves of 64 rows (row group = 64 RH rows).
+// TILES and RH are compile-time, so every MFMA result is read in the MFMA's own basic
+// block (with a runtime count a chain could end in a branch whose target read the first
+// result register without the MFMA's wait states).
+//
+// Workgroup = (row group g, split k): blocks [k per, (k + 1) per) of the group's rows.
+// Operand roles: A = the inputs (16 sequences x 32), B = the weights (32 x 16 rows), so
+// C[seq][row] puts one row in each lane (lane j + 16q: row j of the tile, sequences
+// 4q .. 4q + 3) and each lane scales its four sums by one block scale.
+// Staging, per chunk of up to kQ4MaxPass passes of 8 blocks: every wave first requests the
+// fp32 inputs of its blocks (block v of each pass), then the workgroup copies the passes'
+// weights ([row][8 blocks] 16-byte chunks; a row's blocks are contiguous in memory, so
+// whole cache lines are read) and scales ([row][8 blocks]) straight into LDS, 2 RH copy
+// instructions per wave and pass. Pass i is computed as soon as its copies have landed
+// (vmcnt counts the later passes' copies), so the later passes stream in meanwhile.
+// In LDS, block bb of row r sits at chunk r * 8 + (bb ^ (r & 7)): the 16 rows of a
+// weight read then fall on different banks, two lanes per bank.
+template <int TILES, int RH>
+__global__ __launch_bounds__(kQ4NT) __attribute__((amdgpu_waves_per_eu(RH == 1 && TILES <= 2 ? 4 : 2)))
+void q4_matmul_kernel(Q4Args a) {
+    constexpr int RT = 4 * RH;        // row tiles of the group
+    constexpr int RG = 64 * RH;       // rows of the group
+    constexpr int kPassW = RG * 8 * 16;  // bytes of weights per pass
+    constexpr int kPassS = RG * 8 * 4;   // bytes of scales per pass
+    constexpr int kLds = kQ4Waves * RT * TILES * 64 * 16 > kQ4MaxPass * (kPassW + kPassS)
+                             ? kQ4Waves * RT * TILES * 64 * 16 : kQ4MaxPass * (kPassW + kPassS);
+    static_assert(kLds <= kQ4Lds, "LDS");
+    static_assert(kPassW / 1024 == kQ4Waves * RH && kPassS / 256 == kQ4Waves * RH,
+                  "RH copy instructions of each kind per wave and pass");
+    __shared__ __attribute__((aligned(16))) char smem[kLds];
+    f32x4* s_red = reinterpret_cast<f32x4*>(smem);  // [wave][RT][TILES][64], after the passes
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wr = wave / kQ4WK, wk = wave % kQ4WK;
-    const int g = lane >> 4;
+    const int v = tid >> 6;
+    const int j = lane & 15;
+    const int g = blockIdx.x / a.splits;
+    const int b_lo = (blockIdx.x % a.splits) * a.per;
+    const int b_hi = min(a.nb, b_lo + a.per);
 
-    // Work item: workgroups of one split are consecutive within an XCD.
-    int q = blockIdx.x;
-    const int total = a.groups * a.splits;
-    if (total % 8 == 0) q = (q % 8) * (total / 8) + q / 8;
-    const int split = q / a.groups;
-    const int grow0 = (q % a.groups) * kQ4Rows;  // the workgroup's first row
-    const int row0 = grow0 + wr * kQ4ATiles * 16;  // this wave's first row
-    const int kb0 = wk * BPW;                      // this wave's first block in the split
-    const int blk0 = split * KB;
-
-    // Requests first: x staging, weights (straight to LDS), scales.
-    constexpr int kStage = TILES * 16 * KB * 8 / NT;  // float4 per thread
-    static_assert(kStage * NT == TILES * 16 * KB * 8, "whole float4 per thread");
-    float4 xs[kStage];
+    f32x4 acc[RT][TILES];
 #pragma unroll
-    for (int i = 0; i < kStage; ++i) {
-        const int e = tid + i * NT;
-        const int m = e & 7, col = (e >> 3) % (TILES * 16), b = (e >> 3) / (TILES * 16);
-        xs[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (col < a.batch && blk0 + b < a.nb)
-            xs[i] = *reinterpret_cast<const float4*>(a.x + (size_t)col * a.c_in + (size_t)(blk0 + b) * 32 + 4 * m);
-    }
-    // Weights: the workgroup's rows x KB blocks (each row's KB * 16 contiguous bytes) go
-    // straight into LDS, 16 bytes per lane; row r's block b sits at position b ^ (r % 8)
-    // of its LDS row, so the 4-byte A-operand reads of 16 rows spread over the banks. Rows
-    // and blocks outside the matrix load a valid chunk and are replaced by zero weights
-    // when read.
-    constexpr int kWChunks = kQ4Rows * KB / (kQ4Waves * 64);  // DMA instructions per wave
-    static_assert(kWChunks * kQ4Waves * 64 == kQ4Rows * KB && KB == 8, "whole chunks per wave");
-#pragma unroll
-    for (int j = 0; j < kWChunks; ++j) {
-        const int pos = (wave * kWChunks + j) * 64 + lane;
-        const int r = pos / KB, b = (pos % KB) ^ (r & 7);
-        const bool in = grow0 + r < a.c_out && blk0 + b < a.nb;
-        const uint8_t* src = in ? a.w + (size_t)(grow0 + r) * (a.c_in / 2) + (size_t)(blk0 + b) * 16 : a.w;
-        __builtin_amdgcn_global_load_lds(src, (lds_void*)(s_w + (wave * kWChunks + j) * 64), 16, 0, 0);
-    }
-    // Scales: eight lanes read a row's KB consecutive scales; stored [block][row].
-    constexpr int kScPer = kQ4Rows * KB / NT;
-    float sc[kScPer];
-#pragma unroll
-    for (int i = 0; i < kScPer; ++i) {
-        const int e = tid + i * NT, r = e / KB, b = e % KB;
-        sc[i] = (grow0 + r < a.c_out && blk0 + b < a.nb) ? a.scales[(size_t)(grow0 + r) * a.nb + blk0 + b] : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < kStage; ++i) {
-        const int e = tid + i * NT;
-        const int m = e & 7, col = (e >> 3) % (TILES * 16), b = (e >> 3) / (TILES * 16);
-        const int ct = col >> 4, l = (col & 15) + 16 * (m >> 1), h = m & 1;
-        s_x[((ct * KB + b) * 2 + h) * 64 + l] = *reinterpret_cast<const uint4*>(&xs[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < kScPer; ++i) {
-        const int e = tid + i * NT;
-        s_sc[e % KB][e / KB] = sc[i];
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's weight chunks have landed
-    __syncthreads();
-    uint32_t wv[kQ4ATiles][BPW];
-#pragma unroll
-    for (int t = 0; t < kQ4ATiles; ++t) {
-        const int r = wr * kQ4ATiles * 16 + 16 * t + (lane & 15);  // row in the workgroup
-#pragma unroll
-        for (int bb = 0; bb < BPW; ++bb) {
-            const int b = kb0 + bb;
-            const uint32_t v = reinterpret_cast<const uint32_t*>(s_w)[(r * KB + (b ^ (r & 7))) * 4 + g];
-            // zeros after the offset outside the matrix
-            wv[t][bb] = (grow0 + r < a.c_out && blk0 + b < a.nb) ? v : 0x88888888u;
-        }
-    }
-
-    f32x4 acc[kQ4ATiles][TILES];
-#pragma unroll
-    for (int t = 0; t < kQ4ATiles; ++t)
+    for (int t = 0; t < RT; ++t)
 #pragma unroll
         for (int ct = 0; ct < TILES; ++ct) acc[t][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int c_lo = b_lo; c_lo < b_hi; c_lo += 8 * kQ4MaxPass) {
+        const int cn = min(8 * kQ4MaxPass, b_hi - c_lo);
+        const int passes = (cn + 7) / 8;
+        // 1. the inputs of this wave's blocks (L2-resident): per column tile, 8 of one
+        // sequence per lane (lane j + 16q: sequence 16ct + j, inputs 32b + 8q .. + 7)
+        float4 xr[kQ4MaxPass][TILES][2];
 #pragma unroll
-    for (int bb = 0; bb < BPW; ++bb) {
-        bf16x8 B[TILES][kQ4Parts];  // peel one bf16 part at a time; each residual is exact
+        for (int i = 0; i < kQ4MaxPass; ++i) {
+            const int b = c_lo + 8 * i + v;
 #pragma unroll
-        for (int ct = 0; ct < TILES; ++ct) {
-            const uint4 u0 = s_x[((ct * KB + kb0 + bb) * 2 + 0) * 64 + lane];
-            const uint4 u1 = s_x[((ct * KB + kb0 + bb) * 2 + 1) * 64 + lane];
-            float r[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z),
-                          __uint_as_float(u0.w), __uint_as_float(u1.x), __uint_as_float(u1.y),
-                          __uint_as_float(u1.z), __uint_as_float(u1.w)};
-#pragma unroll
-            for (int p = 0; p < kQ4Parts; ++p) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    B[ct][p][e] = (__bf16)r[e];
-                    r[e] -= (float)B[ct][p][e];
+            for (int ct = 0; ct < TILES; ++ct) {
+                const int seq = 16 * ct + j;
+                if (i < passes && b < b_hi && seq < a.batch) {
+                    const float4* xp = reinterpret_cast<const float4*>(a.x + (size_t)seq * a.c_in + 32 * b + 8 * (lane >> 4));
+                    xr[i][ct][0] = xp[0];
+                    xr[i][ct][1] = xp[1];
+                } else {
+                    xr[i][ct][0] = xr[i][ct][1] = make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
         }
+        // 2. weights and scales of every pass straight to LDS (rows past c_out read the
+        // last row, blocks past the pass read its first block; neither is used)
 #pragma unroll
-        for (int t = 0; t < kQ4ATiles; ++t) {
-            const bf16x8 A = weights_bf16(wv[t][bb]);
-            const f32x4 s4 =
-                *reinterpret_cast<const f32x4*>(&s_sc[kb0 + bb][wr * kQ4ATiles * 16 + 16 * t + 4 * g]);
+        for (int i = 0; i < kQ4MaxPass; ++i) {
+            if (i < passes) {
+                const int p0 = c_lo + 8 * i, pn = min(8, b_hi - p0);
+                char* s_w = smem + i * (kPassW + kPassS);
+                char* s_s = s_w + kPassW;
 #pragma unroll
-            for (int ct = 0; ct < TILES; ++ct) {
-                f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int n = 0; n < RH; ++n) {
+                    const int k = v + kQ4Waves * n;  // copy instruction of this pass
+                    const int e = 64 * k + lane, r = e >> 3, bb = (e & 7) ^ (r & 7);
+                    const int row = min(g * RG + r, a.c_out - 1);
+                    __builtin_amdgcn_global_load_lds(
+                        a.w + (size_t)row * (a.c_in / 2) + (size_t)(p0 + (bb < pn ? bb : 0)) * 16,
+                        (lds_void*)(s_w + 1024 * k), 16, 0, 0);
+                }
 #pragma unroll
-                for (int p = kQ4Parts - 1; p >= 0; --p)  // smallest part first
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B[ct][p], c, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[t][ct][r] = fmaf(s4[r], c[r], acc[t][ct][r]);
+                for (int n = 0; n < RH; ++n) {
+                    const int k = v + kQ4Waves * n;
+                    const int e = 64 * k + lane, r = e >> 3, bb = e & 7;
+                    const int row = min(g * RG + r, a.c_out - 1);
+                    __builtin_amdgcn_global_load_lds(a.scales + (size_t)row * a.nb + p0 + (bb < pn ? bb : 0),
+                                                     (lds_void*)(s_s + 256 * k), 4, 0, 0);
+                }
             }
         }
+        // 3. pass i once its copies have landed, the later passes' still in flight
+#pragma unroll
+        for (int i = 0; i < kQ4MaxPass; ++i) {
+            if (i < passes) {
+                const int later = passes - 1 - i;  // passes issued after this one
+                if (later >= 2) wait_vm<4 * RH>();
+                else if (later == 1) wait_vm<2 * RH>();
+                else wait_vm<0>();
+                __syncthreads();  // every wave's copies of pass i
+                const int b = c_lo + 8 * i + v;
+                if (b < b_hi) {
+                    // A operands: the block's inputs in three exact bf16 parts per column tile
+                    bf16x8 X[TILES][3];
+#pragma unroll
+                    for (int ct = 0; ct < TILES; ++ct) {
+                        const float xv[8] = {xr[i][ct][0].x, xr[i][ct][0].y, xr[i][ct][0].z, xr[i][ct][0].w,
+                                             xr[i][ct][1].x, xr[i][ct][1].y, xr[i][ct][1].z, xr[i][ct][1].w};
+                        split3(xv, X[ct][0], X[ct][1], X[ct][2]);
+                    }
+                    const uint32_t* s_w = reinterpret_cast<const uint32_t*>(smem + i * (kPassW + kPassS));
+                    const float* s_s = reinterpret_cast<const float*>(smem + i * (kPassW + kPassS) + kPassW);
+#pragma unroll
+                    for (int t = 0; t < RT; ++t) {
+                        const int r = 16 * t + j;
+                        const uint32_t wd = s_w[(r * 8 + (v ^ (r & 7))) * 4 + (lane >> 4)];
+                        const float sc = s_s[r * 8 + v] * kQ4Unpack;
+                        const bf16x8 W = unpack_q4(wd);
+#pragma unroll
+                        for (int ct = 0; ct < TILES; ++ct) {
+                            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][2], W, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][1], W, c, 0, 0, 0);
+                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][0], W, c, 0, 0, 0);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[t][ct][e] = fmaf(sc, c[e], acc[t][ct][e]);
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();  // every wave is done with this chunk's LDS
     }
-
-    // Quarter sums: pair slot (wr, wk >> 1); odd quarters write, even ones add and store
-    // back, then every thread adds the two pair sums of its outputs.
-    f32x4* red = reinterpret_cast<f32x4*>(s_x);
-    auto rslot = [&](int pair, int t, int ct) -> f32x4& {
-        return red[(((wr * 2 + pair) * kQ4ATiles + t) * TILES + ct) * 64 + lane];
-    };
     // Pin the last scaled accumulations here, in the MFMAs' basic block: left free, the
     // compiler may sink them past the branches below.
 #pragma unroll
-    for (int t = 0; t < kQ4ATiles; ++t)
+    for (int t = 0; t < RT; ++t)
 #pragma unroll
         for (int ct = 0; ct < TILES; ++ct)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(acc[t][ct][r]));
-    __syncthreads();  // every wave is done with the x slice
-    if (wk & 1) {
+            for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(acc[t][ct][e]));
 #pragma unroll
-        for (int t = 0; t < kQ4ATiles; ++t)
+    for (int t = 0; t < RT; ++t)
 #pragma unroll
-            for (int ct = 0; ct < TILES; ++ct) rslot(wk >> 1, t, ct) = acc[t][ct];
-    }
+        for (int ct = 0; ct < TILES; ++ct) s_red[((v * RT + t) * TILES + ct) * 64 + lane] = acc[t][ct];
     __syncthreads();
-    if (!(wk & 1)) {
+    // Thread unit = one row and four sequences (one lane's f32x4); consecutive threads take
+    // consecutive rows, so each of the four stores is contiguous across threads.
+    const bool single = a.splits == 1;
+    constexpr int kUnits = RG * 4 * TILES;
 #pragma unroll
-        for (int t = 0; t < kQ4ATiles; ++t)
+    for (int k = 0; k < (kUnits + kQ4NT - 1) / kQ4NT; ++k) {
+        const int u = tid + k * kQ4NT;
+        if (u < kUnits) {
+            const int r = u % RG, qq = (u / RG) % 4, ct = u / (RG * 4);
+            const int t = r >> 4, ln = (r & 15) + 16 * qq;
+            f32x4 sum = s_red[(t * TILES + ct) * 64 + ln];
 #pragma unroll
-            for (int ct = 0; ct < TILES; ++ct) {
-                f32x4& r = rslot(wk >> 1, t, ct);
-                r = acc[t][ct] + r;
+            for (int w = 1; w < kQ4Waves; ++w) sum += s_red[((w * RT + t) * TILES + ct) * 64 + ln];
+            const int row = g * RG + r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int seq = 16 * ct + 4 * qq + e;
+                if (seq < a.batch) {
+                    if (single) {
+                        if (row < a.c_out) a.out[(size_t)seq * a.c_out + row] = sum[e];
+                    } else {  // written through to memory (system scope): see below
+                        __hip_atomic_store(&a.part[((size_t)blockIdx.x * a.batch + seq) * RG + r], sum[e],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    }
+                }
             }
+        }
+    }
+    if (single) return;
+    // The row group's last workgroup to finish adds the partials of all of them, in
+    // workgroup order (deterministic), and writes out. The partials are stored and loaded
+    // at system scope, i.e. written through and read past the L2 caches: once a
+    // workgroup's stores are acknowledged (vmcnt 0) they are in memory, where the last
+    // workgroup reads them, so no L2 write-back or invalidation is needed (those cost
+    // more than the whole product on this 8-XCD part).
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const int done = __hip_atomic_fetch_add(&a.arrived[g], 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        s_last = done == a.splits - 1;
+        if (s_last) __hip_atomic_store(&a.arrived[g], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-
-    // Consecutive threads take consecutive rows of one sequence.
-    const float* redf = reinterpret_cast<const float*>(red);
-    constexpr int kPairFloats = kQ4ATiles * TILES * 64 * 4;
+    if (!s_last) return;
+    // Every partial of every output requested before any is added: kQ4RedOut outputs of
+    // up to 16 partials per thread and round (the partials come from memory).
+    const float* p0 = a.part + (size_t)g * a.splits * a.batch * RG;
+    const size_t stride = (size_t)a.batch * RG;
+    const int n = a.batch * RG;
+    constexpr int kQ4RedOut = 4;
+    for (int base = 0; base < n; base += kQ4RedOut * kQ4NT) {
+        float vals[kQ4RedOut][16];
 #pragma unroll
-    for (int i = 0; i < kQ4Rows * 16 * TILES / NT; ++i) {
-        const int e = tid + i * NT;
-        const int row = e % kQ4Rows, col = e / kQ4Rows;
-        const int h = row / (kQ4ATiles * 16), rw = row % (kQ4ATiles * 16);
-        const int t = rw >> 4, rg = (rw >> 2) & 3, r = rw & 3;
-        const int l = (col & 15) + 16 * rg, ct = col >> 4;
-        const int idx = (h * 2 * kPairFloats) + ((t * TILES + ct) * 64 + l) * 4 + r;
-        const float sum = redf[idx] + redf[idx + kPairFloats];
-        if (col < a.batch && grow0 + row < a.c_out) {
-            if (a.splits == 1) a.out[(size_t)col * a.c_out + grow0 + row] = sum;
-            else a.part[((size_t)split * a.batch + col) * a.c_out + grow0 + row] = sum;
+        for (int m = 0; m < kQ4RedOut; ++m) {
+            const int i = base + m * kQ4NT + tid;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                vals[m][k] = (i < n && k < a.splits)
+                                 ? __hip_atomic_load(&p0[(size_t)k * stride + i], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_SYSTEM)
+                                 : 0.f;
+        }
+#pragma unroll
+        for (int m = 0; m < kQ4RedOut; ++m) {
+            const int i = base + m * kQ4NT + tid;
+            float sum = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) sum += vals[m][k];
+            for (int k = 16; k < a.splits; ++k)
+                sum += __hip_atomic_load(&p0[(size_t)k * stride + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            const int seq = i / RG, r = i % RG, row = g * RG + r;
+            if (i < n && row < a.c_out) a.out[(size_t)seq * a.c_out + row] = sum;
         }
     }
 }
 
-// out[col][row] = sum over splits in order of the partials (loads 16 splits at a time).
-__global__ __launch_bounds__(256) void q4_reduce_kernel(Q4Args a) {
-    const size_t n = (size_t)a.batch * a.c_out;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        float sum = 0.f;
-        for (int s0 = 0; s0 < a.splits; s0 += 16) {
-            float v[16];
-#pragma unroll
-            for (int s = 0; s < 16; ++s) v[s] = s0 + s < a.splits ? a.part[(size_t)(s0 + s) * n + i] : 0.f;
-#pragma unroll
-            for (int s = 0; s < 16; ++s) sum += v[s];
-        }
-        a.out[i] = sum;
-    }
-}
-
-// Splits of kQ4KB blocks. Eight blocks keep a workgroup at <= 68 KiB of LDS (two per CU)
-// and give the Wo shapes >= 352 workgroups; sixteen measured slower (fewer, LDS-bound
-// workgroups) despite half the partials.
-int32_t q4_splits(int32_t c_in) { return (c_in / 32 + kQ4KB - 1) / kQ4KB; }
+// Rows of a group in halves of 64: one. 64-row groups need at most 128 VGPRs up to two
+// column tiles, so two 8-wave workgroups share a CU (four waves per SIMD); 128-row groups
+// (two halves) measured slower at one workgroup per CU.
+int q4_rh(int32_t) { return 1; }
 
 }  // namespace
 }  // namespace pkv
@@ -300,9 +382,13 @@ extern "C" {
 
 size_t pkv_q4_matmul_workspace_size(int32_t c_in, int32_t c_out, int32_t batch) {
     if (c_in <= 0 || c_in % 32 || c_out <= 0 || batch <= 0 || batch > pkv::kQ4MaxBatch) return 0;
-    const int32_t splits = pkv::q4_splits(c_in);
-    const size_t bytes = splits > 1 ? (size_t)splits * batch * c_out * sizeof(float) : 0;
-    return bytes > 0 ? bytes : 256;
+    const size_t rg = 64 * (size_t)pkv::q4_rh(batch);
+    const size_t groups = ((size_t)c_out + rg - 1) / rg;
+    // the row groups' arrival counts, then partials of at most kQ4MaxWg workgroups (or
+    // one per row group)
+    const size_t counts = (groups * sizeof(int32_t) + 255) & ~(size_t)255;
+    const size_t wgs = groups > (size_t)pkv::kQ4MaxWg ? groups : (size_t)pkv::kQ4MaxWg;
+    return counts + wgs * batch * rg * sizeof(float);
 }
 
 int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales, const float* x,
@@ -318,35 +404,50 @@ int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales
     if (!w_packed || !scales || !x || !out || !workspace)
         return fail(PKV_ERR_INVALID, "pkv_q4_matmul: null device pointer");
     if ((reinterpret_cast<uintptr_t>(w_packed) & 15) || (reinterpret_cast<uintptr_t>(x) & 15) ||
-        (reinterpret_cast<uintptr_t>(scales) & 3))
-        return fail(PKV_ERR_INVALID, "pkv_q4_matmul: w_packed and x need 16-byte, scales 4-byte alignment");
+        (reinterpret_cast<uintptr_t>(scales) & 3) || (reinterpret_cast<uintptr_t>(workspace) & 15))
+        return fail(PKV_ERR_INVALID, "pkv_q4_matmul: w_packed, x and workspace need 16-byte, "
+                                     "scales 4-byte alignment");
     if (workspace_bytes < pkv_q4_matmul_workspace_size(c_in, c_out, batch))
         return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_q4_matmul_workspace_size()");
+    if ((int64_t)c_out * (c_in / 2) > ((int64_t)1 << 40))
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_q4_matmul: matrix too large");
+    const int tiles = (batch + 15) / 16;
+    const int rh = q4_rh(batch);
+    const void* fn = nullptr;
+    switch (tiles) {
+        case 1: fn = reinterpret_cast<const void*>(&q4_matmul_kernel<1, 1>); break;
+        case 2: fn = reinterpret_cast<const void*>(&q4_matmul_kernel<2, 1>); break;
+        case 3: fn = reinterpret_cast<const void*>(&q4_matmul_kernel<3, 1>); break;
+        default: fn = reinterpret_cast<const void*>(&q4_matmul_kernel<4, 1>); break;
+    }
     Q4Args a{};
     a.w = w_packed;
     a.scales = scales;
     a.x = x;
     a.out = out;
-    a.part = static_cast<float*>(workspace);
     a.c_in = c_in;
     a.c_out = c_out;
     a.batch = batch;
     a.nb = c_in / 32;
-    a.groups = (c_out + kQ4Rows - 1) / kQ4Rows;
-    a.splits = q4_splits(c_in);
-    const int tiles = (batch + 15) / 16;
+    a.groups = (c_out + 64 * rh - 1) / (64 * rh);
+    a.arrived = static_cast<int32_t*>(workspace);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                      (((size_t)a.groups * sizeof(int32_t) + 255) & ~(size_t)255));
+    const int fill = device_fill_workgroups(fn, kQ4NT, 0, kQ4MaxWg);
+    if (fill <= 0) return fail(PKV_ERR_HIP, "pkv_q4_matmul: occupancy query failed");
+    // Splits per row group: as many as keep every workgroup resident in one round.
+    int splits = fill / a.groups;
+    if (splits < 1) splits = 1;
+    if (splits > a.nb) splits = a.nb;
+    a.per = (a.nb + splits - 1) / splits;
+    a.splits = (a.nb + a.per - 1) / a.per;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 grid(a.groups * a.splits), block(kQ4Waves * 64);
+    const dim3 grid(a.groups * a.splits), block(kQ4NT);
     switch (tiles) {
-        case 1: hipLaunchKernelGGL((q4_matmul_kernel<1, kQ4KB>), grid, block, 0, st, a); break;
-        case 2: hipLaunchKernelGGL((q4_matmul_kernel<2, kQ4KB>), grid, block, 0, st, a); break;
-        case 3: hipLaunchKernelGGL((q4_matmul_kernel<3, kQ4KB>), grid, block, 0, st, a); break;
-        default: hipLaunchKernelGGL((q4_matmul_kernel<4, kQ4KB>), grid, block, 0, st, a); break;
-    }
-    if (a.splits > 1) {
-        const size_t n = (size_t)batch * c_out;
-        const int blocks = (int)((n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048);
-        hipLaunchKernelGGL(q4_reduce_kernel, dim3(blocks), dim3(256), 0, st, a);
+        case 1: hipLaunchKernelGGL((q4_matmul_kernel<1, 1>), grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL((q4_matmul_kernel<2, 1>), grid, block, 0, st, a); break;
+        case 3: hipLaunchKernelGGL((q4_matmul_kernel<3, 1>), grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL((q4_matmul_kernel<4, 1>), grid, block, 0, st, a); break;
     }
     return check_launch("pkv_q4_matmul");
 }

@@ -43,10 +43,6 @@
 #include <math.h>
 #include <stdint.h>
 
-#include <map>
-#include <mutex>
-#include <utility>
-
 #include "pkv_internal.h"
 
 namespace pkv {
@@ -1239,33 +1235,9 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
 
 constexpr int kMaxSlots = kStreamMaxSlots;  // workgroups along the keys, at most (merge LDS bound)
 
-struct Occ {
-    std::mutex mu;
-    std::map<std::pair<const void*, int>, int> blocks;  // (kernel, device) -> P
-};
-Occ& occ() {
-    static Occ o;
-    return o;
-}
-
 // Workgroups that fill the device once (all resident together), capped at kMaxSlots.
 int fill_workgroups(const void* fn, int threads, size_t lds) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return -1;
-    Occ& o = occ();
-    std::lock_guard<std::mutex> lk(o.mu);
-    auto key = std::make_pair(fn, dev);
-    auto it = o.blocks.find(key);
-    if (it != o.blocks.end()) return it->second;
-    int cus = 0, per_cu = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return -1;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess)
-        return -1;
-    int p = cus * (per_cu > 0 ? per_cu : 1);
-    if (p > kMaxSlots) p = kMaxSlots;
-    o.blocks.emplace(key, p);
-    return p;
+    return device_fill_workgroups(fn, threads, lds, kMaxSlots);
 }
 
 template <int D, typename KV, int R, int WPH, int ADDR>

@@ -346,14 +346,15 @@ def q4_matmul(w_packed, scales, x, out, c_in: int, c_out: int, batch: int, works
     """Wo projection (q4_matmul_vec, moe_kernels.mojo:59-163) for `batch` vectors: out
     [batch][c_out] = x [batch][c_in] times the Q4_0 matrix (w_packed [c_out][c_in/2] uint8,
     scales [c_out][c_in/32] fp32); all device arrays, w_packed and x 16-byte aligned (device
-    allocations are). Returns the workspace used."""
+    allocations are). A workspace passed in must have been zero-filled before its first use
+    (each call leaves it so). Returns the workspace used."""
     L = lib.load()
     need = L.pkv_q4_matmul_workspace_size(c_in, c_out, batch)
     if need == 0:
         raise lib.PkvError(lib.PKV_ERR_INVALID, "pkv_q4_matmul_workspace_size", "invalid sizes")
     ws = workspace
     if ws is None or ws.nbytes < need:
-        ws = hip.DeviceArray((need,), np.uint8)
+        ws = hip.DeviceArray((need,), np.uint8, zero=True)  # zero-filled before first use
     lib.call("pkv_q4_matmul", stream.handle if stream else None, _ptr(w_packed), _ptr(scales),
              _ptr(x), c_in, c_out, batch, _ptr(out), ws.ptr, ws.nbytes)
     return ws

@@ -122,7 +122,9 @@ def test_q4_matmul_rejections_before_launch():
     assert L.pkv_q4_matmul(None, 16, 4, 16, 4096, 8, 8, 16, 16, 16) == lib.PKV_ERR_WORKSPACE
     assert L.pkv_q4_matmul(None, 16, 4, 8, 4096, 8, 8, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID  # x alignment
     assert L.pkv_q4_matmul(None, 4, 4, 16, 4096, 8, 8, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID  # w alignment
-    assert L.pkv_q4_matmul_workspace_size(4096, 2816, 32) == 16 * 32 * 2816 * 4
+    # 22 row groups' arrival counts (one 256-byte line), then partials of up to 512
+    # workgroups of 128 rows
+    assert L.pkv_q4_matmul_workspace_size(4096, 2816, 32) == 256 + 512 * 32 * 128 * 4
 
 
 def test_lsa_cache_rejections_before_launch():

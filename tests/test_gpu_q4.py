@@ -54,8 +54,11 @@ def test_reference_patterns(gpu):
     (8192, 2816, 32),  # global layers' Wo (16 q heads x 512)
     (4096, 2816, 5),   # a verify-sized batch
     (8192, 1000, 64),  # the largest batch, partial row tile
-    (96, 17, 3),       # a single split
-], ids=["wo-sliding", "wo-global", "b5", "b64", "small"])
+    (96, 17, 3),       # a single workgroup per row group
+    (2848, 300, 40),   # three column tiles, 89 blocks: row groups split over workgroups
+    (4128, 129, 17),   # two column tiles, a 129-row matrix (one row in the last group)
+    (32, 5, 1),        # one block, one sequence
+], ids=["wo-sliding", "wo-global", "b5", "b64", "small", "b40-odd", "b17-odd", "tiny"])
 def test_wo_shapes_within_dot_bound(gpu, c_in, c_out, batch):
     print(f"[q4] c_in={c_in} c_out={c_out} batch={batch}", flush=True)
     rng = np.random.default_rng(c_in + c_out + batch)
@@ -72,3 +75,23 @@ def test_wo_shapes_within_dot_bound(gpu, c_in, c_out, batch):
         err = np.abs(got[s].astype(np.float64) - exact)
         assert np.all(err <= bound), f"sequence {s}: max err / bound {np.max(err / bound)}"
 
+
+
+def test_workspace_reused_across_calls_and_shapes(gpu):
+    """One zero-filled workspace serves a sequence of calls of different shapes (the row
+    groups' arrival counts return to zero after each call): every output equals the one a
+    fresh workspace gives, bit for bit."""
+    print("[q4] workspace reuse", flush=True)
+    rng = np.random.default_rng(7)
+    shapes = [(8192, 2816, 32), (4096, 2816, 32), (2848, 300, 40), (8192, 2816, 32), (96, 17, 3)]
+    need = max(pkv.lib.load().pkv_q4_matmul_workspace_size(ci, co, b) for ci, co, b in shapes)
+    ws = hip.DeviceArray((need,), np.uint8, zero=True)
+    for c_in, c_out, batch in shapes:
+        packed = rng.integers(0, 256, (c_out, c_in // 2), dtype=np.uint8)
+        scales = (rng.random((c_out, c_in // 32)) * 0.01 + 0.001).astype(np.float32)
+        x = rng.standard_normal((batch, c_in)).astype(np.float32)
+        dw, ds, dx = (hip.DeviceArray.from_numpy(a) for a in (packed, scales, x))
+        reused = hip.DeviceArray((batch, c_out), np.float32)
+        pkv.q4_matmul(dw, ds, dx, reused, c_in, c_out, batch, workspace=ws)
+        fresh = _run(packed, scales, x)
+        assert np.array_equal(reused.numpy(), fresh), f"shape {(c_in, c_out, batch)}"
