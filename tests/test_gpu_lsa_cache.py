@@ -200,3 +200,21 @@ def test_rollback_matches_oracle(gpu):
     np.testing.assert_array_equal(cache.closed_blocks.numpy(), [s.closed_blocks[0] for s in states])
     np.testing.assert_array_equal(cache.total_tokens.numpy(), [s.total_tokens[0] for s in states])
     np.testing.assert_array_equal(cache.sizes.numpy(), np.stack([s.sizes for s in states]))
+
+
+def test_expand_reference_known_answer(gpu):
+    """test_lsa_reference.mojo:130-184 through pkv_lsa_expand: position-mode buckets of 16
+    tokens (bucket b = tokens 16b .. 16b + 15), picked [0, 2], position 63, top_k 10, sinks
+    2, window 4 -> [2 .. 11, 60, 61, 62, 63, 0, 1]."""
+    print("[lsa-cache] reference known answer", flush=True)
+    cache = LSABucketCache(1, 512)
+    sizes = np.zeros((1, cache.max_buckets), np.int32)
+    members = np.zeros((1, cache.max_buckets, CAP), np.int32)
+    for b in range(4):
+        sizes[0, b] = 16
+        members[0, b, :16] = np.arange(16 * b, 16 * b + 16)
+    _upload(cache, sizes, members)
+    keys, off, status = _expand(cache, np.array([0]), np.array([[0, 2]]), np.array([2]),
+                                np.array([63]), 10, 2, 4)
+    assert keys.tolist() == list(range(2, 12)) + [60, 61, 62, 63, 0, 1]
+    assert off.tolist() == [0, 16] and status.tolist() == [lib.PKV_SEQ_OK]

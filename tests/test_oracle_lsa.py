@@ -97,3 +97,24 @@ def test_expand_buckets_host_matches_oracle_and_its_definition(seed):
     flat = [int(t) for b in picked for t in members[b, : sizes[b]] if sinks <= t < ws]
     np.testing.assert_array_equal(bucket_part, flat[:n_b])
     assert n_b == min(top_k, len(flat))
+
+
+def _reference_position_buckets():
+    """The buckets test_lsa_reference.mojo:130-148 builds in "position" mode: 64 keys,
+    bucket size 16 -> bucket b holds tokens 16b .. 16b + 15 in order (bucket cap 32)."""
+    sizes = np.full(4, 16, np.int32)
+    members = np.zeros((4, 32), np.int32)
+    for b in range(4):
+        members[b, :16] = np.arange(16 * b, 16 * b + 16)
+    return sizes, members
+
+
+def test_expand_buckets_reference_known_answer():
+    """test_lsa_reference.mojo:150-184: picked [0, 2], position 63, top_k 10, sinks 2,
+    window 4 -> the first ten members of bucket 0 past the sinks, the window, the sinks:
+    [2 .. 11, 60, 61, 62, 63, 0, 1]."""
+    sizes, members = _reference_position_buckets()
+    want = list(range(2, 12)) + [60, 61, 62, 63, 0, 1]
+    got = O.lsa_expand_buckets([0, 2], sizes, members, 63, 10, 2, 4)
+    assert got.tolist() == want
+    assert pkv.lsa_expand_buckets([0, 2], sizes, members, 63, 10, 2, 4).tolist() == want
