@@ -189,8 +189,11 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
  * after this call's append writes it.
  * When one launch of the stream kernel's vector path covers the call (paged pools,
  * head_dim 256 or 512, G * q_len <= 8 on the vector kernel, every kv head in one
- * workgroup), that launch also copies the appended rows into the pool and reads them from
- * k_new / v_new, saving the scatter launch; otherwise the append runs whole first.
+ * workgroup, batch <= 1024), that launch also computes the block allocation from the
+ * state as it stands before the call, copies the appended rows into the pool and reads
+ * them from k_new / v_new; the merge launch after it writes the new table entries,
+ * table_lens, free_count and status. No allocation or scatter launch is made, and no
+ * state word is read and written in one launch. Otherwise the append runs whole first.
  * Arguments as in pkv_append and pkv_attend. Every check of the attention's arguments
  * (including an unsupported geometry) runs before the append launches anything, so a
  * call that returns an error has changed no table, free list or pool. No reference

@@ -724,6 +724,7 @@ int32_t attend_impl(void* stream, const pkv_params* p, const float* q, const voi
     const int G = p->num_heads / p->num_kv_heads;
     const int rows = G * q_len;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (nr && !use_stream) return fail(PKV_ERR_UNSUPPORTED, "appended rows need the stream path");
     if (use_stream) {
         rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, pos, pos_scalar,
                            ring_base, q_len, q_lens, batch, max_pos, nullptr, nullptr, 0, out,
@@ -902,19 +903,38 @@ int32_t pkv_append_attend(void* stream, const pkv_params* p, void* k_pool, void*
     if (workspace_bytes < pkv_workspace_size(p, batch, q_len, max_pos))
         return fail(PKV_ERR_WORKSPACE, "workspace smaller than pkv_workspace_size()");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // The stream kernel takes the appended rows itself when one vector-kernel launch covers
-    // the call; otherwise the append copies them first.
-    const bool fuse = stream_takes_new_rows(p, q_len) &&
+    // When one vector-kernel launch covers the call, the stream kernel does the append
+    // itself (allocation, row copies) and its merge launch writes the state; otherwise the
+    // append runs whole first.
+    const bool fuse = stream_takes_new_rows(p, q_len, batch) &&
                       workspace_bytes >= stream_layout(p, batch, q_len).total;
+    if (fuse) {
+        rc = append_validate(p, k_pool, v_pool, block_tables, table_stride, table_lens, free_list,
+                             free_count, pos, tok_off, max_new, k_new, v_new, total_rows, batch,
+                             status);
+        if (rc != PKV_OK) return rc;
+        NewRows nr{};
+        nr.k_new = static_cast<const char*>(k_new);
+        nr.v_new = static_cast<const char*>(v_new);
+        nr.tok_off = tok_off;
+        nr.k_dst = static_cast<char*>(k_pool);
+        nr.v_dst = static_cast<char*>(v_pool);
+        nr.tables = block_tables;
+        nr.table_lens = table_lens;
+        nr.free_list = free_list;
+        nr.free_count = free_count;
+        nr.status = status;
+        nr.max_new = max_new;
+        nr.total_rows = total_rows;
+        return attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0, 0,
+                           q_len, nullptr, batch, max_pos, out, workspace, workspace_bytes, &nr);
+    }
     rc = append_launch(st, p, k_pool, v_pool, block_tables, table_stride, table_lens, free_list,
                        free_count, pos, tok_off, max_new, k_new, v_new, total_rows, batch, status,
-                       !fuse);
+                       true);
     if (rc != PKV_OK) return rc;
-    NewRows nr{static_cast<const char*>(k_new), static_cast<const char*>(v_new), tok_off,
-               static_cast<char*>(k_pool), static_cast<char*>(v_pool), status, table_lens};
     return attend_impl(stream, p, q, k_pool, v_pool, block_tables, table_stride, pos, 0, 0, q_len,
-                       nullptr, batch, max_pos, out, workspace, workspace_bytes,
-                       fuse ? &nr : nullptr);
+                       nullptr, batch, max_pos, out, workspace, workspace_bytes);
 }
 
 int32_t pkv_verify(void* stream, const pkv_params* p, const float* q, const void* k_pool,

@@ -44,7 +44,10 @@ struct AttendLayout {
 AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos);
 
 // Stream-K attention (pkv_stream.hip): workspace layout and entry.
-//   plan   int32 [batch + 2]       per, then the key prefix of every sequence
+//   plan   int32 [4 batch + 4]     per, the key prefix of every sequence [batch + 1], then
+//                                  for a fused append the allocation plan: the free count
+//                                  as read, table lengths [batch], prefix of the blocks
+//                                  needed [batch + 1], status before the pops [batch]
 //   part_ml                        double (m, l) per (slot, row)
 //   part_o                         double [head_dim] per (slot, row)
 // slots = min(nwg_cap, kStreamMaxSlots) + batch, rows = num_heads * q_len: piece (w, s) of
@@ -61,22 +64,39 @@ StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len,
 // True when the stream kernel covers this geometry: head_dim 256 or 512 with
 // G = num_heads / num_kv_heads <= 8 (any number of queries: launched in groups).
 bool stream_eligible(const pkv_params* p, int32_t G);
-// The appended rows of a fused append + attention (pkv_append_attend). The attention
-// launch copies row r of sequence s (tok_off[s] <= r < tok_off[s + 1], position
-// pos[s] + r - tok_off[s]) into the pool, with scatter_kernel's checks, and reads those
-// positions from k_new / v_new instead of the pool. k_new == NULL: no appended rows.
+// The appended rows of a fused append + attention (pkv_append_attend), with the block
+// manager's state. The attention launch computes the block allocation from the state as
+// it stands before the call (every workgroup the same result), copies row r of sequence s
+// (tok_off[s] <= r < tok_off[s + 1], position pos[s] + r - tok_off[s]) into the pool
+// with scatter_kernel's checks, and reads those positions from k_new / v_new instead of
+// the pool; the merge launch after it writes the new table entries, table_lens,
+// free_count and status. So no word of the state is written in the launch that reads it.
+// k_new == NULL: no appended rows.
 struct NewRows {
     const char* k_new;
     const char* v_new;
     const int32_t* tok_off;     // [batch + 1]
     char* k_dst;                // the pools, written
     char* v_dst;
-    const int32_t* status;      // per sequence, from the block allocation (read only)
-    const int32_t* table_lens;  // after the allocation (read only)
+    int32_t* tables;            // block tables [batch][table_stride]
+    int32_t* table_lens;
+    const int32_t* free_list;
+    int32_t* free_count;
+    int32_t* status;
+    int32_t max_new;
+    int32_t total_rows;
 };
-// True when stream_attend takes the appended rows itself for q_len queries: paged pools
-// and one launch on the vector kernel.
-bool stream_takes_new_rows(const pkv_params* p, int32_t q_len);
+// Largest batch whose allocation plan the fused launch keeps in LDS.
+constexpr int kFuseMaxBatch = 1024;
+// True when stream_attend takes the appended rows itself for q_len queries: paged pools,
+// one launch on the vector kernel and batch <= kFuseMaxBatch.
+bool stream_takes_new_rows(const pkv_params* p, int32_t q_len, int32_t batch);
+// Checks the arguments of a paged or ring append (pkv_state.hip); PKV_OK or an error code.
+int32_t append_validate(const pkv_params* p, void* k_pool, void* v_pool, int32_t* block_tables,
+                        int32_t table_stride, int32_t* table_lens, int32_t* free_list,
+                        int32_t* free_count, const int32_t* pos, const int32_t* tok_off,
+                        int32_t max_new, const void* k_new, const void* v_new,
+                        int32_t total_rows, int32_t batch, int32_t* status);
 // Validates a paged or ring append and launches it (pkv_state.hip): the block allocation,
 // then, with scatter, the row copies.
 int32_t append_launch(hipStream_t st, const pkv_params* p, void* k_pool, void* v_pool,
@@ -85,6 +105,49 @@ int32_t append_launch(hipStream_t st, const pkv_params* p, void* k_pool, void* v
                       const int32_t* tok_off, int32_t max_new, const void* k_new,
                       const void* v_new, int32_t total_rows, int32_t batch, int32_t* status,
                       bool scatter);
+
+// ---- block allocation of an append (BlockManager, model_speculative_moe_batched.mojo:
+// 789-807): sequence s, in index order, pops the blocks it lacks from the top of the free
+// list, free_list[fc - 1 - pref[s] - j] for its j-th new block (pref = exclusive prefix
+// of the needs); one that runs the list dry keeps what it popped (OUT_OF_BLOCKS).
+// Shared by alloc_kernel and the fused append + attention launch.
+
+// Blocks an append of rows [r0, r1) of the new-row arrays at position p needs beyond the
+// len its table holds (>= 0), or a negative PKV_SEQ_* code.
+__device__ inline int append_blocks_needed(int p, int r0, int r1, int max_new,
+                                           int total_rows, int bs, int table_stride,
+                                           int len) {
+    const int n = r1 - r0;
+    if (p < 0 || n <= 0) return 0;
+    if (n > max_new || r0 < 0 || r1 > total_rows) return PKV_SEQ_BAD_ARGS;
+    const long long last_blk = ((long long)p + n - 1) / bs;
+    if (last_blk >= table_stride) return PKV_SEQ_TABLE_FULL;
+    if (len < 0 || len > table_stride) return PKV_SEQ_BAD_BLOCK;
+    const long long need = last_blk + 1 - len;
+    return need > 0 ? (int)need : 0;
+}
+// Blocks granted to a sequence that needs `need` and whose pops start pref entries below
+// the top of a free list of fc entries.
+__device__ inline int append_granted(int need, int fc, int pref) {
+    const int avail = fc - pref;
+    return need == 0 || avail <= 0 ? 0 : (avail < need ? avail : need);
+}
+// Status after the pops (before the check of the touched table entries): code0 is
+// PKV_SEQ_OK or the code append_blocks_needed returned; fc_bad: a free count outside
+// [0, num_blocks], read as an empty list.
+__device__ inline int append_pop_status(int code0, int need, int granted, bool fc_bad) {
+    if (granted < need) return fc_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_OUT_OF_BLOCKS;
+    return code0;
+}
+// Table entry of block index blk after the pops: held entries from the table, new ones
+// from the free list (where the allocation takes them), -1 past the granted blocks.
+__device__ inline int append_block_entry(const int32_t* table, const int32_t* free_list,
+                                         int len, int granted, int fc, int pref, int blk) {
+    if (blk < 0) return -1;
+    if (blk < len) return table[blk];
+    if (blk < len + granted) return free_list[fc - 1 - pref - (blk - len)];
+    return -1;
+}
 
 // pos == NULL: one sequence at pos_scalar; in ring mode its ring starts at row
 // ring_base (otherwise ring slot block_tables[s * table_stride] starts at row

@@ -115,16 +115,8 @@ __device__ inline int ring_append_status(const AppendArgs& a, int s) {
 
 // Blocks sequence s needs (>= 0), or a negative PKV_SEQ_* code.
 __device__ inline int append_need(const AppendArgs& a, int s, int len) {
-    const int p = a.pos[s];
-    const int r0 = a.tok_off[s], r1 = a.tok_off[s + 1];
-    const int n = r1 - r0;
-    if (p < 0 || n <= 0) return 0;
-    if (n > a.max_new || r0 < 0 || r1 > a.total_rows) return PKV_SEQ_BAD_ARGS;
-    const long long last_blk = ((long long)p + n - 1) / a.bs;
-    if (last_blk >= a.table_stride) return PKV_SEQ_TABLE_FULL;
-    if (len < 0 || len > a.table_stride) return PKV_SEQ_BAD_BLOCK;
-    const long long need = last_blk + 1 - len;
-    return need > 0 ? (int)need : 0;
+    return append_blocks_needed(a.pos[s], a.tok_off[s], a.tok_off[s + 1], a.max_new,
+                                a.total_rows, a.bs, a.table_stride, len);
 }
 
 // One workgroup. Sequence s (index order) takes the free-list entries
@@ -162,21 +154,19 @@ __global__ __launch_bounds__(kNT) void alloc_kernel(AppendArgs a) {
     }
     for (int s = tid; s < a.batch; s += kNT) {
         const int need = s_need[s];
-        int code = s_code[s];
-        const int avail = fc - s_pref[s];
-        const int granted = need == 0 || avail <= 0 ? 0 : (avail < need ? avail : need);
+        const int granted = append_granted(need, fc, s_pref[s]);
         if (granted > 0) a.table_lens[s] = s_len[s] + granted;
-        if (granted < need) code = fc_bad ? PKV_SEQ_BAD_BLOCK : PKV_SEQ_OUT_OF_BLOCKS;
+        int code = append_pop_status(s_code[s], need, granted, fc_bad);
         const int p = a.pos[s];
         const int n = a.tok_off[s + 1] - a.tok_off[s];
         if (code == PKV_SEQ_OK && p >= 0 && n > 0) {
             // Every block the rows land in: held entries from the table, new ones from the
             // free list (the entries the loop above writes, read at their source).
             const int32_t* table = a.tables + (size_t)s * a.table_stride;
-            const int len = s_len[s];
             const int b1 = (int)(((long long)p + n - 1) / a.bs);
             for (int blk = p / a.bs; blk <= b1; ++blk) {
-                const int e = blk < len ? table[blk] : a.free_list[fc - 1 - s_pref[s] - (blk - len)];
+                const int e = append_block_entry(table, a.free_list, s_len[s], granted, fc,
+                                                 s_pref[s], blk);
                 if (e < 0 || e >= a.num_blocks) {
                     code = PKV_SEQ_BAD_BLOCK;
                     break;
@@ -591,12 +581,11 @@ __global__ __launch_bounds__(kNT) void rollback_kernel(RollbackArgs a) {
 
 }  // namespace
 
-int32_t append_launch(hipStream_t st, const pkv_params* p, void* k_pool, void* v_pool,
-                      int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
-                      int32_t* free_list, int32_t* free_count, const int32_t* pos,
-                      const int32_t* tok_off, int32_t max_new, const void* k_new,
-                      const void* v_new, int32_t total_rows, int32_t batch, int32_t* status,
-                      bool scatter) {
+int32_t append_validate(const pkv_params* p, void* k_pool, void* v_pool, int32_t* block_tables,
+                        int32_t table_stride, int32_t* table_lens, int32_t* free_list,
+                        int32_t* free_count, const int32_t* pos, const int32_t* tok_off,
+                        int32_t max_new, const void* k_new, const void* v_new,
+                        int32_t total_rows, int32_t batch, int32_t* status) {
     int32_t rc = validate_params(p);
     if (rc != PKV_OK) return rc;
     if (batch <= 0 || max_new <= 0 || table_stride <= 0 || total_rows <= 0)
@@ -607,6 +596,20 @@ int32_t append_launch(hipStream_t st, const pkv_params* p, void* k_pool, void* v
     if (!k_pool || !v_pool || !block_tables || !pos || !tok_off || !k_new || !v_new ||
         !status || (!ring && (!table_lens || !free_list || !free_count)))
         return fail(PKV_ERR_INVALID, "null device pointer");
+    return PKV_OK;
+}
+
+int32_t append_launch(hipStream_t st, const pkv_params* p, void* k_pool, void* v_pool,
+                      int32_t* block_tables, int32_t table_stride, int32_t* table_lens,
+                      int32_t* free_list, int32_t* free_count, const int32_t* pos,
+                      const int32_t* tok_off, int32_t max_new, const void* k_new,
+                      const void* v_new, int32_t total_rows, int32_t batch, int32_t* status,
+                      bool scatter) {
+    const int32_t rc = append_validate(p, k_pool, v_pool, block_tables, table_stride, table_lens,
+                                       free_list, free_count, pos, tok_off, max_new, k_new,
+                                       v_new, total_rows, batch, status);
+    if (rc != PKV_OK) return rc;
+    const bool ring = p->ring_size > 0;  // ring pools use no block-manager state
     AppendArgs a{};
     a.k_pool = static_cast<char*>(k_pool);
     a.v_pool = static_cast<char*>(v_pool);

@@ -39,6 +39,12 @@
 // bf16 pools accumulate in fp32.
 // fp32 pools with 5..8 query rows per KV head (verify) run stream_mfma_kernel instead:
 // the same plan, pieces and partials, with QK^T and PV on the fp64 4x4x4 MFMA.
+//
+// Fused append (pkv_append_attend, vector kernel): every workgroup computes the block
+// allocation of the call from the state as it stands (a prefix over the batch in LDS),
+// copies its share of the appended rows into the pool and takes the new positions from
+// k_new / v_new; the merge launch writes the new table entries, lengths, free count and
+// status. The whole decode step of a layer is these two launches.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -356,6 +362,39 @@ __device__ inline size_t out_row(const StreamArgs& a, int s, int g, int r) {
     return ((size_t)s * a.q_len + j) * a.Hq + h;
 }
 
+// Fused append: the launch computes the block allocation itself from the state as it
+// stands before the call. Its plan, in LDS and (from workgroup (0, 0)) in the workspace
+// after the key plan, holds [0] the free count as read, [1, 1 + B) the table lengths,
+// [1 + B, 2 + 2B) the exclusive prefix of the blocks each sequence needs (total last),
+// [2 + 2B, 2 + 3B) the status before the pops.
+__device__ inline int alloc_plan_ints(int batch) { return 3 * batch + 2; }
+__device__ inline bool fused_append(const StreamArgs& a) { return a.nr.k_new && a.j0 == 0; }
+
+struct SeqAlloc {
+    int len;      // blocks held before the call
+    int granted;  // blocks popped for it
+    int fc;       // free count (0 if the count read lies outside [0, num_blocks])
+    int pref;     // its first pop: free_list[fc - 1 - pref]
+    int code;     // status after the pops
+};
+__device__ inline SeqAlloc seq_alloc(const int* al, int batch, int num_blocks, int s) {
+    const int fc_raw = al[0];
+    const bool fc_bad = fc_raw < 0 || fc_raw > num_blocks;
+    SeqAlloc r;
+    r.fc = fc_bad ? 0 : fc_raw;
+    r.len = al[1 + s];
+    r.pref = al[1 + batch + s];
+    const int need = al[2 + batch + s] - r.pref;
+    r.granted = append_granted(need, r.fc, r.pref);
+    r.code = append_pop_status(al[2 + 2 * batch + s], need, r.granted, fc_bad);
+    return r;
+}
+// Whether the rows of a sequence with this status are copied (as scatter_kernel): OK, or
+// BAD_BLOCK where each row is written only if its table entry lies in the pool.
+__device__ inline bool new_rows_written(int code) {
+    return code == PKV_SEQ_OK || code == PKV_SEQ_BAD_BLOCK;
+}
+
 // Exclusive scan of the key counts in s_pre[0..batch) (in place, one wave), total in
 // s_pre[batch].
 __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
@@ -380,8 +419,9 @@ __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
 // (inactive: zeros), -2 (contract violation: NaN rows), -3 (no query of it in this
 // launch). Workgroup (0, 0) also writes the merge plan and fills the rows of inactive and
 // invalid sequences. Returns `per`, the keys of one workgroup.
+// With a fused append, s_al (alloc_plan_ints(batch) ints) receives the allocation plan.
 template <int D, int ADDR>
-__device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo) {
+__device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo, int* s_al) {
     constexpr bool RING = ADDR == kAddrRing;
     constexpr bool SPARSE = ADDR == kAddrSparse;
     const int tid = threadIdx.x;
@@ -390,6 +430,7 @@ __device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo) {
     const int nthr = blockDim.x;
     const int w = blockIdx.y;
     const int B = a.batch;
+    const bool fused = fused_append(a);
     for (int i = tid; i < B; i += nthr) {
         int n = 0, lo = -1;
         if constexpr (SPARSE) {  // the list's indices; an empty list gives zeros
@@ -432,9 +473,22 @@ __device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo) {
         }
         s_pre[i] = n;
         s_lo[i] = lo;
+        if (ADDR == kAddrPaged && fused) {
+            const int len = a.nr.table_lens[i];
+            const int need = append_blocks_needed(p0, a.nr.tok_off[i], a.nr.tok_off[i + 1],
+                                                  a.nr.max_new, a.nr.total_rows,
+                                                  1 << a.bs_shift, a.table_stride, len);
+            s_al[1 + i] = len;
+            s_al[1 + B + i] = need > 0 ? need : 0;
+            s_al[2 + 2 * B + i] = need < 0 ? need : PKV_SEQ_OK;
+        }
     }
+    if (ADDR == kAddrPaged && fused && tid == 0) s_al[0] = *a.nr.free_count;
     __syncthreads();
-    if (wave == 0) wave_scan_counts(s_pre, B, lane);
+    if (wave == 0) {
+        wave_scan_counts(s_pre, B, lane);
+        if (ADDR == kAddrPaged && fused) wave_scan_counts(s_al + 1 + B, B, lane);
+    }
     __syncthreads();
 
     const int total = ufirst(s_pre[B]);
@@ -443,6 +497,8 @@ __device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo) {
         // Plan for the merge launch; inactive sequences get zeros, contract violations NaN.
         if (tid == 0) a.plan[0] = per;
         for (int i = tid; i <= B; i += nthr) a.plan[1 + i] = s_pre[i];
+        if (ADDR == kAddrPaged && fused)  // for the state writes of the merge launch
+            for (int i = tid; i < alloc_plan_ints(B); i += nthr) a.plan[B + 2 + i] = s_al[i];
         for (int s = 0; s < B; ++s) {
             const int lo = s_lo[s];
             if (lo >= 0 || lo == -3) continue;
@@ -459,12 +515,12 @@ __device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo) {
 
 // Fused append: the appended rows (NewRows) of sequences w, w + nwg, ... go into the pool
 // from workgroup w, the first wave of each kv head copying that head's slice, with the
-// checks of scatter_kernel (pkv_state.hip): a sequence is copied when the block
-// allocation gave it OK or BAD_BLOCK, and a row whose block is not held or whose table
-// entry lies outside the pool is skipped. Status, table lengths and table entries are
-// final before this launch (the allocation is its own launch) and are only read here.
+// checks of scatter_kernel (pkv_state.hip): a sequence is copied when its allocation
+// gives OK or BAD_BLOCK, and a row whose block is neither held nor granted, or whose
+// table entry lies outside the pool, is skipped. The block of a row comes from the plan
+// (held: the table, granted: the free list), so this launch reads no state it writes.
 template <int D, typename KV, int WPH>
-__device__ inline void copy_new_rows(const StreamArgs& a, int wave, int lane) {
+__device__ inline void copy_new_rows(const StreamArgs& a, const int* s_al, int wave, int lane) {
     constexpr int kElt = SKV<KV>::kElt;
     constexpr int kVec = D * kElt / 16;  // 16-byte vectors per head slice
     const int g = wave / WPH;
@@ -476,15 +532,15 @@ __device__ inline void copy_new_rows(const StreamArgs& a, int wave, int lane) {
         const int p0 = a.pos[s];
         const int r0 = a.nr.tok_off[s];
         const int n = a.nr.tok_off[s + 1] - r0;
-        const int st = a.nr.status[s];
-        if ((st != PKV_SEQ_OK && st != PKV_SEQ_BAD_BLOCK) || p0 < 0 || n <= 0) continue;
+        const SeqAlloc al = seq_alloc(s_al, a.batch, a.num_blocks, s);
+        if (!new_rows_written(al.code) || p0 < 0 || n <= 0) continue;
+        if (al.len > a.table_stride) continue;  // a length outside the table: BAD_BLOCK
         const int32_t* table = a.tables + (size_t)s * a.table_stride;
-        const int held = a.nr.table_lens[s];
-        if (held > a.table_stride) continue;  // a length outside the table: BAD_BLOCK
         for (int b = 0; b < n; ++b) {
             const int p = p0 + b;
             const int blk = p >> a.bs_shift;
-            const int phys = blk < held ? table[blk] : -1;
+            const int phys = append_block_entry(table, a.nr.free_list, al.len, al.granted,
+                                                al.fc, al.pref, blk);
             if (phys < 0 || phys >= a.num_blocks) continue;
             const size_t dst = (((size_t)phys << a.bs_shift) | (size_t)(p & bs_mask)) * row_bytes + head_off;
             const size_t src = ((size_t)r0 + b) * row_bytes + head_off;
@@ -522,15 +578,18 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     extern __shared__ int smem[];
     int* s_pre = smem;                  // [batch + 1]
     int* s_lo = smem + a.batch + 1;     // [batch]: window start, -1 inactive, -2 bad
+    int* s_al = smem + 2 * a.batch + 1; // fused append: the allocation plan
 
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
     const int wave = ufirst(tid / kSW);
     const int w = blockIdx.y;
     const int B = a.batch;
+    constexpr bool PAGED = ADDR == kAddrPaged;
 
-    const int per = stream_setup<D, ADDR>(a, s_pre, s_lo);
-    if (ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0) copy_new_rows<D, KV, WPH>(a, wave, lane);
+    const int per = stream_setup<D, ADDR>(a, s_pre, s_lo, s_al);
+    const bool fused = PAGED && fused_append(a);
+    if (fused) copy_new_rows<D, KV, WPH>(a, s_al, wave, lane);
     const int total = ufirst(s_pre[B]);
     const int k0 = w * per;
     if (k0 >= total) return;
@@ -616,17 +675,23 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         int pgbase = -kSW;  // page index held by lane 0 of vpg
         int vpg = 0;
         bool bad = false;
-        // Fused append: positions [pn_lo, pn_hi) come from k_new / v_new (row r0 + t - pos).
+        // Fused append: positions [pn_lo, pn_hi) come from k_new / v_new (row r0 + t - pos);
+        // table indices [g_lo, g_hi) are the blocks granted in this call, whose entries the
+        // merge launch writes: their ids come from the free list (g_top - index).
         int pn_lo = INT32_MAX, pn_hi = INT32_MIN, nr0 = 0;
-        if (ADDR == kAddrPaged && a.nr.k_new) {
+        int g_lo = INT32_MAX, g_hi = INT32_MIN, g_top = 0;
+        if (fused) {
             const int r0 = ufirst(a.nr.tok_off[s]);
             const int n = ufirst(a.nr.tok_off[s + 1]) - r0;
-            const int st = ufirst(a.nr.status[s]);
-            if ((st == PKV_SEQ_OK || st == PKV_SEQ_BAD_BLOCK) && pos0 >= 0 && n > 0) {
+            const SeqAlloc al = seq_alloc(s_al, B, a.num_blocks, s);
+            if (new_rows_written(ufirst(al.code)) && pos0 >= 0 && n > 0) {
                 pn_lo = pos0;
                 pn_hi = pos0 + n;
                 nr0 = r0;
             }
+            g_lo = ufirst(al.len);
+            g_hi = g_lo + ufirst(al.granted);
+            g_top = ufirst(al.fc) - 1 - ufirst(al.pref) + g_lo;
         }
 
         for (int t = ta; t < tb; t += U) {
@@ -647,7 +712,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
                 pgbase = t >> a.bs_shift;
                 int b = 0;
                 if (pgbase + lane <= last_page) {
-                    b = trow[pgbase + lane];
+                    const int pg = pgbase + lane;
+                    b = (pg >= g_lo && pg < g_hi) ? a.nr.free_list[g_top - pg] : trow[pg];
                     if (b < 0 || b >= a.num_blocks) {
                         bad = true;
                         b = 0;
@@ -829,7 +895,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int w = blockIdx.y;
     const int B = a.batch;
 
-    const int per = stream_setup<D, ADDR>(a, s_pre, s_lo);
+    const int per = stream_setup<D, ADDR>(a, s_pre, s_lo, nullptr);  // never a fused append
     const int total = ufirst(s_pre[B]);
     const int k0 = w * per;
     if (k0 >= total) return;
@@ -1129,6 +1195,45 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
 // (row, sequence). A NaN m_c marks a piece that met a table entry outside the pool.
 // After the plan, every piece's (m, l) and the o rows of the first kMergeRegs pieces are
 // requested together, so a typical sequence costs two memory round trips.
+// Fused append: the block-manager state after the call, from the allocation plan the
+// attention launch left in the workspace (the launch boundary orders its reads of the old
+// state before these writes). As alloc_kernel (pkv_state.hip): the granted table entries,
+// table_lens, free_count and every sequence's final status, BAD_BLOCK where a block the
+// rows land in has an entry outside the pool.
+__device__ inline void write_alloc_state(const StreamArgs& a) {
+    const int B = a.batch;
+    const int* al = a.plan + B + 2;
+    const int fc_raw = al[0];
+    const bool fc_bad = fc_raw < 0 || fc_raw > a.num_blocks;
+    for (int s = threadIdx.x; s < B; s += blockDim.x) {
+        const SeqAlloc r = seq_alloc(al, B, a.num_blocks, s);
+        int32_t* table = a.nr.tables + (size_t)s * a.table_stride;
+        for (int j = 0; j < r.granted; ++j) table[r.len + j] = a.nr.free_list[r.fc - 1 - r.pref - j];
+        if (r.granted > 0) a.nr.table_lens[s] = r.len + r.granted;
+        int code = r.code;
+        const int p = a.pos[s];
+        const int n = a.nr.tok_off[s + 1] - a.nr.tok_off[s];
+        if (code == PKV_SEQ_OK && p >= 0 && n > 0) {
+            const int b1 = (int)(((long long)p + n - 1) >> a.bs_shift);
+            for (int blk = p >> a.bs_shift; blk <= b1; ++blk) {
+                const int e = append_block_entry(table, a.nr.free_list, r.len, r.granted, r.fc,
+                                                 r.pref, blk);
+                if (e < 0 || e >= a.num_blocks) {
+                    code = PKV_SEQ_BAD_BLOCK;
+                    break;
+                }
+            }
+        }
+        a.nr.status[s] = code;
+    }
+    if (threadIdx.x == 0 && !fc_bad) {
+        const int total = al[1 + 2 * B];
+        *a.nr.free_count = fc_raw - (total < fc_raw ? total : fc_raw);
+    }
+}
+
+// grid (rows_seq, batch), plus one row of workgroups (blockIdx.y == batch) with a fused
+// append, whose first workgroup writes the state.
 template <int D, typename Acc>
 __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
     constexpr int kMaxPieces = 1024;
@@ -1143,6 +1248,10 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
     const int wave = tid / kSW;
+    if (s == a.batch) {  // fused append
+        if (row == 0) write_alloc_state(a);
+        return;
+    }
     if (row / a.Hq >= seq_queries(a, s)) return;  // a row past the sequence's queries
     const int per = a.plan[0];
     const int ps = a.plan[1 + s], pe = a.plan[2 + s];
@@ -1245,7 +1354,8 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     using Acc = typename SKV<KV>::Acc;
     const int waves = a.Hkv * WPH < kMaxWaves ? a.Hkv * WPH : kMaxWaves;
     const int threads = waves * kSW;
-    const size_t lds = (size_t)(2 * a.batch + 1) * sizeof(int);
+    const bool fused = ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0;
+    const size_t lds = (size_t)(2 * a.batch + 1 + (fused ? 3 * a.batch + 2 : 0)) * sizeof(int);
     const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH, ADDR>);
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
@@ -1257,8 +1367,8 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     dim3 grid(groups, a.nwg);
     hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, ADDR>), grid, dim3(threads), lds, st,
                        a);
-    hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch), dim3(kMergeNT),
-                       0, st, a);
+    hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch + (fused ? 1 : 0)),
+                       dim3(kMergeNT), 0, st, a);
     return PKV_OK;
 }
 
@@ -1333,7 +1443,7 @@ StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len, in
     const size_t rows = (size_t)p->num_heads * q_len;
     const size_t slots = (size_t)(nwg_cap < kMaxSlots ? nwg_cap : kMaxSlots) + batch;
     L.plan_off = 0;
-    L.ml_off = align((size_t)(batch + 2) * sizeof(int32_t));
+    L.ml_off = align((size_t)(4 * (size_t)batch + 4) * sizeof(int32_t));
     L.o_off = L.ml_off + align(slots * rows * 2 * sizeof(double));
     L.total = L.o_off + align(slots * rows * (size_t)p->head_dim * sizeof(double));
     return L;
@@ -1343,9 +1453,9 @@ bool stream_eligible(const pkv_params* p, int32_t G) {
     return (p->head_dim == 256 || p->head_dim == 512) && G >= 1 && G <= 8;
 }
 
-bool stream_takes_new_rows(const pkv_params* p, int32_t q_len) {
+bool stream_takes_new_rows(const pkv_params* p, int32_t q_len, int32_t batch) {
     const int G = p->num_heads / p->num_kv_heads;
-    if (p->ring_size > 0 || !stream_eligible(p, G)) return false;
+    if (p->ring_size > 0 || !stream_eligible(p, G) || batch > kFuseMaxBatch) return false;
     const int rows = G * q_len;
     if (rows > 8) return false;  // one launch (no query groups)
     const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
@@ -1398,7 +1508,7 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.part_o = ws + lay.o_off;
     a.out = out;
     if (nr) {
-        if (!stream_takes_new_rows(p, q_len))
+        if (!stream_takes_new_rows(p, q_len, batch))
             return fail(PKV_ERR_UNSUPPORTED, "stream path: appended rows need one vector-kernel launch");
         a.nr = *nr;
     }

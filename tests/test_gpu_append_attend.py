@@ -9,6 +9,7 @@ kv head) and the path that appends first (the fp64 MFMA verify kernel)."""
 import numpy as np
 import pytest
 
+from oracle import oracle as O
 from pkv import BF16, F32, LayerSpec, PagedKVCache, hip, lib
 
 pytestmark = pytest.mark.gpu
@@ -138,3 +139,103 @@ def test_append_attend_unsupported_geometry_changes_nothing(gpu):
     _same(c.k_pools[0].numpy(), kp, "K pool")
     _same(c.v_pools[0].numpy(), vp, "V pool")
     c.free()
+
+
+@pytest.mark.parametrize("kv_dtype,q_len", [(F32, 1), (BF16, 2)], ids=["f32-decode", "bf16-q2"])
+def test_append_attend_allocation_follows_oracle(gpu, kv_dtype, q_len):
+    """The fused launch computes the block allocation itself (the merge launch writes the
+    state): every status the allocation gives -- a new table, a block opened mid-batch,
+    TABLE_FULL, an inactive slot, a free list that runs dry part-way (OUT_OF_BLOCKS),
+    BAD_ARGS -- with status, tables, lengths, free list and count bit-exact against the
+    oracle's block manager (O.CacheState) and the pools against its append; then a free
+    count outside [0, num_blocks] (BAD_BLOCK for the sequences that need blocks, count
+    left as is) against pkv_append + pkv_attend on a second cache. Outputs equal the two
+    separate calls wherever the allocation gave OK."""
+    print(f"[append_attend] allocation statuses {kv_dtype} q_len={q_len}", flush=True)
+    rng = np.random.default_rng(40 + q_len)
+    hq, hkv, d = 16, 8, 256
+    B, stride, nb = 6, 3, 16
+    spec = LayerSpec(hq, hkv, d, window=0, kv_dtype=kv_dtype)
+    kvs = spec.kv_stride
+    npdt = np.uint16 if kv_dtype == BF16 else np.float32
+    lens = np.array([0, 1, 3, 0, 2, 1], np.int32)
+    tables = np.zeros((B, stride), np.int32)
+    perm = rng.permutation(nb).astype(np.int32)
+    o = 0
+    for s in range(B):
+        tables[s, :lens[s]] = perm[o:o + lens[s]]
+        o += lens[s]
+    # one block short of what the batch needs: the last sequence that needs one runs dry
+    free = np.sort(perm[o:o + 2])
+    # s0 new table; s1 opens block 1 (q_len 2) or stays in block 0; s2 TABLE_FULL;
+    # s3 inactive; s4 opens block 2 (runs dry for q_len 2); s5 BAD_ARGS (rows past the end)
+    pos = np.array([0, 16 - q_len + 1, stride * BS, -1, 32, 5], np.int32)
+    if q_len == 1:
+        pos[1] = 16  # opens block 1 too, so s4 runs dry in both variants
+    rows = B * q_len
+    tok_off = (np.arange(B + 1) * q_len).astype(np.int32)
+    tok_off[B] = rows + 3  # s5's rows reach past total_rows
+    kp = _values(rng, nb * BS * kvs, kv_dtype)
+    vp = _values(rng, nb * BS * kvs, kv_dtype)
+
+    def cache():
+        c = PagedKVCache([spec], block_size=BS, num_blocks=nb, max_seqs=B,
+                         max_blocks_per_seq=stride, max_q_len=q_len,
+                         max_pos=stride * BS + q_len, scale=0.0625)
+        c.tables.upload(tables)
+        c.table_lens.upload(lens)
+        fl = np.zeros(nb, np.int32)
+        fl[:free.size] = free
+        c.free_list.upload(fl)
+        c.free_count.upload(np.array([free.size], np.int32))
+        c.k_pools[0].upload(kp.reshape(c.k_pools[0].shape))
+        c.v_pools[0].upload(vp.reshape(c.v_pools[0].shape))
+        return c
+
+    st = O.CacheState(1, kvs, BS, nb, B, stride, alloc_pools=False, dtype=npdt)
+    st.k_pools[0], st.v_pools[0] = kp.copy(), vp.copy()
+    st.tables[:] = tables
+    st.table_lens[:] = lens
+    st.bm.free_list[:free.size] = free
+    st.bm.count[0] = free.size
+    fused, sep = cache(), cache()
+    k_new = _values(rng, (rows + 3) * kvs, kv_dtype).reshape(rows + 3, kvs)
+    v_new = _values(rng, (rows + 3) * kvs, kv_dtype).reshape(rows + 3, kvs)
+    q = rng.standard_normal((B, q_len, hq, d), dtype=np.float32)
+    dk, dv, dq = (hip.DeviceArray.from_numpy(x) for x in (k_new, v_new, q))
+    for rnd in range(2):
+        out_f = hip.DeviceArray((B, q_len, hq, d), np.float32)
+        out_s = hip.DeviceArray((B, q_len, hq, d), np.float32)
+        if rnd == 1:  # a free count outside [0, num_blocks]: devices only
+            pos = np.array([48 - q_len, 20, -1, -1, -1, -1], np.int32)
+            tok_off = (np.arange(B + 1) * q_len).astype(np.int32)
+            for c in (fused, sep):
+                c.free_count.upload(np.array([nb + 5], np.int32))
+        total = rows + 3 if rnd == 0 else rows
+        st_f = fused.append_attend(0, pos, tok_off, dk, dv, q_len, total, dq, q_len, out_f).numpy()
+        st_s = sep.append(0, pos, tok_off, dk, dv, q_len, total).numpy()
+        sep.attend(0, dq, pos, q_len, out_s)
+        a, b = fused.snapshot(), sep.snapshot()
+        _same(st_f, st_s, f"round {rnd}: status vs pkv_append")
+        for key in ("tables", "table_lens", "free_list", "free_count"):
+            _same(np.asarray(a[key]), np.asarray(b[key]), f"round {rnd}: {key} vs pkv_append")
+        _same(fused.k_pools[0].numpy(), sep.k_pools[0].numpy(), f"round {rnd}: K pool")
+        _same(fused.v_pools[0].numpy(), sep.v_pools[0].numpy(), f"round {rnd}: V pool")
+        ok = st_f == lib.PKV_SEQ_OK
+        _same(out_f.numpy()[ok], out_s.numpy()[ok], f"round {rnd}: outputs of OK sequences")
+        if rnd == 0:
+            ref = st.append(0, pos, tok_off, k_new, v_new, q_len)
+            _same(st_f, ref, "status vs oracle")
+            assert list(ref) == [lib.PKV_SEQ_OK, lib.PKV_SEQ_OK, lib.PKV_SEQ_TABLE_FULL,
+                                 lib.PKV_SEQ_OK, lib.PKV_SEQ_OUT_OF_BLOCKS,
+                                 lib.PKV_SEQ_BAD_ARGS], list(ref)
+            _same(a["tables"], st.tables, "tables vs oracle")
+            _same(a["table_lens"], st.table_lens, "table lengths vs oracle")
+            _same(a["free_list"], st.free_list, "free list vs oracle")
+            _same(fused.k_pools[0].numpy().reshape(-1), st.k_pools[0], "K pool vs oracle")
+            _same(fused.v_pools[0].numpy().reshape(-1), st.v_pools[0], "V pool vs oracle")
+        else:
+            assert list(st_f[:2]) == [lib.PKV_SEQ_BAD_BLOCK, lib.PKV_SEQ_OK], list(st_f)
+            assert a["free_count"] == nb + 5
+    fused.free()
+    sep.free()
