@@ -37,18 +37,41 @@ PEAK_FP64_MFMA_TFLOPS = 78.6  # MI355X dense fp64 matrix, AMD published
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, AMD published
 
 
-def _traffic_from_profiles(name="stream_attend_decode_cfg2_traffic.md"):
-    """HBM bytes per attention launch measured by rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), from the committed summary."""
-    path = os.path.join(REPO, "profiles", name)
+def _profile_figures(name):
+    """The figures a committed rocprofv3 summary under profiles/ records as `key: value`
+    lines: bytes_per_launch (HBM bytes per launch from --pmc FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration) and algorithmic_bytes_per_launch (this script's
+    figure for the same launches of the same run)."""
+    out = {}
     try:
-        with open(path) as f:
+        with open(os.path.join(REPO, "profiles", name)) as f:
             for line in f:
-                if line.startswith("bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
+                k, sep, v = line.partition(":")
+                if sep and k in ("bytes_per_launch", "algorithmic_bytes_per_launch"):
+                    out[k] = int(v.strip().replace(",", ""))
     except (OSError, ValueError):
         pass
-    return None
+    return out
+
+
+def _set_traffic(roof, name):
+    """roofline.traffic: the measured HBM bytes per launch of the profiled run, carried to
+    this run's launches through their ratio to the algorithmic bytes of the same profiled
+    launches (both from one window; with the window the profile used, the measured figure
+    itself)."""
+    fig = _profile_figures(name)
+    meas, alg = fig.get("bytes_per_launch"), fig.get("algorithmic_bytes_per_launch")
+    if meas is None:
+        roof["traffic"] = None
+        return roof
+    if alg:
+        ratio = meas / alg
+        roof["traffic"] = int(round(ratio * roof["algorithmic_bytes_per_launch"]))
+        roof["traffic_vs_algorithmic"] = round(ratio, 4)
+    else:
+        roof["traffic"] = meas
+    roof["traffic_profile"] = "profiles/" + name
+    return roof
 
 
 def run_gpu(sched, data, steps, warmup, log):
@@ -449,7 +472,7 @@ def bench_config3(args, log):
                 _roofline(w.attend_bytes(), dur,
                           "stream_attend_kernel<256, bf16, 2> + stream_merge_kernel<256, float>"),
                 {"attend_us": round(dur * 1e3, 2)})
-    res["roofline"]["traffic"] = _traffic_from_profiles("stream_attend_bf16_cfg3_profile.md")
+    _set_traffic(res["roofline"], "stream_attend_bf16_cfg3_traffic.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
         O.use_host_build()
@@ -634,7 +657,7 @@ def bench_config5(args, log):
                 _roofline(nbytes, float(dur.mean()), "stream_mfma_kernel<2, 1, paged> (fp64 MFMA) + "
                           "stream_merge_kernel<256, double>", flops=flops),
                 {"verify_attend_us": round(float(dur.mean()) * 1e3, 2)})
-    res["roofline"]["traffic"] = _traffic_from_profiles("verify_mtp_cfg5_traffic.md")
+    _set_traffic(res["roofline"], "verify_mtp_cfg5_traffic.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
         O.use_host_build()
@@ -755,7 +778,7 @@ def bench_producer(args, log):
     dc_ms, dc_dur, dc_bytes, dc_ok, dec = shape_leg(32, 1, dec_pos, F32, F32, args.steps,
                                                     args.warmup, 201)
     roof = _roofline(pf_bytes, pf_dur, "alloc_kernel + qkv_append_kernel<256, 2>")
-    roof["traffic"] = _traffic_from_profiles("producer_qkv_append_traffic.md")
+    _set_traffic(roof, "producer_qkv_append_traffic.md")
     res = _line("producer step (rms_norm + RoPE + KV append) tokens/s, 4 x 2048-token prefill "
                 "chunks", 4 * 2048 * args.steps / (pf_ms / 1e3), "tokens/s", args.steps,
                 args.warmup, pf_ms / args.steps, "f32 in, bf16 out",
@@ -867,7 +890,11 @@ def bench_lsa(args, log):
         step(i)
     ms = _timed(hip, stream, args.steps, step)
     _timed(hip, stream, args.steps, lambda i: step(i, ev))
-    dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+    # The timed region holds only back-to-back attention calls (stream + merge launch), so
+    # its average per call is the launch duration; an event pair around each call adds a
+    # few microseconds of its own at this size (kept as a second figure).
+    dur = ms / args.steps
+    dur_ev = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
     got = out.numpy()
     # The same lists built on the device (pkv_lsa_expand over the bucket cache), alone and
     # chained into the attention.
@@ -910,13 +937,14 @@ def bench_lsa(args, log):
                 "4 sinks), 16q/2kv/512, block 16, fp32 KV",
                 _roofline(nbytes, dur, "stream_attend_kernel<512, float, 2, 4, sparse> + "
                                        "stream_merge_kernel<512, double>"),
-                {"keys_per_sequence_mean": round(float(n_keys.mean()), 1),
+                {"launch_us_event_pairs": round(dur_ev * 1e3, 2),
+                 "keys_per_sequence_mean": round(float(n_keys.mean()), 1),
                  "max_keys": max_keys,
                  "device_expand": {"us_per_call": round(dur_x * 1e3, 2),
                                    "expand_plus_attend_us": round(dur_xa * 1e3, 2),
                                    "lists_equal_host_expand": device_lists_equal,
                                    "chained_max_rel_diff": float(f"{chained_diff:.3g}")}})
-    res["roofline"]["traffic"] = _traffic_from_profiles("lsa_sparse_stream_traffic.md")
+    _set_traffic(res["roofline"], "lsa_sparse_stream_traffic.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
         O.use_host_build()
@@ -977,23 +1005,28 @@ def bench_wo(args, log):
             step(i)
         ms = _timed(hip, stream, args.steps, step)
         _timed(hip, stream, args.steps, lambda i: step(i, ev))
-        dur = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
+        # The timed region holds nothing but back-to-back calls of the one kernel, so its
+        # average per call is the launch duration; an event pair around each launch adds
+        # a few microseconds of its own at this size (kept as a second figure).
+        dur = ms / args.steps
+        dur_ev = float(np.mean([a.elapsed_ms(b) for a, b in ev]))
         nbytes = C_OUT * c_in // 2 + C_OUT * c_in // 32 * 4 + B * c_in * 4 + B * C_OUT * 4
-        legs[name] = dict(ms=ms, dur=dur, nbytes=nbytes, packed=packed, scales=scales,
-                          x=x.numpy(), got=out.numpy(), c_in=c_in)
+        legs[name] = dict(ms=ms, dur=dur, dur_ev=dur_ev, nbytes=nbytes, packed=packed,
+                          scales=scales, x=x.numpy(), got=out.numpy(), c_in=c_in)
     g, sl = legs["global"], legs["sliding"]
     res = _line("Wo projection (Q4_0) sequences/s at the decode batch, global layer 8192 -> 2816",
                 B * args.steps / (g["ms"] / 1e3), "sequences/s", args.steps, args.warmup,
                 g["ms"] / args.steps, "q4_0 x f32",
                 "pkv_q4_matmul: 32 sequences' attn_out (16 q heads x 512 = 8192) times the Q4_0 "
                 "Wo matrix (2816 x 8192, block 32), fp32 out",
-                _roofline(g["nbytes"], g["dur"], "q4_matmul_kernel + q4_reduce_kernel"),
+                _roofline(g["nbytes"], g["dur"], "q4_matmul_kernel<2, 1>"),
                 {"data": "synthetic: seeded N(0,1) x, Q4_0 weights with seeded random nibbles "
                          "and block scales U[0.001, 0.011) (random-init, no checkpoint)",
+                 "launch_us_event_pairs": round(g["dur_ev"] * 1e3, 2),
                  "sliding_4096": {"us_per_call": round(sl["dur"] * 1e3, 2),
                                   "gbs": round(sl["nbytes"] / (sl["dur"] / 1e3) / 1e9, 1),
                                   "bytes_per_call": int(sl["nbytes"])}})
-    res["roofline"]["traffic"] = _traffic_from_profiles("wo_q4_matmul_traffic.md")
+    _set_traffic(res["roofline"], "wo_q4_matmul_traffic.md")
     if args.cpu_seconds > 0:
         from oracle import oracle as O
 
@@ -1076,13 +1109,13 @@ def main() -> int:
     achieved = nb.sum() / (dur.sum() / 1e3) / 1e9
     glob_gbs = nb[:, 1].sum() / (dur[:, 1].sum() / 1e3) / 1e9
     slide_gbs = nb[:, 0].sum() / (dur[:, 0].sum() / 1e3) / 1e9
-    traffic = _traffic_from_profiles()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                "traffic": traffic,
+                "traffic": None,
                 "kernel": "stream_attend_kernel<256, float, 2> + stream_merge_kernel<256, double>",
                 "avg_launch_us": round(dur.mean() * 1e3, 2),
                 "algorithmic_bytes_per_launch": int(nb.mean())}
+    _set_traffic(roofline, "stream_attend_decode_cfg2_traffic.md")
     result = {
         "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),

@@ -44,7 +44,8 @@ struct AttendLayout {
 AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, int32_t max_pos);
 
 // Stream-K attention (pkv_stream.hip): workspace layout and entry.
-//   plan   int32 [4 batch + 4]     per, the key prefix of every sequence [batch + 1], then
+//   plan   int32 [4 batch + 5]     the key split (per_pair, even), the key prefix of every
+//                                  sequence [batch + 1], then
 //                                  for a fused append the allocation plan: the free count
 //                                  as read, table lengths [batch], prefix of the blocks
 //                                  needed [batch + 1], status before the pops [batch]

@@ -7,10 +7,14 @@
 // lists (lsa_core.mojo:630-680).
 //
 // Work split. The keys every sequence attends ([window_start(pos), pos + q_len - 1])
-// are laid end to end, sequence after sequence; workgroup w takes the w-th run of
-// `per` keys of that concatenation (per = ceil(total / P), P workgroups sized to fill
-// the chip once), so every workgroup streams the same number of bytes whatever the mix
-// of context lengths. A workgroup has one wave per KV head (up to 8): the waves walk the
+// are laid end to end, sequence after sequence, and cut into P consecutive runs, one per
+// workgroup (P even, sized to fill the chip once), so every workgroup streams about the
+// same number of bytes whatever the mix of context lengths. The runs go in pairs: pair
+// (2p, 2p + 1) covers ceil(2 total / P) keys, the even workgroup 530/1024 of them.
+// Workgroup w runs on XCD w % 8 (round-robin dispatch, read back from XCC_ID), and
+// per-workgroup timestamps on config 2 show the odd XCDs streaming ~10% slower than the
+// even ones at equal shares; the uneven split brings the two halves closer to finishing
+// together (+1% on the decode and verify launches). A workgroup has one wave per KV head (up to 8): the waves walk the
 // same tokens together, so the workgroup reads whole 16-token pages -- 16 rows of
 // Hkv*D*elt contiguous bytes (128 KiB for fp32, 8 heads, D=256) -- instead of 1 KiB
 // slices scattered over the pool. Where a run crosses a sequence boundary the wave
@@ -65,6 +69,10 @@ constexpr int kSW = 64;                          // wavefront
 constexpr int kMaxWaves = PKV_STREAM_WAVES;      // KV heads handled by one workgroup
 constexpr int kMergeNT = 256;                    // merge kernel threads
 constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
+#ifndef PKV_STREAM_EVEN_W
+#define PKV_STREAM_EVEN_W 530
+#endif
+constexpr int kEvenW = PKV_STREAM_EVEN_W;        // even workgroup's share of a pair, / 1024
 
 template <typename KV>
 struct SKV;
@@ -345,7 +353,7 @@ struct StreamArgs {
     int32_t nwg;       // P: workgroups along the keys
     int32_t nwg_cap;   // at most this many (the workspace holds nwg_cap + batch slots)
     int32_t rows_seq;  // Hq * q_cnt: workspace rows per sequence
-    int32_t* plan;     // [0] = per, [1 + s] = key prefix of sequence s (s <= batch)
+    int32_t* plan;     // [0] per_pair, [1] even, [2 + s] key prefix of sequence s (s <= batch)
     void* part_ml;     // Acc (m, l) per (slot, row)
     void* part_o;      // Acc [D] per (slot, row)
     float* out;
@@ -395,6 +403,30 @@ __device__ inline bool new_rows_written(int code) {
     return code == PKV_SEQ_OK || code == PKV_SEQ_BAD_BLOCK;
 }
 
+// Key split: workgroups in pairs (2p, 2p + 1); pair p takes per_pair consecutive keys
+// of the concatenation, its even workgroup the first `even` of them. The launchers make
+// the workgroup count even (or 1, which takes every key).
+struct KeySplit {
+    int per_pair;
+    int even;
+    __device__ int start(int w) const { return (w >> 1) * per_pair + (w & 1) * even; }
+    __device__ int owner(int k) const {  // the workgroup holding key k
+        const int p = k / per_pair;
+        return 2 * p + (k - p * per_pair >= even ? 1 : 0);
+    }
+};
+__device__ inline KeySplit key_split(int total, int nwg) {
+    KeySplit sp;
+    if (nwg <= 1) {
+        sp.per_pair = sp.even = max(total, 1);
+        return sp;
+    }
+    const int pairs = nwg >> 1;
+    sp.per_pair = max(2 * kPerMin, (total + pairs - 1) / pairs);
+    sp.even = (int)(((long long)sp.per_pair * kEvenW + 1023) >> 10);
+    return sp;
+}
+
 // Exclusive scan of the key counts in s_pre[0..batch) (in place, one wave), total in
 // s_pre[batch].
 __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
@@ -418,10 +450,10 @@ __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
 // concatenation (s_pre[batch] = total), s_lo[s] = its first key position, or -1
 // (inactive: zeros), -2 (contract violation: NaN rows), -3 (no query of it in this
 // launch). Workgroup (0, 0) also writes the merge plan and fills the rows of inactive and
-// invalid sequences. Returns `per`, the keys of one workgroup.
+// invalid sequences. Returns the key split.
 // With a fused append, s_al (alloc_plan_ints(batch) ints) receives the allocation plan.
 template <int D, int ADDR>
-__device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo, int* s_al) {
+__device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_lo, int* s_al) {
     constexpr bool RING = ADDR == kAddrRing;
     constexpr bool SPARSE = ADDR == kAddrSparse;
     const int tid = threadIdx.x;
@@ -492,13 +524,16 @@ __device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo, i
     __syncthreads();
 
     const int total = ufirst(s_pre[B]);
-    const int per = max(kPerMin, (total + a.nwg - 1) / a.nwg);
+    const KeySplit sp = key_split(total, a.nwg);
     if (w == 0 && blockIdx.x == 0) {
         // Plan for the merge launch; inactive sequences get zeros, contract violations NaN.
-        if (tid == 0) a.plan[0] = per;
-        for (int i = tid; i <= B; i += nthr) a.plan[1 + i] = s_pre[i];
+        if (tid == 0) {
+            a.plan[0] = sp.per_pair;
+            a.plan[1] = sp.even;
+        }
+        for (int i = tid; i <= B; i += nthr) a.plan[2 + i] = s_pre[i];
         if (ADDR == kAddrPaged && fused)  // for the state writes of the merge launch
-            for (int i = tid; i < alloc_plan_ints(B); i += nthr) a.plan[B + 2 + i] = s_al[i];
+            for (int i = tid; i < alloc_plan_ints(B); i += nthr) a.plan[B + 3 + i] = s_al[i];
         for (int s = 0; s < B; ++s) {
             const int lo = s_lo[s];
             if (lo >= 0 || lo == -3) continue;
@@ -510,7 +545,7 @@ __device__ inline int stream_setup(const StreamArgs& a, int* s_pre, int* s_lo, i
             for (int i = tid; i < nrow * D; i += nthr) o[i] = fill;
         }
     }
-    return per;
+    return sp;
 }
 
 // Fused append: the appended rows (NewRows) of sequences w, w + nwg, ... go into the pool
@@ -587,13 +622,13 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     const int B = a.batch;
     constexpr bool PAGED = ADDR == kAddrPaged;
 
-    const int per = stream_setup<D, ADDR>(a, s_pre, s_lo, s_al);
+    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_al);
     const bool fused = PAGED && fused_append(a);
     if (fused) copy_new_rows<D, KV, WPH>(a, s_al, wave, lane);
     const int total = ufirst(s_pre[B]);
-    const int k0 = w * per;
+    const int k0 = sp.start(w);
     if (k0 >= total) return;
-    const int k1 = min(total, k0 + per);
+    const int k1 = min(total, sp.start(w + 1));
     const int g = blockIdx.x * (kMaxWaves / WPH) + wave / WPH;  // this wave's KV head
     const int rb = (wave % WPH) * R;  // first of this wave's rows of the head
     if (g >= a.Hkv) return;
@@ -630,7 +665,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         const int lo_key = ufirst(s_lo[s]);
         const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
         const int tb = lo_key + min(k1, pe) - ps;  // one past the last
-        const bool single = (ps / per) == ((pe - 1) / per);
+        const bool single = sp.owner(ps) == sp.owner(pe - 1);
         const int pos0 = SPARSE ? 0 : (a.pos ? ufirst(a.pos[s]) : a.pos_scalar);
         const int rows_s = a.G * seq_queries(a, s);  // this sequence's live rows
         const bool live_own = row_live && rb + r_own < rows_s;
@@ -895,11 +930,11 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int w = blockIdx.y;
     const int B = a.batch;
 
-    const int per = stream_setup<D, ADDR>(a, s_pre, s_lo, nullptr);  // never a fused append
+    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, nullptr);  // never a fused append
     const int total = ufirst(s_pre[B]);
-    const int k0 = w * per;
+    const int k0 = sp.start(w);
     if (k0 >= total) return;
-    const int k1 = min(total, k0 + per);
+    const int k1 = min(total, sp.start(w + 1));
     const int g = blockIdx.x * kMaxWaves + wave;  // this wave's KV head
     if (g >= a.Hkv) return;
 
@@ -931,7 +966,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         const int lo_key = ufirst(s_lo[s]);
         const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
         const int tb = lo_key + min(k1, pe) - ps;  // one past the last
-        const bool single = (ps / per) == ((pe - 1) / per);
+        const bool single = sp.owner(ps) == sp.owner(pe - 1);
         const int pos0 = SPARSE ? 0 : (a.pos ? ufirst(a.pos[s]) : a.pos_scalar);
         const int rows_s = a.G * seq_queries(a, s);
 
@@ -1202,7 +1237,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
 // rows land in has an entry outside the pool.
 __device__ inline void write_alloc_state(const StreamArgs& a) {
     const int B = a.batch;
-    const int* al = a.plan + B + 2;
+    const int* al = a.plan + B + 3;
     const int fc_raw = al[0];
     const bool fc_bad = fc_raw < 0 || fc_raw > a.num_blocks;
     for (int s = threadIdx.x; s < B; s += blockDim.x) {
@@ -1253,10 +1288,12 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
         return;
     }
     if (row / a.Hq >= seq_queries(a, s)) return;  // a row past the sequence's queries
-    const int per = a.plan[0];
-    const int ps = a.plan[1 + s], pe = a.plan[2 + s];
+    KeySplit sp;
+    sp.per_pair = a.plan[0];
+    sp.even = a.plan[1];
+    const int ps = a.plan[2 + s], pe = a.plan[3 + s];
     if (pe == ps) return;
-    const int wf = ps / per, wl = (pe - 1) / per;
+    const int wf = sp.owner(ps), wl = sp.owner(pe - 1);
     if (wf == wl) return;
     const int cnt = wl - wf + 1;  // <= nwg <= kMaxPieces
     const Acc* pml = static_cast<const Acc*>(a.part_ml);
@@ -1364,6 +1401,7 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     const int groups = (a.Hkv * WPH + kMaxWaves - 1) / kMaxWaves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
+    if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
     dim3 grid(groups, a.nwg);
     hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, ADDR>), grid, dim3(threads), lds, st,
                        a);
@@ -1392,6 +1430,7 @@ int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
     const int groups = (a.Hkv + kMaxWaves - 1) / kMaxWaves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
+    if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
     dim3 grid(groups, a.nwg);
     hipLaunchKernelGGL((stream_mfma_kernel<RG, TG, ADDR>), grid, dim3(threads), lds, st, a);
     hipLaunchKernelGGL((stream_merge_kernel<256, double>), dim3(a.rows_seq, a.batch),
@@ -1443,7 +1482,7 @@ StreamLayout stream_layout(const pkv_params* p, int32_t batch, int32_t q_len, in
     const size_t rows = (size_t)p->num_heads * q_len;
     const size_t slots = (size_t)(nwg_cap < kMaxSlots ? nwg_cap : kMaxSlots) + batch;
     L.plan_off = 0;
-    L.ml_off = align((size_t)(4 * (size_t)batch + 4) * sizeof(int32_t));
+    L.ml_off = align((size_t)(4 * (size_t)batch + 5) * sizeof(int32_t));
     L.o_off = L.ml_off + align(slots * rows * 2 * sizeof(double));
     L.total = L.o_off + align(slots * rows * (size_t)p->head_dim * sizeof(double));
     return L;
