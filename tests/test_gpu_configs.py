@@ -10,8 +10,7 @@ outputs within the parity rule of tests/parity.py (1e-4 fp32, 2e-2 bf16).
 
 Float data comes from the device-side seeded generator (pkv.synth) and is downloaded
 for the oracle; the oracle replays the same appends / rollbacks on its own state.
-Config 2 (the benchmark schedule) is checked by bench.py's parity sample and by
-test_gpu_attend.py's mixed-context batches."""
+Config 2 (the benchmark schedule) runs whole in test_gpu_config2.py."""
 import numpy as np
 import pytest
 
