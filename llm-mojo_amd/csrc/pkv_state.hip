@@ -132,6 +132,7 @@ __global__ __launch_bounds__(kNT) void alloc_kernel(AppendArgs a) {
     __shared__ int s_need[kMaxBatch];
     __shared__ int s_code[kMaxBatch];
     __shared__ int s_pref[kMaxBatch + 1];
+    __shared__ int s_tp[kMaxBatch + 1];
     const int tid = threadIdx.x;
     int fc = *a.free_count;
     const bool fc_bad = fc < 0 || fc > a.num_blocks;
@@ -152,29 +153,34 @@ __global__ __launch_bounds__(kNT) void alloc_kernel(AppendArgs a) {
         const int j = e - s_pref[s];
         a.tables[(size_t)s * a.table_stride + s_len[s] + j] = a.free_list[fc - 1 - e];
     }
+    // Status after the pops; s_need then counts the blocks each sequence's rows land in.
     for (int s = tid; s < a.batch; s += kNT) {
         const int need = s_need[s];
         const int granted = append_granted(need, fc, s_pref[s]);
         if (granted > 0) a.table_lens[s] = s_len[s] + granted;
-        int code = append_pop_status(s_code[s], need, granted, fc_bad);
+        const int code = append_pop_status(s_code[s], need, granted, fc_bad);
         const int p = a.pos[s];
         const int n = a.tok_off[s + 1] - a.tok_off[s];
-        if (code == PKV_SEQ_OK && p >= 0 && n > 0) {
-            // Every block the rows land in: held entries from the table, new ones from the
-            // free list (the entries the loop above writes, read at their source).
-            const int32_t* table = a.tables + (size_t)s * a.table_stride;
-            const int b1 = (int)(((long long)p + n - 1) / a.bs);
-            for (int blk = p / a.bs; blk <= b1; ++blk) {
-                const int e = append_block_entry(table, a.free_list, s_len[s], granted, fc,
-                                                 s_pref[s], blk);
-                if (e < 0 || e >= a.num_blocks) {
-                    code = PKV_SEQ_BAD_BLOCK;
-                    break;
-                }
-            }
-        }
-        a.status[s] = code;
+        s_code[s] = code;
+        s_need[s] = code == PKV_SEQ_OK && p >= 0 && n > 0
+                        ? (int)(((long long)p + n - 1) / a.bs) - p / a.bs + 1 : 0;
     }
+    __syncthreads();
+    const int checks = lds_prefix(s_need, s_tp, a.batch, s_tmp);
+    // Every block the rows land in, flattened over the batch so the entry reads are all in
+    // flight together: held entries from the table, new ones from the free list (the entries
+    // the loop above writes, read at their source). One outside the pool: BAD_BLOCK.
+    for (int e = tid; e < checks; e += kNT) {
+        const int s = find_seq(s_tp, a.batch, e);
+        const int blk = a.pos[s] / a.bs + (e - s_tp[s]);
+        const int need = s_pref[s + 1] - s_pref[s];
+        const int ent = append_block_entry(a.tables + (size_t)s * a.table_stride, a.free_list,
+                                           s_len[s], append_granted(need, fc, s_pref[s]), fc,
+                                           s_pref[s], blk);
+        if (ent < 0 || ent >= a.num_blocks) s_code[s] = PKV_SEQ_BAD_BLOCK;
+    }
+    __syncthreads();
+    for (int s = tid; s < a.batch; s += kNT) a.status[s] = s_code[s];
     if (tid == 0 && !fc_bad) *a.free_count = fc - popped;
 }
 
