@@ -1019,7 +1019,7 @@ def bench_wo(args, log):
                 g["ms"] / args.steps, "q4_0 x f32",
                 "pkv_q4_matmul: 32 sequences' attn_out (16 q heads x 512 = 8192) times the Q4_0 "
                 "Wo matrix (2816 x 8192, block 32), fp32 out",
-                _roofline(g["nbytes"], g["dur"], "q4_matmul_kernel<2, 1>"),
+                _roofline(g["nbytes"], g["dur"], "q4_matmul_kernel<2, 1, 3>"),
                 {"data": "synthetic: seeded N(0,1) x, Q4_0 weights with seeded random nibbles "
                          "and block scales U[0.001, 0.011) (random-init, no checkpoint)",
                  "launch_us_event_pairs": round(g["dur_ev"] * 1e3, 2),

@@ -58,7 +58,7 @@ struct Q4Args {
     const float* scales;  // [c_out][c_in / 32]
     const float* x;       // [batch][c_in]
     float* out;           // [batch][c_out]
-    float* part;          // [workgroups][batch][rows of a group] (split row groups)
+    float* part;          // [workgroups][rows of a group][16 TILES sequence slots] (split groups)
     int32_t* arrived;     // [groups]: workgroups of the row group done (zero between calls)
     int32_t c_in;
     int32_t c_out;
@@ -142,33 +142,169 @@ __device__ inline void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// s_barrier without the fence of __syncthreads (which waits for every load in flight).
+__device__ inline void pass_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 constexpr int kQ4Lds = 128 * 1024;
 constexpr int kQ4MaxPass = 3;  // passes of 8 blocks staged at once (one block per wave each)
 
-// TILES column tiles of 16 sequences; RH row halves of 64 rows (row group = 64 RH rows).
-// TILES and RH are compile-time, so every MFMA result is read in the MFMA's own basic
-// block (with a runtime count a chain could end in a branch whose target read the first
-// result register without the MFMA's wait states).
+// One LDS dword read the compiler does not track: it would otherwise wait for every
+// direct-to-LDS copy in flight (vmcnt 0) before it, since it cannot tell which LDS words
+// a copy writes. The caller waits (lgkmcnt) before using the value (read_tile).
+// base: an LDS byte address; OFF: a constant byte offset (< 65536).
+template <int OFF>
+__device__ inline uint32_t lds_read_u32(uint32_t base) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(base), "i"(OFF));
+    return v;
+}
+__device__ inline uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+
+// The inputs of one block for this wave's column tiles: per column tile, 8 of one sequence
+// per lane (lane j + 16q: sequence 16ct + j, inputs 32b + 8q .. + 7). The sequence is
+// clamped into the batch, so both loads are always issued: those of a sequence past the
+// batch only reach outputs that are not stored.
+template <int TILES>
+struct XPass {
+    f32x4 v[TILES][2];
+};
+template <int TILES>
+__device__ inline XPass<TILES> load_x(const Q4Args& a, int b, int j, int lane) {
+    XPass<TILES> r;
+#pragma unroll
+    for (int ct = 0; ct < TILES; ++ct) {
+        const int seq = min(16 * ct + j, a.batch - 1);
+        const f32x4* xp = reinterpret_cast<const f32x4*>(a.x + (size_t)seq * a.c_in + 32 * b + 8 * (lane >> 4));
+        r.v[ct][0] = xp[0];
+        r.v[ct][1] = xp[1];
+    }
+    return r;
+}
+
+// Pass i's weights ([row][8 blocks] 16-byte chunks; a row's blocks are contiguous in
+// memory, so whole cache lines are read) and scales ([row][8 blocks]) straight into LDS:
+// RH copy instructions of each kind per wave. Block bb of row r sits at chunk
+// r * 8 + (bb ^ (r & 7)), so the 16 rows of a weight read fall on different banks. Rows
+// past c_out read the last row and blocks past the run read the pass's first block (the
+// run's last, for a pass wholly past the run); none of them is used.
+template <int RH, int PASS_W, int PASS_S>
+__device__ inline void copy_pass(const Q4Args& a, char* smem, int g, int c_lo, int b_hi, int v,
+                                 int lane, int i) {
+    constexpr int RG = 64 * RH;
+    const int p0 = c_lo + 8 * i, pn = min(8, b_hi - p0), pf = min(p0, b_hi - 1);
+    char* s_w = smem + i * (PASS_W + PASS_S);
+    char* s_s = s_w + PASS_W;
+#pragma unroll
+    for (int n = 0; n < RH; ++n) {
+        const int k = v + kQ4Waves * n;  // copy instruction of this pass
+        const int e = 64 * k + lane, r = e >> 3, bb = (e & 7) ^ (r & 7);
+        const int row = min(g * RG + r, a.c_out - 1);
+        __builtin_amdgcn_global_load_lds(
+            a.w + (size_t)row * (a.c_in / 2) + (size_t)(bb < pn ? p0 + bb : pf) * 16,
+            (lds_void*)(s_w + 1024 * k), 16, 0, 0);
+    }
+#pragma unroll
+    for (int n = 0; n < RH; ++n) {
+        const int k = v + kQ4Waves * n;
+        const int e = 64 * k + lane, r = e >> 3, bb = e & 7;
+        const int row = min(g * RG + r, a.c_out - 1);
+        __builtin_amdgcn_global_load_lds(a.scales + (size_t)row * a.nb + (bb < pn ? p0 + bb : pf),
+                                         (lds_void*)(s_s + 256 * k), 4, 0, 0);
+    }
+}
+
+// Row tile T's weight dword and block scale in pass I (row r = 16T + j of the group:
+// weights at pass + ((r 8 + (v ^ (r & 7))) 4 + lane / 16) 4, the scale at
+// pass + PASS_W + (r 8 + v) 4, i.e. the lane's base plus a constant), both complete on
+// return: the values are tied to the lgkmcnt wait, so no use can be scheduled above it.
+template <int I, int T, int PASS, int PASS_W>
+__device__ inline void read_tile(uint32_t w_base, uint32_t s_base, uint32_t& wd, uint32_t& sc) {
+    wd = lds_read_u32<I * PASS + T * 2048>(w_base);
+    sc = lds_read_u32<I * PASS + PASS_W + T * 512>(s_base);
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(wd), "+v"(sc));
+}
+
+// One block of pass I: the wave splits its inputs into three exact bf16 operands once and
+// feeds them to every row tile of the group.
+template <int I, int TILES, int RT, int PASS, int PASS_W>
+__device__ inline void compute_pass(const XPass<TILES>& xr, uint32_t w_base, uint32_t s_base,
+                                    f32x4 (&acc)[RT][TILES]) {
+    static_assert(RT == 4, "row tiles of a 64-row group");
+    bf16x8 X[TILES][3];
+#pragma unroll
+    for (int ct = 0; ct < TILES; ++ct) {
+        const float xv[8] = {xr.v[ct][0].x, xr.v[ct][0].y, xr.v[ct][0].z, xr.v[ct][0].w,
+                             xr.v[ct][1].x, xr.v[ct][1].y, xr.v[ct][1].z, xr.v[ct][1].w};
+        split3(xv, X[ct][0], X[ct][1], X[ct][2]);
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        uint32_t wd, scb;
+        if (t == 0) read_tile<I, 0, PASS, PASS_W>(w_base, s_base, wd, scb);
+        else if (t == 1) read_tile<I, 1, PASS, PASS_W>(w_base, s_base, wd, scb);
+        else if (t == 2) read_tile<I, 2, PASS, PASS_W>(w_base, s_base, wd, scb);
+        else read_tile<I, 3, PASS, PASS_W>(w_base, s_base, wd, scb);
+        const float sc = __uint_as_float(scb) * kQ4Unpack;
+        const bf16x8 W = unpack_q4(wd);
+#pragma unroll
+        for (int ct = 0; ct < TILES; ++ct) {
+            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][2], W, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][1], W, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][0], W, c, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][ct][e] = fmaf(sc, c[e], acc[t][ct][e]);
+        }
+    }
+}
+
+// 16 bytes stored and loaded at system scope (written through, read past the L2 caches).
+// The loads are not tracked by the compiler; wait_loads completes them (the values are
+// tied to the wait, so no use can be scheduled above it).
+__device__ inline void store16_system(float* p, f32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ inline f32x4 load16_system(const float* p) {
+    f32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+constexpr int kQ4RedLoads = 8;  // partials requested at once per thread
+__device__ inline void wait_loads(f32x4 (&v)[kQ4RedLoads]) {
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),
+                   "+v"(v[7]));
+}
+
+// TILES column tiles of 16 sequences; RH row halves of 64 rows (row group = 64 RH rows);
+// PASSES passes of 8 blocks per chunk. All three are compile-time, so every MFMA result is
+// read in the MFMA's own basic block (with a runtime count a chain could end in a branch
+// whose target read the first result register without the MFMA's wait states), and every
+// chunk issues the same loads (exact vmcnt waits).
 //
 // Workgroup = (row group g, split k): blocks [k per, (k + 1) per) of the group's rows.
 // Operand roles: A = the inputs (16 sequences x 32), B = the weights (32 x 16 rows), so
 // C[seq][row] puts one row in each lane (lane j + 16q: row j of the tile, sequences
 // 4q .. 4q + 3) and each lane scales its four sums by one block scale.
-// Staging, per chunk of up to kQ4MaxPass passes of 8 blocks: every wave first requests the
-// fp32 inputs of its blocks (block v of each pass), then the workgroup copies the passes'
-// weights ([row][8 blocks] 16-byte chunks; a row's blocks are contiguous in memory, so
-// whole cache lines are read) and scales ([row][8 blocks]) straight into LDS, 2 RH copy
-// instructions per wave and pass. Pass i is computed as soon as its copies have landed
-// (vmcnt counts the later passes' copies), so the later passes stream in meanwhile.
-// In LDS, block bb of row r sits at chunk r * 8 + (bb ^ (r & 7)): the 16 rows of a
-// weight read then fall on different banks, two lanes per bank.
-template <int TILES, int RH>
+// Staging, per chunk: each pass's inputs (registers, block v of the pass for wave v) and
+// weights and scales (LDS, copied by the whole workgroup) are requested up front, and pass
+// i is computed as soon as its own loads have landed, the later passes' still streaming in.
+template <int TILES, int RH, int PASSES>
 __global__ __launch_bounds__(kQ4NT) __attribute__((amdgpu_waves_per_eu(RH == 1 && TILES <= 2 ? 4 : 2)))
 void q4_matmul_kernel(Q4Args a) {
+    static_assert(PASSES >= 1 && PASSES <= kQ4MaxPass, "passes");
     constexpr int RT = 4 * RH;        // row tiles of the group
     constexpr int RG = 64 * RH;       // rows of the group
     constexpr int kPassW = RG * 8 * 16;  // bytes of weights per pass
     constexpr int kPassS = RG * 8 * 4;   // bytes of scales per pass
+    constexpr int kXLoads = 2 * TILES;  // input load instructions per wave and pass
+    static_assert(kXLoads + 4 * RH < 64, "vmcnt");
     constexpr int kLds = kQ4Waves * RT * TILES * 64 * 16 > kQ4MaxPass * (kPassW + kPassS)
                              ? kQ4Waves * RT * TILES * 64 * 16 : kQ4MaxPass * (kPassW + kPassS);
     static_assert(kLds <= kQ4Lds, "LDS");
@@ -190,92 +326,51 @@ void q4_matmul_kernel(Q4Args a) {
 #pragma unroll
         for (int ct = 0; ct < TILES; ++ct) acc[t][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int c_lo = b_lo; c_lo < b_hi; c_lo += 8 * kQ4MaxPass) {
-        const int cn = min(8 * kQ4MaxPass, b_hi - c_lo);
-        const int passes = (cn + 7) / 8;
-        // 1. the inputs of this wave's blocks (L2-resident): per column tile, 8 of one
-        // sequence per lane (lane j + 16q: sequence 16ct + j, inputs 32b + 8q .. + 7)
-        float4 xr[kQ4MaxPass][TILES][2];
-#pragma unroll
-        for (int i = 0; i < kQ4MaxPass; ++i) {
-            const int b = c_lo + 8 * i + v;
-#pragma unroll
-            for (int ct = 0; ct < TILES; ++ct) {
-                const int seq = 16 * ct + j;
-                if (i < passes && b < b_hi && seq < a.batch) {
-                    const float4* xp = reinterpret_cast<const float4*>(a.x + (size_t)seq * a.c_in + 32 * b + 8 * (lane >> 4));
-                    xr[i][ct][0] = xp[0];
-                    xr[i][ct][1] = xp[1];
-                } else {
-                    xr[i][ct][0] = xr[i][ct][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-            }
+    const uint32_t w_base = lds_addr(smem) + ((j * 8 + (v ^ (j & 7))) * 4 + (lane >> 4)) * 4;
+    const uint32_t s_base = lds_addr(smem) + (j * 8 + v) * 4;
+    for (int c_lo = b_lo; c_lo < b_hi; c_lo += 8 * PASSES) {
+        // 1. Loads, in this issue order: inputs of pass 0, weights and scales of pass 0,
+        // inputs of pass 1, weights and scales of passes 1 and 2; the inputs of pass 2
+        // follow once pass 0 is computed (in the registers pass 0 frees). Every chunk
+        // issues all PASSES passes (a pass past the run reads in-range blocks it does not
+        // use), so no branch separates a load from its use and each wait below counts
+        // exactly the instructions issued after the pass it waits for. Compiler barriers
+        // keep the groups in this order.
+        XPass<TILES> x0, x1, x2;
+        x0 = load_x<TILES>(a, min(c_lo + v, b_hi - 1), j, lane);
+        copy_pass<RH, kPassW, kPassS>(a, smem, g, c_lo, b_hi, v, lane, 0);
+        asm volatile("" ::: "memory");
+        if constexpr (PASSES > 1) {
+            x1 = load_x<TILES>(a, min(c_lo + 8 + v, b_hi - 1), j, lane);
+            copy_pass<RH, kPassW, kPassS>(a, smem, g, c_lo, b_hi, v, lane, 1);
+            asm volatile("" ::: "memory");
         }
-        // 2. weights and scales of every pass straight to LDS (rows past c_out read the
-        // last row, blocks past the pass read its first block; neither is used)
-#pragma unroll
-        for (int i = 0; i < kQ4MaxPass; ++i) {
-            if (i < passes) {
-                const int p0 = c_lo + 8 * i, pn = min(8, b_hi - p0);
-                char* s_w = smem + i * (kPassW + kPassS);
-                char* s_s = s_w + kPassW;
-#pragma unroll
-                for (int n = 0; n < RH; ++n) {
-                    const int k = v + kQ4Waves * n;  // copy instruction of this pass
-                    const int e = 64 * k + lane, r = e >> 3, bb = (e & 7) ^ (r & 7);
-                    const int row = min(g * RG + r, a.c_out - 1);
-                    __builtin_amdgcn_global_load_lds(
-                        a.w + (size_t)row * (a.c_in / 2) + (size_t)(p0 + (bb < pn ? bb : 0)) * 16,
-                        (lds_void*)(s_w + 1024 * k), 16, 0, 0);
-                }
-#pragma unroll
-                for (int n = 0; n < RH; ++n) {
-                    const int k = v + kQ4Waves * n;
-                    const int e = 64 * k + lane, r = e >> 3, bb = e & 7;
-                    const int row = min(g * RG + r, a.c_out - 1);
-                    __builtin_amdgcn_global_load_lds(a.scales + (size_t)row * a.nb + p0 + (bb < pn ? bb : 0),
-                                                     (lds_void*)(s_s + 256 * k), 4, 0, 0);
-                }
-            }
+        if constexpr (PASSES > 2) {
+            copy_pass<RH, kPassW, kPassS>(a, smem, g, c_lo, b_hi, v, lane, 2);
+            asm volatile("" ::: "memory");
         }
-        // 3. pass i once its copies have landed, the later passes' still in flight
-#pragma unroll
-        for (int i = 0; i < kQ4MaxPass; ++i) {
-            if (i < passes) {
-                const int later = passes - 1 - i;  // passes issued after this one
-                if (later >= 2) wait_vm<4 * RH>();
-                else if (later == 1) wait_vm<2 * RH>();
-                else wait_vm<0>();
-                __syncthreads();  // every wave's copies of pass i
-                const int b = c_lo + 8 * i + v;
-                if (b < b_hi) {
-                    // A operands: the block's inputs in three exact bf16 parts per column tile
-                    bf16x8 X[TILES][3];
-#pragma unroll
-                    for (int ct = 0; ct < TILES; ++ct) {
-                        const float xv[8] = {xr[i][ct][0].x, xr[i][ct][0].y, xr[i][ct][0].z, xr[i][ct][0].w,
-                                             xr[i][ct][1].x, xr[i][ct][1].y, xr[i][ct][1].z, xr[i][ct][1].w};
-                        split3(xv, X[ct][0], X[ct][1], X[ct][2]);
-                    }
-                    const uint32_t* s_w = reinterpret_cast<const uint32_t*>(smem + i * (kPassW + kPassS));
-                    const float* s_s = reinterpret_cast<const float*>(smem + i * (kPassW + kPassS) + kPassW);
-#pragma unroll
-                    for (int t = 0; t < RT; ++t) {
-                        const int r = 16 * t + j;
-                        const uint32_t wd = s_w[(r * 8 + (v ^ (r & 7))) * 4 + (lane >> 4)];
-                        const float sc = s_s[r * 8 + v] * kQ4Unpack;
-                        const bf16x8 W = unpack_q4(wd);
-#pragma unroll
-                        for (int ct = 0; ct < TILES; ++ct) {
-                            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][2], W, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][1], W, c, 0, 0, 0);
-                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(X[ct][0], W, c, 0, 0, 0);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) acc[t][ct][e] = fmaf(sc, c[e], acc[t][ct][e]);
-                        }
-                    }
-                }
-            }
+        // 2. Pass i once its loads have landed, the later passes' still in flight. The
+        // barrier carries no fence: a fence would wait for every outstanding copy (vmcnt
+        // 0), and so would the compiler before any LDS read it sees after a direct-to-LDS
+        // copy; the wave's own vmcnt wait covers its share of pass i, the barrier the
+        // others', and the pass's LDS words are read by read_tile.
+        wait_vm<PASSES == 3 ? kXLoads + 4 * RH : PASSES == 2 ? kXLoads + 2 * RH : 0>();
+        pass_barrier();
+        if (c_lo + v < b_hi) compute_pass<0, TILES, RT, kPassW + kPassS, kPassW>(x0, w_base, s_base, acc);
+        if constexpr (PASSES > 2) {
+            asm volatile("" ::: "memory");
+            x2 = load_x<TILES>(a, min(c_lo + 16 + v, b_hi - 1), j, lane);
+            asm volatile("" ::: "memory");
+        }
+        if constexpr (PASSES > 1) {
+            wait_vm<PASSES == 3 ? kXLoads + 2 * RH : 0>();  // w2, x2 pending
+            pass_barrier();
+            if (c_lo + 8 + v < b_hi) compute_pass<1, TILES, RT, kPassW + kPassS, kPassW>(x1, w_base, s_base, acc);
+        }
+        if constexpr (PASSES > 2) {
+            wait_vm<0>();
+            pass_barrier();
+            if (c_lo + 16 + v < b_hi) compute_pass<2, TILES, RT, kPassW + kPassS, kPassW>(x2, w_base, s_base, acc);
         }
         __syncthreads();  // every wave is done with this chunk's LDS
     }
@@ -292,31 +387,30 @@ void q4_matmul_kernel(Q4Args a) {
 #pragma unroll
         for (int ct = 0; ct < TILES; ++ct) s_red[((v * RT + t) * TILES + ct) * 64 + lane] = acc[t][ct];
     __syncthreads();
-    // Thread unit = one row and four sequences (one lane's f32x4); consecutive threads take
-    // consecutive rows, so each of the four stores is contiguous across threads.
+    // Thread unit = one row and four sequences (one lane's f32x4). Consecutive threads take
+    // a row's sequence quads, then the next row: a wave's partial stores (and the last
+    // workgroup's loads) cover contiguous memory.
     const bool single = a.splits == 1;
     constexpr int kUnits = RG * 4 * TILES;
+    constexpr int SW = 16 * TILES;  // sequence slots of a partial row
 #pragma unroll
     for (int k = 0; k < (kUnits + kQ4NT - 1) / kQ4NT; ++k) {
         const int u = tid + k * kQ4NT;
         if (u < kUnits) {
-            const int r = u % RG, qq = (u / RG) % 4, ct = u / (RG * 4);
+            const int qq = u % 4, ct = (u / 4) % TILES, r = u / (4 * TILES);
             const int t = r >> 4, ln = (r & 15) + 16 * qq;
             f32x4 sum = s_red[(t * TILES + ct) * 64 + ln];
 #pragma unroll
             for (int w = 1; w < kQ4Waves; ++w) sum += s_red[((w * RT + t) * TILES + ct) * 64 + ln];
             const int row = g * RG + r;
+            if (single) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int seq = 16 * ct + 4 * qq + e;
-                if (seq < a.batch) {
-                    if (single) {
-                        if (row < a.c_out) a.out[(size_t)seq * a.c_out + row] = sum[e];
-                    } else {  // written through to memory (system scope): see below
-                        __hip_atomic_store(&a.part[((size_t)blockIdx.x * a.batch + seq) * RG + r], sum[e],
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    const int seq = 16 * ct + 4 * qq + e;
+                    if (seq < a.batch && row < a.c_out) a.out[(size_t)seq * a.c_out + row] = sum[e];
                 }
+            } else {  // the four sequences' sums in one store, written through (see below)
+                store16_system(a.part + ((size_t)blockIdx.x * RG + r) * SW + 16 * ct + 4 * qq, sum);
             }
         }
     }
@@ -338,34 +432,29 @@ void q4_matmul_kernel(Q4Args a) {
     }
     __syncthreads();
     if (!s_last) return;
-    // Every partial of every output requested before any is added: kQ4RedOut outputs of
-    // up to 16 partials per thread and round (the partials come from memory).
-    const float* p0 = a.part + (size_t)g * a.splits * a.batch * RG;
-    const size_t stride = (size_t)a.batch * RG;
-    const int n = a.batch * RG;
-    constexpr int kQ4RedOut = 4;
-    for (int base = 0; base < n; base += kQ4RedOut * kQ4NT) {
-        float vals[kQ4RedOut][16];
+    // Per unit, the partials of kQ4RedLoads workgroups are requested together (a group past
+    // the last workgroup re-reads the last one and is not added), then added in workgroup
+    // order.
+    const float* p0 = a.part + (size_t)g * a.splits * RG * SW;
+    for (int u = tid; u < kUnits; u += kQ4NT) {
+        const int qq = u % 4, ct = (u / 4) % TILES, r = u / (4 * TILES);
+        const float* pu = p0 + (size_t)r * SW + 16 * ct + 4 * qq;
+        f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < a.splits; k0 += kQ4RedLoads) {
+            f32x4 vals[kQ4RedLoads];
 #pragma unroll
-        for (int m = 0; m < kQ4RedOut; ++m) {
-            const int i = base + m * kQ4NT + tid;
+            for (int k = 0; k < kQ4RedLoads; ++k)
+                vals[k] = load16_system(pu + (size_t)min(k0 + k, a.splits - 1) * RG * SW);
+            wait_loads(vals);
 #pragma unroll
-            for (int k = 0; k < 16; ++k)
-                vals[m][k] = (i < n && k < a.splits)
-                                 ? __hip_atomic_load(&p0[(size_t)k * stride + i], __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_SYSTEM)
-                                 : 0.f;
+            for (int k = 0; k < kQ4RedLoads; ++k)
+                if (k0 + k < a.splits) sum += vals[k];
         }
+        const int row = g * RG + r;
 #pragma unroll
-        for (int m = 0; m < kQ4RedOut; ++m) {
-            const int i = base + m * kQ4NT + tid;
-            float sum = 0.f;
-#pragma unroll
-            for (int k = 0; k < 16; ++k) sum += vals[m][k];
-            for (int k = 16; k < a.splits; ++k)
-                sum += __hip_atomic_load(&p0[(size_t)k * stride + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            const int seq = i / RG, r = i % RG, row = g * RG + r;
-            if (i < n && row < a.c_out) a.out[(size_t)seq * a.c_out + row] = sum;
+        for (int e = 0; e < 4; ++e) {
+            const int seq = 16 * ct + 4 * qq + e;
+            if (seq < a.batch && row < a.c_out) a.out[(size_t)seq * a.c_out + row] = sum[e];
         }
     }
 }
@@ -385,10 +474,11 @@ size_t pkv_q4_matmul_workspace_size(int32_t c_in, int32_t c_out, int32_t batch) 
     const size_t rg = 64 * (size_t)pkv::q4_rh(batch);
     const size_t groups = ((size_t)c_out + rg - 1) / rg;
     // the row groups' arrival counts, then partials of at most kQ4MaxWg workgroups (or
-    // one per row group)
+    // one per row group): [workgroup][row of the group][16 x column tiles sequence slots]
     const size_t counts = (groups * sizeof(int32_t) + 255) & ~(size_t)255;
     const size_t wgs = groups > (size_t)pkv::kQ4MaxWg ? groups : (size_t)pkv::kQ4MaxWg;
-    return counts + wgs * batch * rg * sizeof(float);
+    const size_t slots = 16 * (((size_t)batch + 15) / 16);
+    return counts + wgs * rg * slots * sizeof(float);
 }
 
 int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales, const float* x,
@@ -413,13 +503,15 @@ int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales
         return fail(PKV_ERR_UNSUPPORTED, "pkv_q4_matmul: matrix too large");
     const int tiles = (batch + 15) / 16;
     const int rh = q4_rh(batch);
-    const void* fn = nullptr;
-    switch (tiles) {
-        case 1: fn = reinterpret_cast<const void*>(&q4_matmul_kernel<1, 1>); break;
-        case 2: fn = reinterpret_cast<const void*>(&q4_matmul_kernel<2, 1>); break;
-        case 3: fn = reinterpret_cast<const void*>(&q4_matmul_kernel<3, 1>); break;
-        default: fn = reinterpret_cast<const void*>(&q4_matmul_kernel<4, 1>); break;
-    }
+    // Kernel instance per (column tiles, passes of a chunk); every instance has the same
+    // register cap and LDS, so the occupancy query takes the three-pass one.
+    using Kern = void (*)(Q4Args);
+    static const Kern kKerns[4][kQ4MaxPass] = {
+        {q4_matmul_kernel<1, 1, 1>, q4_matmul_kernel<1, 1, 2>, q4_matmul_kernel<1, 1, 3>},
+        {q4_matmul_kernel<2, 1, 1>, q4_matmul_kernel<2, 1, 2>, q4_matmul_kernel<2, 1, 3>},
+        {q4_matmul_kernel<3, 1, 1>, q4_matmul_kernel<3, 1, 2>, q4_matmul_kernel<3, 1, 3>},
+        {q4_matmul_kernel<4, 1, 1>, q4_matmul_kernel<4, 1, 2>, q4_matmul_kernel<4, 1, 3>}};
+    const void* fn = reinterpret_cast<const void*>(kKerns[tiles - 1][kQ4MaxPass - 1]);
     Q4Args a{};
     a.w = w_packed;
     a.scales = scales;
@@ -442,13 +534,10 @@ int32_t pkv_q4_matmul(void* stream, const uint8_t* w_packed, const float* scales
     a.per = (a.nb + splits - 1) / splits;
     a.splits = (a.nb + a.per - 1) / a.per;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    // passes of 8 blocks per chunk: a run of `per` blocks in chunks of up to kQ4MaxPass
+    const int passes = a.per >= 8 * kQ4MaxPass ? kQ4MaxPass : (a.per + 7) / 8;
     const dim3 grid(a.groups * a.splits), block(kQ4NT);
-    switch (tiles) {
-        case 1: hipLaunchKernelGGL((q4_matmul_kernel<1, 1>), grid, block, 0, st, a); break;
-        case 2: hipLaunchKernelGGL((q4_matmul_kernel<2, 1>), grid, block, 0, st, a); break;
-        case 3: hipLaunchKernelGGL((q4_matmul_kernel<3, 1>), grid, block, 0, st, a); break;
-        default: hipLaunchKernelGGL((q4_matmul_kernel<4, 1>), grid, block, 0, st, a); break;
-    }
+    hipLaunchKernelGGL(kKerns[tiles - 1][passes - 1], grid, block, 0, st, a);
     return check_launch("pkv_q4_matmul");
 }
 
