@@ -376,6 +376,9 @@ __device__ inline size_t out_row(const StreamArgs& a, int s, int g, int r) {
 // [1 + B, 2 + 2B) the exclusive prefix of the blocks each sequence needs (total last),
 // [2 + 2B, 2 + 3B) the status before the pops.
 __device__ inline int alloc_plan_ints(int batch) { return 3 * batch + 2; }
+// Ints of a stream kernel's per-sequence LDS before the allocation plan: s_pre [batch + 1],
+// s_lo [batch], s_meta [3 batch + 1].
+__host__ __device__ constexpr int stream_seq_ints(int batch) { return 5 * batch + 2; }
 __device__ inline bool fused_append(const StreamArgs& a) { return a.nr.k_new && a.j0 == 0; }
 
 struct SeqAlloc {
@@ -451,9 +454,14 @@ __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
 // (inactive: zeros), -2 (contract violation: NaN rows), -3 (no query of it in this
 // launch). Workgroup (0, 0) also writes the merge plan and fills the rows of inactive and
 // invalid sequences. Returns the key split.
+// s_meta (meta_ints(batch) ints) keeps what the pieces need of each sequence, so a piece
+// reads none of it from global memory: [s] its position (sparse: its list's first index),
+// [batch + s] its query count in this launch, and with a fused append [2 batch + s] its
+// first appended row (tok_off[s]; [3 batch] = tok_off[batch]).
 // With a fused append, s_al (alloc_plan_ints(batch) ints) receives the allocation plan.
 template <int D, int ADDR>
-__device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_lo, int* s_al) {
+__device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_lo, int* s_meta,
+                                        int* s_al) {
     constexpr bool RING = ADDR == kAddrRing;
     constexpr bool SPARSE = ADDR == kAddrSparse;
     const int tid = threadIdx.x;
@@ -471,11 +479,15 @@ __device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_
             else if (cnt > 0) lo = 0, n = cnt;
             s_pre[i] = n;
             s_lo[i] = lo;
+            s_meta[i] = kb;
+            s_meta[B + i] = seq_queries(a, i);
             continue;
         }
         const int p0 = a.pos ? a.pos[i] : a.pos_scalar;
         const int qlen = a.q_lens ? a.q_lens[i] : a.q_len;
         const int qc = seq_queries(a, i);
+        s_meta[i] = p0;
+        s_meta[B + i] = qc;
         if (qlen < 0 || qlen > a.q_len) {
             lo = -2;  // a query count outside the layout: NaN rows
         } else if (qc == 0) {
@@ -513,6 +525,8 @@ __device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_
             s_al[1 + i] = len;
             s_al[1 + B + i] = need > 0 ? need : 0;
             s_al[2 + 2 * B + i] = need < 0 ? need : PKV_SEQ_OK;
+            s_meta[2 * B + i] = a.nr.tok_off[i];
+            if (i == B - 1) s_meta[3 * B] = a.nr.tok_off[B];
         }
     }
     if (ADDR == kAddrPaged && fused && tid == 0) s_al[0] = *a.nr.free_count;
@@ -555,7 +569,8 @@ __device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_
 // table entry lies outside the pool, is skipped. The block of a row comes from the plan
 // (held: the table, granted: the free list), so this launch reads no state it writes.
 template <int D, typename KV, int WPH>
-__device__ inline void copy_new_rows(const StreamArgs& a, const int* s_al, int wave, int lane) {
+__device__ inline void copy_new_rows(const StreamArgs& a, const int* s_meta, const int* s_al,
+                                     int wave, int lane) {
     constexpr int kElt = SKV<KV>::kElt;
     constexpr int kVec = D * kElt / 16;  // 16-byte vectors per head slice
     const int g = wave / WPH;
@@ -563,31 +578,42 @@ __device__ inline void copy_new_rows(const StreamArgs& a, const int* s_al, int w
     const size_t row_bytes = (size_t)a.Hkv * D * kElt;
     const size_t head_off = (size_t)g * D * kElt;
     const int bs_mask = (1 << a.bs_shift) - 1;
-    for (int s = blockIdx.y; s < a.batch; s += a.nwg) {
-        const int p0 = a.pos[s];
-        const int r0 = a.nr.tok_off[s];
-        const int n = a.nr.tok_off[s + 1] - r0;
-        const SeqAlloc al = seq_alloc(s_al, a.batch, a.num_blocks, s);
+    const int B = a.batch;
+    for (int s = blockIdx.y; s < B; s += a.nwg) {
+        const int p0 = s_meta[s];
+        const int r0 = s_meta[2 * B + s];
+        const int n = s_meta[2 * B + s + 1] - r0;
+        const SeqAlloc al = seq_alloc(s_al, B, a.num_blocks, s);
         if (!new_rows_written(al.code) || p0 < 0 || n <= 0) continue;
         if (al.len > a.table_stride) continue;  // a length outside the table: BAD_BLOCK
         const int32_t* table = a.tables + (size_t)s * a.table_stride;
         for (int b = 0; b < n; ++b) {
             const int p = p0 + b;
             const int blk = p >> a.bs_shift;
+            // the row's values are requested with its block's table entry (one round trip)
+            const size_t src = ((size_t)r0 + b) * row_bytes + head_off;
+            const uint4* ks = reinterpret_cast<const uint4*>(a.nr.k_new + src);
+            const uint4* vs = reinterpret_cast<const uint4*>(a.nr.v_new + src);
+            uint4 kv[(kVec + kSW - 1) / kSW], vv[(kVec + kSW - 1) / kSW];
+#pragma unroll
+            for (int j = 0; j < (kVec + kSW - 1) / kSW; ++j) {
+                const int i = min(lane + j * kSW, kVec - 1);
+                kv[j] = ks[i];
+                vv[j] = vs[i];
+            }
             const int phys = append_block_entry(table, a.nr.free_list, al.len, al.granted,
                                                 al.fc, al.pref, blk);
             if (phys < 0 || phys >= a.num_blocks) continue;
             const size_t dst = (((size_t)phys << a.bs_shift) | (size_t)(p & bs_mask)) * row_bytes + head_off;
-            const size_t src = ((size_t)r0 + b) * row_bytes + head_off;
-            const uint4* ks = reinterpret_cast<const uint4*>(a.nr.k_new + src);
-            const uint4* vs = reinterpret_cast<const uint4*>(a.nr.v_new + src);
             uint4* kd = reinterpret_cast<uint4*>(a.nr.k_dst + dst);
             uint4* vd = reinterpret_cast<uint4*>(a.nr.v_dst + dst);
-            for (int i = lane; i < kVec; i += kSW) {
-                const uint4 kv = ks[i];
-                const uint4 vv = vs[i];
-                kd[i] = kv;
-                vd[i] = vv;
+#pragma unroll
+            for (int j = 0; j < (kVec + kSW - 1) / kSW; ++j) {
+                const int i = lane + j * kSW;
+                if (i < kVec) {
+                    kd[i] = kv[j];
+                    vd[i] = vv[j];
+                }
             }
         }
     }
@@ -613,7 +639,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     extern __shared__ int smem[];
     int* s_pre = smem;                  // [batch + 1]
     int* s_lo = smem + a.batch + 1;     // [batch]: window start, -1 inactive, -2 bad
-    int* s_al = smem + 2 * a.batch + 1; // fused append: the allocation plan
+    int* s_meta = smem + 2 * a.batch + 1;             // [3 batch + 1] (stream_setup)
+    int* s_al = smem + stream_seq_ints(a.batch);      // fused append: the allocation plan
 
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
@@ -622,9 +649,9 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     const int B = a.batch;
     constexpr bool PAGED = ADDR == kAddrPaged;
 
-    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_al);
+    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, s_al);
     const bool fused = PAGED && fused_append(a);
-    if (fused) copy_new_rows<D, KV, WPH>(a, s_al, wave, lane);
+    if (fused) copy_new_rows<D, KV, WPH>(a, s_meta, s_al, wave, lane);
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
@@ -666,72 +693,30 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
         const int tb = lo_key + min(k1, pe) - ps;  // one past the last
         const bool single = sp.owner(ps) == sp.owner(pe - 1);
-        const int pos0 = SPARSE ? 0 : (a.pos ? ufirst(a.pos[s]) : a.pos_scalar);
-        const int rows_s = a.G * seq_queries(a, s);  // this sequence's live rows
-        const bool live_own = row_live && rb + r_own < rows_s;
-
-        // Query rows -> registers (scaled); rows beyond `rows` stay zero.
-        Acc qr[R][EPL];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (rb + r < rows) {
-                const float* qp = a.q + out_row(a, s, g, rb + r) * D + lane * EPL;
-#pragma unroll
-                for (int e = 0; e < EPL; e += 2) {
-                    const float2 v = *reinterpret_cast<const float2*>(qp + e);
-                    qr[r][e] = (Acc)v.x * (Acc)a.scale;
-                    qr[r][e + 1] = (Acc)v.y * (Acc)a.scale;
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) qr[r][e] = (Acc)0;
-            }
-        }
-        // query position of my row and its first key (sparse: every listed key)
-        const int pq_own = SPARSE ? INT32_MAX : pos0 + a.j0 + (rb + r_own) / a.G;
-        const int ws_own = SPARSE ? 0 : window_start(pq_own, a.window);
-        const int kbeg = SPARSE ? ufirst(a.key_off[s]) : 0;
-
-        Acc m_own = (Acc)-INFINITY, l_own = (Acc)0;
-        Acc acc[R][EPL];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[r][e] = (Acc)0;
-
         const int32_t* trow = a.tables + (size_t)s * a.table_stride;
-        int64_t rbase = 0;  // ring mode: first row of the sequence's ring
-        int r0 = 0;         // ring mode: ring row of key ta
-        if constexpr (RING) {
-            rbase = a.pos ? (int64_t)ufirst(trow[0]) * a.ring_size : a.ring_base;
-            r0 = ta % a.ring_size;
-        }
         const int last_page = (tb - 1) >> a.bs_shift;
-        int pgbase = -kSW;  // page index held by lane 0 of vpg
+        // the sequence's position (sparse: its list's first index) and query count, from
+        // the setup's LDS copy
+        const int kbeg = SPARSE ? ufirst(s_meta[s]) : 0;
+        const int pos0 = SPARSE ? 0 : ufirst(s_meta[s]);
+        const int rows_s = a.G * ufirst(s_meta[B + s]);  // this sequence's live rows
+        const bool live_own = row_live && rb + r_own < rows_s;
+        int pgbase = -kSW;  // page index (sparse: list index) held by lane 0 of vpg
         int vpg = 0;
         bool bad = false;
-        // Fused append: positions [pn_lo, pn_hi) come from k_new / v_new (row r0 + t - pos);
-        // table indices [g_lo, g_hi) are the blocks granted in this call, whose entries the
-        // merge launch writes: their ids come from the free list (g_top - index).
-        int pn_lo = INT32_MAX, pn_hi = INT32_MIN, nr0 = 0;
+        // Fused append: table indices [g_lo, g_hi) are the blocks granted in this call, whose
+        // entries the merge launch writes: their ids come from the free list (g_top - index).
         int g_lo = INT32_MAX, g_hi = INT32_MIN, g_top = 0;
         if (fused) {
-            const int r0 = ufirst(a.nr.tok_off[s]);
-            const int n = ufirst(a.nr.tok_off[s + 1]) - r0;
             const SeqAlloc al = seq_alloc(s_al, B, a.num_blocks, s);
-            if (new_rows_written(ufirst(al.code)) && pos0 >= 0 && n > 0) {
-                pn_lo = pos0;
-                pn_hi = pos0 + n;
-                nr0 = r0;
-            }
             g_lo = ufirst(al.len);
             g_hi = g_lo + ufirst(al.granted);
             g_top = ufirst(al.fc) - 1 - ufirst(al.pref) + g_lo;
         }
-
-        for (int t = ta; t < tb; t += U) {
-            const int tl = min(t + U - 1, tb - 1);
-            if (SPARSE && tl - pgbase >= kSW) {  // pool rows of the next 64 listed keys
+        // Pool rows of the 64 keys from t on: sparse, lane l reads listed key t + l and its
+        // block's table entry; paged, lane l reads the page id of page (t >> bs_shift) + l.
+        auto load_pages = [&](int t) {
+            if constexpr (SPARSE) {
                 pgbase = t;
                 int row = 0;
                 if (t + lane < tb) {
@@ -742,8 +727,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
                     else row = (phys << a.bs_shift) | (key & bs_mask);
                 }
                 vpg = row;
-            }
-            if (ADDR == kAddrPaged && (tl >> a.bs_shift) - pgbase >= kSW) {  // next 64 page ids
+            } else if constexpr (ADDR == kAddrPaged) {
                 pgbase = t >> a.bs_shift;
                 int b = 0;
                 if (pgbase + lane <= last_page) {
@@ -756,6 +740,96 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
                 }
                 vpg = b;
             }
+        };
+
+        // The piece's first loads are all requested before any of them is used, so they
+        // share one round trip: the first 64 page ids (sparse: listed keys) and the query
+        // rows. Every load is issued (indices clamped into range; the values of lanes past
+        // the piece or of rows past `rows` are not used), so no branch separates a load from
+        // its use.
+        int first_raw = 0;
+        if constexpr (SPARSE) {
+            pgbase = ta;
+            first_raw = a.keys[kbeg + min(ta + lane, tb - 1)];
+        } else if constexpr (ADDR == kAddrPaged) {
+            pgbase = ta >> a.bs_shift;
+            const int pg = min(pgbase + lane, last_page);
+            const int32_t* src = (pg >= g_lo && pg < g_hi) ? a.nr.free_list + (g_top - pg) : trow + pg;
+            first_raw = *src;
+        }
+        asm volatile("" ::: "memory");  // issued before the query rows
+        float qraw[R][EPL];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float* qp = a.q + out_row(a, s, g, min(rb + r, rows - 1)) * D + lane * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; e += 2) {
+                const float2 v = *reinterpret_cast<const float2*>(qp + e);
+                qraw[r][e] = v.x;
+                qraw[r][e + 1] = v.y;
+            }
+        }
+        asm volatile("" ::: "memory");  // the query rows go out before the table lookup
+        // (branch-free from here on, so the compiler does not move a load into a branch)
+        if constexpr (SPARSE) {  // the listed keys' table entries (one more round trip)
+            const int key = first_raw;
+            const int blk = key >> a.bs_shift;
+            const bool in_table = key >= 0 && blk < a.table_stride;
+            const int ent = trow[in_table ? blk : 0];
+            const int phys = in_table ? ent : -1;
+            const bool lane_ok = ta + lane < tb;
+            const bool id_ok = phys >= 0 && phys < a.num_blocks;
+            bad = bad || (lane_ok && !id_ok);
+            vpg = lane_ok && id_ok ? (phys << a.bs_shift) | (key & bs_mask) : 0;
+        } else if constexpr (ADDR == kAddrPaged) {
+            const bool lane_ok = pgbase + lane <= last_page;
+            const bool id_ok = first_raw >= 0 && first_raw < a.num_blocks;
+            bad = bad || (lane_ok && !id_ok);
+            vpg = lane_ok && id_ok ? first_raw : 0;
+        }
+        // Query rows -> registers (scaled); rows beyond `rows` are scaled by zero (a product,
+        // not a select: the compiler would move the load into a branch for the select).
+        Acc qr[R][EPL];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const Acc sc = rb + r < rows ? (Acc)a.scale : (Acc)0;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) qr[r][e] = (Acc)qraw[r][e] * sc;
+        }
+        // query position of my row and its first key (sparse: every listed key)
+        const int pq_own = SPARSE ? INT32_MAX : pos0 + a.j0 + (rb + r_own) / a.G;
+        const int ws_own = SPARSE ? 0 : window_start(pq_own, a.window);
+
+        Acc m_own = (Acc)-INFINITY, l_own = (Acc)0;
+        Acc acc[R][EPL];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[r][e] = (Acc)0;
+
+        int64_t rbase = 0;  // ring mode: first row of the sequence's ring
+        int r0 = 0;         // ring mode: ring row of key ta
+        if constexpr (RING) {
+            rbase = a.pos ? (int64_t)ufirst(trow[0]) * a.ring_size : a.ring_base;
+            r0 = ta % a.ring_size;
+        }
+        // Fused append: positions [pn_lo, pn_hi) come from k_new / v_new (row r0 + t - pos).
+        int pn_lo = INT32_MAX, pn_hi = INT32_MIN, nr0 = 0;
+        if (fused) {
+            const int r0 = ufirst(s_meta[2 * B + s]);
+            const int n = ufirst(s_meta[2 * B + s + 1]) - r0;
+            const SeqAlloc al = seq_alloc(s_al, B, a.num_blocks, s);
+            if (new_rows_written(ufirst(al.code)) && pos0 >= 0 && n > 0) {
+                pn_lo = pos0;
+                pn_hi = pos0 + n;
+                nr0 = r0;
+            }
+        }
+
+        for (int t = ta; t < tb; t += U) {
+            const int tl = min(t + U - 1, tb - 1);
+            if (SPARSE && tl - pgbase >= kSW) load_pages(t);  // the next 64 listed keys
+            if (ADDR == kAddrPaged && (tl >> a.bs_shift) - pgbase >= kSW) load_pages(t);  // next 64 pages
             // K and V rows of the batch, all in flight together (tokens past the piece
             // re-read its last row and are masked).
             uint32_t kw[U][NWD], vw[U][NWD];
@@ -898,9 +972,9 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
 typedef __attribute__((address_space(3))) void lds_void;
 // s_waitcnt with only lgkmcnt = 0 (vmcnt and expcnt at their maxima).
 constexpr int kLgkm0 = 0xC07F;
-// LDS of the MFMA kernel: s_pre / s_lo, then one staging area per wave.
+// LDS of the MFMA kernel: s_pre / s_lo / s_meta, then one staging area per wave.
 __host__ __device__ constexpr size_t mfma_stage_offset(int batch) {
-    return ((size_t)(2 * batch + 1) * sizeof(int) + 15) & ~(size_t)15;
+    return ((size_t)stream_seq_ints(batch) * sizeof(int) + 15) & ~(size_t)15;
 }
 constexpr int kSlot = 1024 + 16;  // one token's 1 KiB slice plus bank padding
 __host__ __device__ constexpr size_t mfma_stage_bytes(int tg) { return (size_t)tg * 8 * kSlot; }
@@ -923,6 +997,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     extern __shared__ int smem[];
     int* s_pre = smem;               // [batch + 1]
     int* s_lo = smem + a.batch + 1;  // [batch]
+    int* s_meta = smem + 2 * a.batch + 1;  // [3 batch + 1] (stream_setup)
 
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
@@ -930,7 +1005,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int w = blockIdx.y;
     const int B = a.batch;
 
-    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, nullptr);  // never a fused append
+    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, nullptr);  // never a fused append
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
@@ -967,9 +1042,25 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
         const int tb = lo_key + min(k1, pe) - ps;  // one past the last
         const bool single = sp.owner(ps) == sp.owner(pe - 1);
-        const int pos0 = SPARSE ? 0 : (a.pos ? ufirst(a.pos[s]) : a.pos_scalar);
-        const int rows_s = a.G * seq_queries(a, s);
+        // the sequence's position (sparse: its list's first index) and query count, from
+        // the setup's LDS copy
+        const int kbeg = SPARSE ? ufirst(s_meta[s]) : 0;
+        const int pos0 = SPARSE ? 0 : ufirst(s_meta[s]);
+        const int rows_s = a.G * ufirst(s_meta[B + s]);
+        const int32_t* trow = a.tables + (size_t)s * a.table_stride;
+        const int last_page = (tb - 1) >> a.bs_shift;
 
+        // The piece's first loads are all requested before any of them is used (one round
+        // trip): the first 64 page ids (sparse: listed keys) and the query rows. Each is
+        // issued (indices clamped into range; values past the piece or of rows past `rows`
+        // are not used), so no branch separates a load from its use.
+        int first_raw = 0;
+        if constexpr (SPARSE) {
+            first_raw = a.keys[kbeg + min(ta + lane, tb - 1)];
+        } else if constexpr (ADDR == kAddrPaged) {
+            first_raw = trow[min((ta >> a.bs_shift) + lane, last_page)];
+        }
+        asm volatile("" ::: "memory");  // issued before the query rows
         // this lane's rows 4rg + x: Q slice (B operand), query position, first key
         float4 qf[RG][4];  // fp32: converted at each use, which saves registers
         int pq[RG], wsr[RG];
@@ -980,14 +1071,15 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
             live[rg] = r < rows_s;
             pq[rg] = SPARSE ? INT32_MAX : pos0 + a.j0 + r / a.G;
             wsr[rg] = SPARSE ? 0 : window_start(pq[rg], a.window);
+            const float* qp = a.q + out_row(a, s, g, min(r, rows - 1)) * D + 16 * b + 4 * y;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) qf[rg][q] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (r < rows) {
-                const float* qp = a.q + out_row(a, s, g, r) * D + 16 * b + 4 * y;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) qf[rg][q] = *reinterpret_cast<const float4*>(qp + 64 * q);
-            }
+            for (int q = 0; q < 4; ++q) qf[rg][q] = *reinterpret_cast<const float4*>(qp + 64 * q);
         }
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (4 * rg + x >= rows) qf[rg][q] = make_float4(0.f, 0.f, 0.f, 0.f);
         double m[RG], l[RG], o[RG][4][4];
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
@@ -999,18 +1091,35 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                 for (int e = 0; e < 4; ++e) o[rg][q][e] = 0.0;
         }
 
-        const int32_t* trow = a.tables + (size_t)s * a.table_stride;
         int64_t rbase = 0;  // ring mode: first row of the sequence's ring
         int r0 = 0;         // ring mode: ring row of key ta
         if constexpr (RING) {
             rbase = a.pos ? (int64_t)ufirst(trow[0]) * a.ring_size : a.ring_base;
             r0 = ta % a.ring_size;
         }
-        const int kbeg = SPARSE ? ufirst(a.key_off[s]) : 0;
-        const int last_page = (tb - 1) >> a.bs_shift;
         int pgbase = -kSW;  // page index (sparse: list index) held by lane 0 of vpg
         int vpg = 0;
         bool bad = false;
+        asm volatile("" ::: "memory");  // the query rows go out before the table lookup
+        // (branch-free, so the compiler does not move a load into a branch)
+        if constexpr (SPARSE) {  // the first listed keys' table entries (one more round trip)
+            pgbase = ta;
+            const int key = first_raw;
+            const int blk = key >> a.bs_shift;
+            const bool in_table = key >= 0 && blk < a.table_stride;
+            const int ent = trow[in_table ? blk : 0];
+            const int phys = in_table ? ent : -1;
+            const bool lane_ok = ta + lane < tb;
+            const bool id_ok = phys >= 0 && phys < a.num_blocks;
+            bad = bad || (lane_ok && !id_ok);
+            vpg = lane_ok && id_ok ? (phys << a.bs_shift) | (key & bs_mask) : 0;
+        } else if constexpr (ADDR == kAddrPaged) {
+            pgbase = ta >> a.bs_shift;
+            const bool lane_ok = pgbase + lane <= last_page;
+            const bool id_ok = first_raw >= 0 && first_raw < a.num_blocks;
+            bad = bad || (lane_ok && !id_ok);
+            vpg = lane_ok && id_ok ? first_raw : 0;
+        }
 
         // Batch staging: each token's K and V slices go from global memory straight into
         // this wave's LDS slots (one 1 KiB row per slot, slots kSlot bytes apart), so the
@@ -1392,7 +1501,7 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     const int waves = a.Hkv * WPH < kMaxWaves ? a.Hkv * WPH : kMaxWaves;
     const int threads = waves * kSW;
     const bool fused = ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0;
-    const size_t lds = (size_t)(2 * a.batch + 1 + (fused ? 3 * a.batch + 2 : 0)) * sizeof(int);
+    const size_t lds = (size_t)(stream_seq_ints(a.batch) + (fused ? 3 * a.batch + 2 : 0)) * sizeof(int);
     const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH, ADDR>);
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
