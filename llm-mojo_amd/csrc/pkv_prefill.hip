@@ -6,10 +6,11 @@
 // the cached prefix plus the chunk itself. The chunk's K/V rows are appended first
 // (pkv_append); this kernel then attends all chunk queries in one launch.
 //
-// Workgroup = (tile of 128/G queries, kv head g, sequence), eight waves (two per SIMD, so
-// one wave's softmax overlaps the other's matrix work); wave w owns 16 rows: query block
-// w / G (16 consecutive queries) of q head g*G + w % G. All waves share the K/V tiles of
-// 64 keys staged in LDS. Per key tile (v_mfma_f32_16x16x32_bf16 throughout):
+// Workgroup = (tile of 128/G queries, kv head g, sequence), eight waves, two per SIMD
+// (waves w and w + 4 share one); wave w owns 16 rows: query block w / G (16 consecutive
+// queries) of q head g*G + w % G. All waves share the K/V tiles of 64 keys staged in LDS.
+// The two waves of a SIMD run half a tile apart (scores and softmax of one tile beside
+// the other's PV of the tile before). Per key tile (v_mfma_f32_16x16x32_bf16 throughout):
 //   S^T = K Q^T (A = K rows from LDS, B = Q from registers): row j of the wave lands in
 //     lanes j, j+16, j+32, j+48, each holding 4 of every 16 keys, so the online softmax
 //     needs two cross-lane steps (permlane16 / permlane32 swaps);
@@ -28,6 +29,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "pkv_internal.h"
 
@@ -51,9 +54,13 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kKTile = kKT * kD;    // elements per K buffer (32 KiB)
 constexpr int kVTile = kKT * kD;    // elements per V buffer (32 KiB)
 constexpr int kVAhead = 6;          // PV operands requested ahead of the matrix cores
-// __builtin_amdgcn_sched_group_barrier instruction classes
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ inline void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 struct PrefillArgs {
     const uint16_t* q;  // bf16 [rows][Hq][D]
@@ -75,8 +82,6 @@ struct PrefillArgs {
     float* out;  // fp32 [rows][Hq][D]
 };
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
 
 __device__ inline float swap32_max(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -96,25 +101,70 @@ __device__ inline float swap16_sum(float x) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
+// 16 bytes per lane from global memory straight into LDS at dst + 16 * lane (dst uniform).
+__device__ inline void copy16_to_lds(const uint16_t* src, uint16_t* dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
+}
+
+// LDS reads the compiler does not track. It cannot tell which LDS words a direct-to-LDS
+// copy in flight writes, so before any read it can see it waits for every copy (vmcnt),
+// including the ones just issued for a later tile. The caller waits for these reads with
+// lgkm_wait, which ties the values, so no use is scheduled above the wait.
+// addr: an LDS byte address; OFF: a constant byte offset (< 65536).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+template <int OFF>
+__device__ inline i32x4 lds_read_b128(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    i32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
 // ds_read_b64_tr_b16 (checked on the device): inside each 16-lane group, output lane j
-// element e is element j % 4 of what input lane 4e + j / 4 addressed. With input lane a
-// addressing dims 4(a % 4) .. +3 of key k0 + a / 4, output lane j holds dim j of keys
-// k0 .. k0 + 3.
-__device__ inline s16x4 read_tr(const uint16_t* p) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+// element e is element j % 4 of what input lane 4e + j / 4 addressed.
+template <int OFF>
+__device__ inline i32x2 lds_read_tr16(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    i32x2 v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+// s_waitcnt lgkmcnt(N): at most N of this wave's LDS reads still in flight (they complete
+// in order), so every read issued before the last N has landed.
+template <int N>
+__device__ inline void lgkm_wait(i32x4& a) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt");
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(N));
+}
+template <int N>
+__device__ inline void lgkm_wait(i32x4& a, i32x4& b, i32x4& c, i32x4& d) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt");
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(N));
+}
+
+template <int P>
+using Par = std::integral_constant<int, P>;
+
+// f(Par<I>{}), f(Par<I + 1>{}), ..., f(Par<N - 1>{}): constant indices for template offsets.
+template <int I, int N, typename F>
+__device__ inline void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(Par<I>{});
+        static_for<I + 1, N>(f);
+    }
 }
 
 template <int G>
 __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     constexpr int QB = 128 / G;  // queries per workgroup
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    uint16_t* sK = smem;                    // [2][kKTile]
-    uint16_t* sV = smem + 2 * kKTile;       // [2][kVTile]
-    // element offset of each key's head slice in the pools, per staged tile
-    int64_t* s_off = reinterpret_cast<int64_t*>(smem + 2 * kKTile + 2 * kVTile);  // [4][kKT]
-    int* s_bad = reinterpret_cast<int*>(s_off + 4 * kKT);
+    // Static arrays indexed by constant buffer numbers, so the compiler can tell a
+    // direct-to-LDS copy into one buffer from reads of another and does not wait for the
+    // copy before those reads.
+    __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKTile];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[2][kVTile];
+    __shared__ int s_bad[kNT / 64];  // per wave: a table entry of the range is outside the pool
 
     const int s = blockIdx.z;
     const int g = blockIdx.y;
@@ -168,52 +218,56 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     const int kb0 = k_lo & ~(kKT - 1);
     const int ntiles = (k_hi - kb0) / kKT + 1;
     const int32_t* trow = a.tables + (size_t)s * a.table_stride;
-    const size_t head_off = (size_t)g * kD;
-    const size_t row_elems = (size_t)a.Hkv * kD;
     const int bs_mask = (1 << a.bs_shift) - 1;
 
-    // Pool offsets of the keys of tile t -> s_off[t % 4] (threads 0..63). Keys outside
-    // [k_lo, k_hi] re-read a valid row and are masked.
-    auto stage_rows = [&](int t) {
-        if (tid < kKT && t < ntiles) {
-            const int kpos = min(max(kb0 + t * kKT + tid, k_lo), k_hi);
-            int b = trow[kpos >> a.bs_shift];
-            if (b < 0 || b >= a.num_blocks) {
-                *s_bad = 1;
-                b = 0;
-            }
-            const int row = (b << a.bs_shift) | (kpos & bs_mask);
-            s_off[(t & 3) * kKT + tid] = (int64_t)row * (int64_t)row_elems + (int64_t)head_off;
-        }
-    };
-    // K and V tiles t -> sK[t % 2], sV[t % 2] straight from global memory into LDS: each
-    // wave instruction fills two key rows (1 KiB), eight waves x 4 instructions = 64 rows.
-    // The wave's four key offsets are read from s_off once, for K and V both. Lane i loads
-    // the global chunk that belongs at 16-byte position i % 32 of its row: for K that is
-    // chunk (i % 32) ^ (key & 15); for V, LDS position p of key row k holds global chunk
+    // Tile copies. Wave w copies keys 8w .. 8w+7 of a tile, which lie in one block
+    // (block_size >= 8): instruction j (of four) fills key rows 8w + 2j (lanes 0-31) and
+    // 8w + 2j + 1 (lanes 32-63), 1 KiB straight from global memory into LDS. The block's
+    // table entry is one load per wave and tile (the same address in every lane), made a
+    // step before the copies that use it; a copy's address is that block's first row
+    // (scalar) plus a per-lane offset that is the same for every tile. Keys outside
+    // [k_lo, k_hi] (and tiles past the last) read rows of a valid block and are masked or
+    // never read; a bad entry reads block 0 (the whole range was checked up front).
+    // K: lane i loads the global chunk that belongs at 16-byte position i % 32 of its row,
+    // i.e. chunk (i % 32) ^ (key & 15). V: LDS position p of key row k holds global chunk
     // 2 * ((p / 2) ^ (k & 15)) + p % 2 (the 32-byte chunk swizzle).
-    auto issue_kv = [&](int t) {
-        uint16_t* kdst = sK + (t & 1) * kKTile;
-        uint16_t* vdst = sV + (t & 1) * kVTile;
-        const int64_t* offs = s_off + (t & 3) * kKT;
-        int64_t ko[4];
+    const uint32_t row_bytes = (uint32_t)a.Hkv * kD * 2;
+    uint32_t k_voff[4], v_voff[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ko[j] = offs[wave * 8 + 2 * j + (lane >> 5)];
+    for (int j = 0; j < 4; ++j) {
+        const int kk = (8 * wave + 2 * j + (lane >> 5)) & 15, p16 = lane & 31;
+        const uint32_t r = (uint32_t)(2 * j + (lane >> 5)) * row_bytes;
+        k_voff[j] = r + 16 * (p16 ^ kk);
+        v_voff[j] = r + 16 * ((((p16 >> 1) ^ kk) << 1) | (p16 & 1));
+    }
+    auto blk_ptr = [&](int t) {
+        return trow + (min(max(kb0 + t * kKT + 8 * wave, k_lo), k_hi) >> a.bs_shift);
+    };
+    // Byte offset of the first row this wave copies in tile t, from its block's entry e.
+    auto tile_off = [&](int t, int e) -> uint64_t {
+        e = __builtin_amdgcn_readfirstlane(e);
+        const int b = (uint32_t)e < (uint32_t)a.num_blocks ? e : 0;
+        const uint32_t row = ((uint32_t)b << a.bs_shift) | ((kb0 + t * kKT + 8 * wave) & bs_mask);
+        return (uint64_t)row * row_bytes + (uint64_t)g * (kD * 2);
+    };
+    // The entry load untracked by the compiler (its waits would cover every copy issued
+    // after it): it completes with the step's barrier wait, which ties its value.
+    auto load_blk_async = [&](int t, int& e) {
+        asm volatile("global_load_dword %0, %1, off" : "=v"(e) : "v"(blk_ptr(t)));
+    };
+    auto issue_k = [&](auto PAR, int t, int e) {
+        const char* base = reinterpret_cast<const char*>(a.k_pool) + tile_off(t, e);
+        uint16_t* dst = sK[decltype(PAR)::value] + 8 * wave * kD;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int key = wave * 8 + 2 * j + (lane >> 5);
-            const int c = (lane & 31) ^ (key & 15);
-            __builtin_amdgcn_global_load_lds(a.k_pool + ko[j] + 8 * c,
-                                             (lds_void*)(kdst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
-        }
+        for (int j = 0; j < 4; ++j)
+            copy16_to_lds(reinterpret_cast<const uint16_t*>(base + k_voff[j]), dst + 2 * j * kD);
+    };
+    auto issue_v = [&](auto PAR, int t, int e) {
+        const char* base = reinterpret_cast<const char*>(a.v_pool) + tile_off(t, e);
+        uint16_t* dst = sV[decltype(PAR)::value] + 8 * wave * kD;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int key = wave * 8 + 2 * j + (lane >> 5);
-            const int p16 = lane & 31;
-            const int c = ((((p16 >> 1) ^ (key & 15)) << 1) | (p16 & 1));
-            __builtin_amdgcn_global_load_lds(a.v_pool + ko[j] + 8 * c,
-                                             (lds_void*)(vdst + (wave * 8 + 2 * j) * kD), 16, 0, 0);
-        }
+        for (int j = 0; j < 4; ++j)
+            copy16_to_lds(reinterpret_cast<const uint16_t*>(base + v_voff[j]), dst + 2 * j * kD);
     };
 
     // Q as the B operand of S^T: lane holds Q[row][32c + 8*grp .. +7] for c = 0..7.
@@ -232,57 +286,44 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     for (int u = 0; u < 16; ++u) o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY;  // reference max (log2 domain) of this lane's row
     float l = 0.f;        // this lane's share of the running sum (its 16 of every 64 keys)
+    bf16x8 ph[2], pl[2];  // P = P_hi + P_lo of the last scored tile, as PV's B operands
 
-    // prologue: tile 0 staged, tile 1's and 2's offsets known
-    if (tid == 0) *s_bad = 0;
-    stage_rows(0);
-    stage_rows(1);
-    stage_rows(2);
-    __syncthreads();
-    issue_kv(0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    for (int t = 0; t < ntiles; ++t) {
+    // S^T = K Q^T for tile t, then the online softmax and the P split.
+    auto score = [&](auto PAR, int t) {
+        constexpr int par = decltype(PAR)::value;
         const int kb = kb0 + t * kKT;
-        if (t + 1 < ntiles) issue_kv(t + 1);
-        const uint16_t* cK = sK + (t & 1) * kKTile;
-        const uint16_t* cV = sV + (t & 1) * kVTile;
-
-        // S^T = K Q^T: four 16-key sub-tiles (independent accumulators). The K operands of
-        // 32-dim step c + 2 are requested while step c runs on the matrix cores; the
-        // scheduling groups below keep that order (the compiler otherwise waits for each
-        // read right after issuing it).
+        // Four 16-key sub-tiles (independent accumulators). The K operand of sub-tile u,
+        // 32-dim step c is row 16u + l16, chunk (4c + grp) ^ l16, i.e. byte
+        // 8192u + 512 l16 + 16 (grp ^ (l16 & 3)) + 64 ((c & 3) ^ (l16 >> 2)) + 256 (c >> 2):
+        // four per-lane bases (c & 3) and constant offsets. The operands of step c + 2 are
+        // requested while step c runs on the matrix cores.
         f32x4 st[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) st[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto kop = [&](int u, int c) -> bf16x8 {
-            const int key = 16 * u + l16;
-            const int ch = (4 * c + grp) ^ (key & 15);
-            return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(&cK[key * kD + 8 * ch]));
+        const uint32_t k_lane = lds_addr(sK[0]) + 512 * l16 + 16 * (grp ^ (l16 & 3));
+        uint32_t k_addr[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) k_addr[q] = k_lane + 64 * (q ^ (l16 >> 2));
+        i32x4 ka[3][4];
+        auto kread = [&](auto C) {
+            constexpr int c = decltype(C)::value;
+            static_for<0, 4>([&](auto U) {
+                constexpr int u = decltype(U)::value;
+                ka[c % 3][u] = lds_read_b128<par * 2 * kKTile + 8192 * u + 256 * (c >> 2)>(k_addr[c & 3]);
+            });
         };
-        bf16x8 ka[3][4];
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int u = 0; u < 4; ++u) ka[c][u] = kop(u, c);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            if (c + 2 < 8) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) ka[(c + 2) % 3][u] = kop(u, c + 2);
-            }
+        kread(Par<0>{});
+        kread(Par<1>{});
+        static_for<0, 8>([&](auto C) {
+            constexpr int c = decltype(C)::value;
+            if constexpr (c + 2 < 8) kread(Par<c + 2>{});
+            constexpr int ahead = c + 2 < 8 ? 8 : (c + 1 < 8 ? 4 : 0);  // reads issued after step c's
+            lgkm_wait<ahead>(ka[c % 3][0], ka[c % 3][1], ka[c % 3][2], ka[c % 3][3]);
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[c % 3][u], qreg[c], st[u], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
-#pragma unroll
-        for (int c = 0; c < 6; ++c) {
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+                st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[c % 3][u]),
+                                                               qreg[c], st[u], 0, 0, 0);
+        });
         // Tiles that straddle a row's causal edge or window start get -inf outside
         // [window_start(qpos), qpos]; st[u][r] is key kb + 16u + 4grp + r. Rows past the
         // chunk are never written, so they need no mask.
@@ -315,7 +356,6 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         // to bf16 (its top 16 bits, so two of them pack with one permute) and P_lo the exact
         // remainder p - P_hi rounded to nearest: |p - P_hi - P_lo| <= 2^-16 p.
         float lsum[2] = {0.f, 0.f};
-        bf16x8 ph[2], pl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -338,46 +378,124 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int u = 0; u < 16; ++u) o[u] *= alpha;
         }
-        // O^T += V^T P^T: 16 d-tiles x 2 steps of 32 keys, hi then lo; the V operand of
-        // (step ks, d-tile u) is dims 16u + l16 of keys 32ks + 4grp + 0..3 and
-        // 32ks + 16 + 4grp + 0..3 (elements 0..3 and 4..7), two transposed reads.
-        auto vop = [&](int ks, int u) -> bf16x8 {
-            const int kr = 32 * ks + 4 * grp + (l16 >> 2);  // key this lane addresses
-            const int dq = 4 * (l16 & 3);                    // its dims within the 16-dim tile
-            const s16x4 lo = read_tr(&cV[kr * kD + ((u ^ (kr & 15)) << 4) + dq]);
-            const int kr2 = kr + 16;
-            const s16x4 hi = read_tr(&cV[kr2 * kD + ((u ^ (kr2 & 15)) << 4) + dq]);
-            const s16x8 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            return __builtin_bit_cast(bf16x8, v);
+    };
+
+    // O^T += V^T P^T for tile t: 16 d-tiles x 2 steps of 32 keys, hi then lo; the V operand
+    // of (step ks, d-tile u) is dims 16u + l16 of keys 32ks + 4grp + 0..3 and
+    // 32ks + 16 + 4grp + 0..3 (elements 0..3 and 4..7), two transposed reads. The 32
+    // (step, d-tile) operands run as one pipeline, kVAhead operands requested ahead of the
+    // matrix cores (across the step boundary too).
+    auto accumulate = [&](auto PAR) {
+        constexpr int par = decltype(PAR)::value;
+        // Operand (ks, u): with z = 4 grp + l16 / 4 (the key this lane addresses, mod 16),
+        // byte 512 (32 ks + z) + 32 (u ^ z) + 8 (l16 & 3), and 16 keys (8192 bytes) further
+        // for its second half.
+        const int z = 4 * grp + (l16 >> 2);
+        const uint32_t v_lane = lds_addr(sV[0]) + 512 * z + 8 * (l16 & 3);
+        auto vread = [&](auto I) -> i32x4 {
+            constexpr int i = decltype(I)::value, ks = i / 16, u = i % 16;
+            constexpr int off = par * 2 * kVTile + 16384 * ks;
+            const uint32_t ad = v_lane + ((u ^ z) << 5);
+            const i32x2 lo = lds_read_tr16<off>(ad);
+            const i32x2 hi = lds_read_tr16<off + 8192>(ad);
+            return i32x4{lo.x, lo.y, hi.x, hi.y};
         };
-        // The 32 (step, d-tile) operands run as one pipeline, kVAhead operands requested
-        // ahead of the matrix cores (across the step boundary too), and the scheduling
-        // groups interleave each operand's two reads with two MFMAs.
-        {
-            bf16x8 va[kVAhead];
-#pragma unroll
-            for (int i = 0; i < kVAhead; ++i) va[i] = vop(i / 16, i % 16);
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const int ks = i / 16, u = i % 16;
-                const bf16x8 cur = va[i % kVAhead];
-                if (i + kVAhead < 32) va[i % kVAhead] = vop((i + kVAhead) / 16, (i + kVAhead) % 16);
-                o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, ph[ks], o[u], 0, 0, 0);
-                o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, pl[ks], o[u], 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kVAhead, 1);
-#pragma unroll
-            for (int i = 0; i < 32 - kVAhead; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 1);
-                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
-            }
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kVAhead, 1);
+        i32x4 va[kVAhead];
+        static_for<0, kVAhead>([&](auto I) { va[decltype(I)::value] = vread(I); });
+        static_for<0, 32>([&](auto I) {
+            constexpr int i = decltype(I)::value, ks = i / 16, u = i % 16;
+            i32x4 cur = va[i % kVAhead];
+            if constexpr (i + kVAhead < 32) va[i % kVAhead] = vread(Par<i + kVAhead>{});
+            constexpr int later = 2 * (31 - i < kVAhead ? 31 - i : kVAhead);  // reads issued after
+            lgkm_wait<later>(cur);
+            const bf16x8 vb = __builtin_bit_cast(bf16x8, cur);
+            o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb, ph[ks], o[u], 0, 0, 0);
+            o[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb, pl[ks], o[u], 0, 0, 0);
+        });
+    };
+
+    // Prologue: Q, the table entries of tiles 0 and 1, the check of every table entry of
+    // the range (one load per thread per 512 blocks), tile 0's K and V.
+    int blk[2];  // table entry of this wave's block in tiles t (blk[t % 2]) and t + 1
+    blk[0] = *blk_ptr(0);
+    blk[1] = *blk_ptr(1);
+    int bad_local = 0;
+    {
+        const int b_lo = k_lo >> a.bs_shift, nblk = (k_hi >> a.bs_shift) - b_lo + 1;
+        for (int i = tid; i < nblk; i += kNT) {
+            const int e = trow[b_lo + i];
+            bad_local |= (e < 0 || e >= a.num_blocks);
         }
-        stage_rows(t + 3);
-        __builtin_amdgcn_s_waitcnt(0);  // tile t+1's direct-to-LDS K loads have landed
-        __syncthreads();
     }
-    const bool bad = *s_bad != 0;
+    issue_k(Par<0>{}, 0, blk[0]);
+    issue_v(Par<0>{}, 0, blk[0]);
+    const int bad_wave = __any(bad_local);
+    if (lane == 0) s_bad[wave] = bad_wave;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    bool bad = false;
+#pragma unroll
+    for (int w = 0; w < kNT / 64; ++w) bad |= s_bad[w] != 0;
+
+    // Ping-pong over the two waves of each SIMD (waves w and w + 4). The workgroup's
+    // barriers split time into steps; per tile t the lead waves (0-3) score tile t in step
+    // 2t and accumulate it in step 2t + 1, the trailing waves (4-7) one step later. So
+    // while one wave of a SIMD runs its softmax on the vector ALUs, the other's PV keeps
+    // the matrix cores busy. Copies (every wave copies its eight keys of each):
+    //   step 2t:     K of tile t + 1 -> sK[(t + 1) % 2] (its old tile t - 1 was last
+    //                scored in step 2t - 1);
+    //   step 2t + 1: the table entries of tile t + 2, then V of tile t + 1
+    //                -> sV[(t + 1) % 2] (tile t - 1 was last accumulated in step 2t).
+    // Before the barrier that ends a step, each wave waits for its copies of the step
+    // before (vmcnt 4: the four copies just issued stay in flight), so every tile is in
+    // LDS one step before its first reader. Copies past the last tile re-read valid rows
+    // into buffers nobody reads again. The barriers carry no fence (a fence would wait for
+    // the copies just issued).
+    auto step_barrier = [&]() {
+        asm volatile("s_waitcnt vmcnt(4)"
+                     : "+v"(blk[0]), "+v"(blk[1])
+                     :
+                     : "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    constexpr int kLead = 4;
+    if (wave < kLead) {
+        auto lead = [&](auto PAR, int t) {
+            constexpr int par = decltype(PAR)::value;
+            issue_k(Par<par ^ 1>{}, t + 1, blk[par ^ 1]);  // step 2t
+            score(PAR, t);
+            step_barrier();
+            load_blk_async(t + 2, blk[par]);  // step 2t + 1
+            issue_v(Par<par ^ 1>{}, t + 1, blk[par ^ 1]);
+            accumulate(PAR);
+            step_barrier();
+        };
+        for (int t = 0; t < ntiles; t += 2) {
+            lead(Par<0>{}, t);
+            if (t + 1 < ntiles) lead(Par<1>{}, t + 1);
+        }
+    } else {
+        issue_k(Par<1>{}, 1, blk[1]);  // step 0
+        step_barrier();
+        auto trail = [&](auto PAR, int t) {
+            constexpr int par = decltype(PAR)::value;
+            load_blk_async(t + 2, blk[par]);  // step 2t + 1
+            issue_v(Par<par ^ 1>{}, t + 1, blk[par ^ 1]);
+            score(PAR, t);
+            step_barrier();
+            issue_k(PAR, t + 2, blk[par]);  // step 2t + 2
+            accumulate(PAR);
+            if (t + 1 < ntiles) step_barrier();
+        };
+        for (int t = 0; t < ntiles; t += 2) {
+            trail(Par<0>{}, t);
+            if (t + 1 < ntiles) trail(Par<1>{}, t + 1);
+        }
+    }
+    // No copy may still be writing LDS when the workgroup's last wave ends.
+    __builtin_amdgcn_s_waitcnt(0);
+
     const float l_row = swap32_sum(swap16_sum(l));
     const float inv = 1.f / (l_row + 1e-10f);
     if (live) {
@@ -393,9 +511,6 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         }
     }
 }
-
-// Dynamic LDS of prefill_kernel: two K and two V^T tiles, four key-offset tables, a flag.
-constexpr size_t kPrefillLds = (size_t)(2 * kKTile + 2 * kVTile) * 2 + 4 * kKT * 8 + 16;
 
 }  // namespace
 }  // namespace pkv
@@ -418,6 +533,8 @@ int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void
     if (p->ring_size > 0)
         return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: paged pools only (ring_size 0)");
     if (p->head_dim != kD) return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: head_dim 256 only");
+    if (p->block_size < 8)
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: block_size must be at least 8");
     const int G = p->num_heads / p->num_kv_heads;
     if (G != 1 && G != 2 && G != 4)
         return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: num_heads / num_kv_heads must be 1, 2 or 4");
@@ -451,17 +568,10 @@ int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void
     a.qtiles = (max_q + qb - 1) / qb;
     dim3 grid(a.qtiles, p->num_kv_heads, batch);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const void* fn = G == 1 ? reinterpret_cast<const void*>(&prefill_kernel<1>)
-                   : G == 2 ? reinterpret_cast<const void*>(&prefill_kernel<2>)
-                            : reinterpret_cast<const void*>(&prefill_kernel<4>);
-    // Above 64 KiB of dynamic LDS the kernel must opt in (once per kernel and device).
-    static_assert(kPrefillLds <= 160 * 1024, "LDS budget of one CU");
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrefillLds) !=
-        hipSuccess)
-        return fail(PKV_ERR_HIP, "pkv_prefill: could not reserve the kernel's LDS");
-    if (G == 1) hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kNT), kPrefillLds, st, a);
-    else if (G == 2) hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kNT), kPrefillLds, st, a);
-    else hipLaunchKernelGGL(prefill_kernel<4>, grid, dim3(kNT), kPrefillLds, st, a);
+    // The kernel's four 32 KiB K/V buffers are static LDS (128 KiB of the CU's 160 KiB).
+    if (G == 1) hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kNT), 0, st, a);
+    else if (G == 2) hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kNT), 0, st, a);
+    else hipLaunchKernelGGL(prefill_kernel<4>, grid, dim3(kNT), 0, st, a);
     return check_launch("pkv_prefill");
 }
 

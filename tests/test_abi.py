@@ -115,6 +115,15 @@ def test_ring_mode_rejections():
     assert L.pkv_paged_attention_layer(*full_causal) == lib.PKV_ERR_INVALID
 
 
+def test_prefill_block_size_below_8_rejected_before_launch():
+    """The prefill kernel copies each wave's eight keys of a tile from one block."""
+    L = lib.load()
+    small = _params(kv_dtype=1, block_size=4, num_blocks=64)
+    assert L.pkv_prefill(None, ctypes.byref(small), 1, 1, 1, 1, 4, 1, 1, 16, 1, 100, 1) \
+        == lib.PKV_ERR_UNSUPPORTED
+    assert b"block_size" in L.pkv_last_error()
+
+
 def test_q4_matmul_rejections_before_launch():
     L = lib.load()
     assert L.pkv_q4_matmul(None, 16, 4, 16, 100, 8, 1, 16, 16, 1 << 20) == lib.PKV_ERR_INVALID
