@@ -54,6 +54,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kKTile = kKT * kD;    // elements per K buffer (32 KiB)
 constexpr int kVTile = kKT * kD;    // elements per V buffer (32 KiB)
 constexpr int kVAhead = 6;          // PV operands requested ahead of the matrix cores
+constexpr int kKAhead = 2;          // QK^T steps whose K operands are requested ahead
+static_assert(2 * kVAhead < 16 && 4 * kKAhead < 16, "LDS reads in flight fit lgkmcnt");
 
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima).
 template <int N>
@@ -304,24 +306,24 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
         uint32_t k_addr[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) k_addr[q] = k_lane + 64 * (q ^ (l16 >> 2));
-        i32x4 ka[3][4];
+        i32x4 ka[kKAhead + 1][4];
         auto kread = [&](auto C) {
             constexpr int c = decltype(C)::value;
             static_for<0, 4>([&](auto U) {
                 constexpr int u = decltype(U)::value;
-                ka[c % 3][u] = lds_read_b128<par * 2 * kKTile + 8192 * u + 256 * (c >> 2)>(k_addr[c & 3]);
+                ka[c % (kKAhead + 1)][u] =
+                    lds_read_b128<par * 2 * kKTile + 8192 * u + 256 * (c >> 2)>(k_addr[c & 3]);
             });
         };
-        kread(Par<0>{});
-        kread(Par<1>{});
+        static_for<0, kKAhead>(kread);
         static_for<0, 8>([&](auto C) {
-            constexpr int c = decltype(C)::value;
-            if constexpr (c + 2 < 8) kread(Par<c + 2>{});
-            constexpr int ahead = c + 2 < 8 ? 8 : (c + 1 < 8 ? 4 : 0);  // reads issued after step c's
-            lgkm_wait<ahead>(ka[c % 3][0], ka[c % 3][1], ka[c % 3][2], ka[c % 3][3]);
+            constexpr int c = decltype(C)::value, slot = c % (kKAhead + 1);
+            if constexpr (c + kKAhead < 8) kread(Par<c + kKAhead>{});
+            constexpr int later = 4 * (7 - c < kKAhead ? 7 - c : kKAhead);  // reads issued after step c's
+            lgkm_wait<later>(ka[slot][0], ka[slot][1], ka[slot][2], ka[slot][3]);
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[c % 3][u]),
+                st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[slot][u]),
                                                                qreg[c], st[u], 0, 0, 0);
         });
         // Tiles that straddle a row's causal edge or window start get -inf outside

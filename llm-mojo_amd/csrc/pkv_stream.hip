@@ -283,28 +283,38 @@ __device__ inline float exp_acc(float x) { return expf(x); }
 
 // ---- loads ------------------------------------------------------------------------
 
-// NW 32-bit words per lane from a lane-contiguous run.
-template <int NW>
+// NW 32-bit words per lane from a lane-contiguous run. NT: non-temporal loads (NT bit),
+// for rows that one wave alone reads; rows that several waves of a head read in turn
+// (WPH > 1) must stay in the L2 for the later waves (NT loads there doubled the LSA
+// launch's time).
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+template <bool NT, typename T>
+__device__ inline T ld(const PKV_GLOBAL T* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <int NW, bool NT>
 __device__ inline void load_words(gchar* p, uint32_t (&w)[NW]) {
-    typedef const PKV_GLOBAL uint4 g4;
-    typedef const PKV_GLOBAL uint2 g2;
+    typedef const PKV_GLOBAL u32x4v g4;
+    typedef const PKV_GLOBAL u32x2v g2;
     typedef const PKV_GLOBAL uint32_t g1;
     if constexpr (NW % 4 == 0) {
 #pragma unroll
         for (int i = 0; i < NW / 4; ++i) {
-            const uint4 v = reinterpret_cast<g4*>(p)[i];
+            const u32x4v v = ld<NT>(reinterpret_cast<g4*>(p) + i);
             w[4 * i + 0] = v.x;
             w[4 * i + 1] = v.y;
             w[4 * i + 2] = v.z;
             w[4 * i + 3] = v.w;
         }
     } else if constexpr (NW == 2) {
-        const uint2 v = *reinterpret_cast<g2*>(p);
+        const u32x2v v = ld<NT>(reinterpret_cast<g2*>(p));
         w[0] = v.x;
         w[1] = v.y;
     } else {
         static_assert(NW == 1, "words per lane");
-        w[0] = *reinterpret_cast<g1*>(p);
+        w[0] = ld<NT>(reinterpret_cast<g1*>(p));
     }
 }
 
@@ -852,15 +862,15 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
                     const size_t off = fresh ? (size_t)(nr0 + (tt - pn_lo)) * row_bytes : row_off(tt);
                     const char* kb = fresh ? a.nr.k_new + (size_t)g * D * kElt : kbase;
                     const char* vb = fresh ? a.nr.v_new + (size_t)g * D * kElt : vbase;
-                    load_words<NWD>(uniform_ptr(kb + off) + lane_off, kw[u]);
-                    load_words<NWD>(uniform_ptr(vb + off) + lane_off, vw[u]);
+                    load_words<NWD, WPH == 1>(uniform_ptr(kb + off) + lane_off, kw[u]);
+                    load_words<NWD, WPH == 1>(uniform_ptr(vb + off) + lane_off, vw[u]);
                 }
             } else {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const size_t off = row_off(min(t + u, tb - 1));
-                    load_words<NWD>(uniform_ptr(kbase + off) + lane_off, kw[u]);
-                    load_words<NWD>(uniform_ptr(vbase + off) + lane_off, vw[u]);
+                    load_words<NWD, WPH == 1>(uniform_ptr(kbase + off) + lane_off, kw[u]);
+                    load_words<NWD, WPH == 1>(uniform_ptr(vbase + off) + lane_off, vw[u]);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);  // keep all 2U loads ahead of the math
@@ -1167,9 +1177,9 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                     off = (((size_t)pg << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
                 }
                 __builtin_amdgcn_global_load_lds(uniform_ptr(kbase + off) + 16 * lane,
-                                                 (lds_void*)(buf + (2 * j) * kSlot), 16, 0, 0);
+                                                 (lds_void*)(buf + (2 * j) * kSlot), 16, 0, kCpolNT);
                 __builtin_amdgcn_global_load_lds(uniform_ptr(vbase + off) + 16 * lane,
-                                                 (lds_void*)(buf + (2 * j + 1) * kSlot), 16, 0, 0);
+                                                 (lds_void*)(buf + (2 * j + 1) * kSlot), 16, 0, kCpolNT);
             }
         };
 
