@@ -285,33 +285,44 @@ __device__ inline uint32_t pack_bf16x2(float x0, float x1) {
     return (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
 }
 
+// E values of a pool row or of q_out, as non-temporal stores (written once by this step).
 template <int E>
 __device__ inline void store_row(void* base, size_t elem, bool bf16, const float (&x)[E]) {
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    typedef float f4v __attribute__((ext_vector_type(4)));
     if (bf16) {
         uint16_t* d = static_cast<uint16_t*>(base) + elem;
         if constexpr (E == 2) {
-            *reinterpret_cast<uint32_t*>(d) = pack_bf16x2(x[0], x[1]);
+            __builtin_nontemporal_store(pack_bf16x2(x[0], x[1]), reinterpret_cast<uint32_t*>(d));
         } else {
-            *reinterpret_cast<uint2*>(d) = make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]));
+            __builtin_nontemporal_store(u2v{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])}, reinterpret_cast<u2v*>(d));
         }
     } else {
         float* d = static_cast<float*>(base) + elem;
         if constexpr (E == 2) {
-            *reinterpret_cast<float2*>(d) = make_float2(x[0], x[1]);
+            __builtin_nontemporal_store(f2v{x[0], x[1]}, reinterpret_cast<f2v*>(d));
         } else {
-            *reinterpret_cast<float4*>(d) = make_float4(x[0], x[1], x[2], x[3]);
+            __builtin_nontemporal_store(f4v{x[0], x[1], x[2], x[3]}, reinterpret_cast<f4v*>(d));
         }
     }
 }
 
-template <int E>
+// E fp32 values; NT: a non-temporal load (the projections of a token are read once).
+template <int E, bool NT = false>
 __device__ inline void load_vec(const float* p, float (&x)[E]) {
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    typedef float f4v __attribute__((ext_vector_type(4)));
     if constexpr (E == 2) {
-        const float2 v = *reinterpret_cast<const float2*>(p);
+        f2v v;
+        if constexpr (NT) v = __builtin_nontemporal_load(reinterpret_cast<const f2v*>(p));
+        else v = *reinterpret_cast<const f2v*>(p);
         x[0] = v.x;
         x[1] = v.y;
     } else {
-        const float4 v = *reinterpret_cast<const float4*>(p);
+        f4v v;
+        if constexpr (NT) v = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
+        else v = *reinterpret_cast<const f4v*>(p);
         x[0] = v.x;
         x[1] = v.y;
         x[2] = v.z;
@@ -409,8 +420,8 @@ __global__ __launch_bounds__(kQkvWaves * kWave) void qkv_append_kernel(QkvArgs a
             const int it = first + j * kQkvWaves;
             if (it < slots) {
                 const float* src = src_of(it * HS + sub);
-                load_vec<EL>(src + hl * EL, f1[j]);
-                load_vec<EL>(src + HALF + hl * EL, f2[j]);
+                load_vec<EL, true>(src + hl * EL, f1[j]);
+                load_vec<EL, true>(src + HALF + hl * EL, f2[j]);
             }
         }
     };
