@@ -86,6 +86,19 @@ def test_prefill_small_ragged(gpu, hq, hkv, window):
     _run(w, q_counts=[1, 17, 64, 130, 200])
 
 
+@pytest.mark.parametrize("bs", [8, 32, 64])
+def test_prefill_block_sizes(gpu, bs):
+    """Each wave copies eight keys of a tile from one block: block sizes 8 (exactly one
+    block), 32 and 64 (a wave's keys start inside a block)."""
+    print(f"[prefill] block_size {bs}", flush=True)
+
+    class Chunk(PrefillChunk):
+        BS = bs
+
+    w = Chunk(seed=bs, batch=4, chunk=160, prefix_max=400, prefix=[0, 9, 77, 400])
+    _run(w, q_counts=[3, 64, 100, 160])
+
+
 def test_prefill_config4_full(gpu):
     print("[prefill] config 4: 4 x 2048-token chunks over prefixes up to 6144", flush=True)
     w = PrefillChunk(seed=4)
