@@ -168,9 +168,21 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sV[2][kVTile];
     __shared__ int s_bad[kNT / 64];  // per wave: a table entry of the range is outside the pool
 
-    const int s = blockIdx.z;
-    const int g = blockIdx.y;
-    const int tile = a.qtiles - 1 - (int)blockIdx.x;  // long (late) tiles first
+    // Workgroup order. The hardware hands out workgroup ids in increasing order, round-robin
+    // over the eight XCDs (id mod 8), and each XCD gives its next id to whichever of its CUs
+    // frees first. Ids run over (sequence, tile from the last to the first, kv head) with the
+    // kv head fastest, so every XCD receives the same run of tile lengths, long to short
+    // within a sequence: a CU that finished a short tile takes the next sequence's long one,
+    // and the CUs' total work evens out (with the tiles of one kv head spread over the XCDs
+    // instead, the CUs' sums differed by ~30%). The head turns by one every four tiles, so
+    // with 8 kv heads each XCD takes four neighbouring tiles of one head one after another:
+    // they start together and read the same K/V rows at about the same time, from its L2
+    // (turned every tile, the L2 misses doubled). Every kv head still visits every XCD.
+    const int lin = blockIdx.x;
+    const int pair = lin / a.Hkv;  // (sequence, tile)
+    const int g = (lin - pair * a.Hkv + (pair >> 2)) % a.Hkv;
+    const int s = pair / a.qtiles;
+    const int tile = a.qtiles - 1 - (pair - s * a.qtiles);  // long (late) tiles first
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int grp = lane >> 4;  // 16-lane group
@@ -568,7 +580,11 @@ int32_t pkv_prefill(void* stream, const pkv_params* p, const void* q, const void
     a.out = out;
     const int qb = 128 / G;
     a.qtiles = (max_q + qb - 1) / qb;
-    dim3 grid(a.qtiles, p->num_kv_heads, batch);
+    // one workgroup id per (sequence, tile, kv head); the launch's work-items must fit in 32 bits
+    const int64_t wgs = (int64_t)a.qtiles * p->num_kv_heads * batch;
+    if (wgs > (int64_t)(UINT32_MAX / kNT))
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_prefill: too many (sequence, query tile, kv head) workgroups");
+    const dim3 grid((uint32_t)wgs);
     hipStream_t st = static_cast<hipStream_t>(stream);
     // The kernel's four 32 KiB K/V buffers are static LDS (128 KiB of the CU's 160 KiB).
     if (G == 1) hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kNT), 0, st, a);
