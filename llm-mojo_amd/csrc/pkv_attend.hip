@@ -423,14 +423,14 @@ __global__ __launch_bounds__(kNT) void attend_chunk_kernel(AttendArgs a) {
         for (int o = REP * R; o < LPR; o <<= 1) mb = fmax(mb, __shfl_xor(mb, o));
 #pragma unroll
         for (int o = LPR; o < kWave; o <<= 1) mb = fmax(mb, __shfl_xor(mb, o));
-        const Acc m_new = fmax(m_own, mb);
+        const bool moved = mb > m_own + (Acc)kLazyMove;  // lazy reference max; -inf: any live key
+        const Acc m_new = moved ? mb : m_own;
         const Acc p_own = ok ? exp_acc(sc_own - m_new) : (Acc)0;
         Acc lb = p_own;
 #pragma unroll
         for (int o = REP * R; o < LPR; o <<= 1) lb += __shfl_xor(lb, o);
 #pragma unroll
         for (int o = LPR; o < kWave; o <<= 1) lb += __shfl_xor(lb, o);
-        const bool moved = m_new != m_own;
         Acc scl = (Acc)1;
         if (moved) scl = exp_acc(m_own - m_new);  // m_own = -inf gives 0
         l_own = l_own * scl + lb;

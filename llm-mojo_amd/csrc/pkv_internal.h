@@ -18,6 +18,15 @@ constexpr int kBlockThreads = 256; // 4 waves per workgroup for every kernel her
 // streams ~9% faster with it (config 2: 0.68 -> 0.75 of HBM, same box).
 constexpr int kCpolNT = 2;
 
+// Lazy reference max of the online softmax (decode, verify, sparse and chunk attention): a
+// row's reference m moves only when a batch's max exceeds it by more than kLazyMove
+// (natural-log units), so the weights exp(s - m) stay below e^20 (~4.9e8, far inside float
+// and double range) and the result does not change (softmax does not depend on the
+// reference; the 1e-10 of the denominator shifts by at most a relative 1e-10, as l >= 1
+// whenever a key is live). The rescale of the accumulators and its exponential then run on
+// the few batches that move it, not on every batch whose max grows a little.
+constexpr float kLazyMove = 20.f;
+
 // Thread-local message behind pkv_last_error().
 void set_error(const std::string& msg);
 void clear_error();

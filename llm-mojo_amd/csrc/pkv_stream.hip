@@ -281,6 +281,7 @@ __device__ inline gchar* uniform_ptr(const char* p) {
 __device__ inline double exp_acc(double x) { return exp(x); }
 __device__ inline float exp_acc(float x) { return expf(x); }
 
+
 // ---- loads ------------------------------------------------------------------------
 
 // NW 32-bit words per lane from a lane-contiguous run. NT: non-temporal loads (NT bit),
@@ -893,10 +894,10 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             const bool ok = live_own && t_own < tb && t_own <= pq_own && t_own >= ws_own;
             const Acc sc = ok ? dots[0] : (Acc)-INFINITY;
             const Acc mb = allreduce_hi<ROWB>(sc, OpMax());
-            const Acc m_new = fmax(m_own, mb);
+            const bool moved = mb > m_own + (Acc)kLazyMove;  // m_own = -inf: any live key
+            const Acc m_new = moved ? mb : m_own;
             const Acc p_own = ok ? exp_acc(sc - m_new) : (Acc)0;
             const Acc lb = allreduce_hi<ROWB>(p_own, OpSum());
-            const bool moved = m_new != m_own;
             Acc scl = (Acc)1;
             if (moved) scl = exp_acc(m_own - m_new);  // m_own = -inf gives 0
             l_own = l_own * scl + lb;
@@ -1185,6 +1186,11 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
 
         issue(ta, stage);
         for (int t = ta; t < tb; t += U) {
+            // Waves w and w + 4 share a SIMD, whose issue slots bound this loop. The arbiter
+            // favours the older wave, which left the other one alone for the last ~15% of the
+            // piece; alternating their priorities every batch keeps the two in step.
+            if ((((t - ta) / U) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_s_waitcnt(0);  // this batch's slices are in LDS
             float4 kw[TG][4], vw[TG][4];
 #pragma unroll
@@ -1234,7 +1240,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                     if (ok[tg][rg]) mb = fmax(mb, v);
                 }
                 mb = allreduce_hi<16>(mb, OpMax());
-                m_new[rg] = fmax(m[rg], mb);
+                m_new[rg] = mb > m[rg] + (double)kLazyMove ? mb : m[rg];  // lazy reference max
             }
             // Every block holds the same scores. With two row groups, blocks of even index
             // take row group 0's exponentials and odd ones row group 1's, and a rotation by
