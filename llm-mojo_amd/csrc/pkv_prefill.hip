@@ -174,13 +174,13 @@ __global__ __launch_bounds__(kNT) void prefill_kernel(PrefillArgs a) {
     // kv head fastest, so every XCD receives the same run of tile lengths, long to short
     // within a sequence: a CU that finished a short tile takes the next sequence's long one,
     // and the CUs' total work evens out (with the tiles of one kv head spread over the XCDs
-    // instead, the CUs' sums differed by ~30%). The head turns by one every four tiles, so
-    // with 8 kv heads each XCD takes four neighbouring tiles of one head one after another:
-    // they start together and read the same K/V rows at about the same time, from its L2
-    // (turned every tile, the L2 misses doubled). Every kv head still visits every XCD.
+    // instead, the CUs' sums differed by ~30%). The head turns by one every eight tiles, so
+    // with 8 kv heads each XCD takes neighbouring tiles of one head one after another: they
+    // start together and read the same K/V rows at about the same time, from its L2 (turned
+    // every tile, the L2 misses doubled). Every kv head still visits every XCD.
     const int lin = blockIdx.x;
     const int pair = lin / a.Hkv;  // (sequence, tile)
-    const int g = (lin - pair * a.Hkv + (pair >> 2)) % a.Hkv;
+    const int g = (lin - pair * a.Hkv + (pair >> 3)) % a.Hkv;
     const int s = pair / a.qtiles;
     const int tile = a.qtiles - 1 - (pair - s * a.qtiles);  // long (late) tiles first
     const int tid = threadIdx.x;
