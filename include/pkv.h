@@ -325,7 +325,9 @@ int32_t pkv_lsa_rollback(void* stream, const int32_t* index_ids, const int32_t* 
  * pos[s], pos[s]+1, ...; query i attends keys [window_start(pos[s]+i), pos[s]+i] of its
  * own table (prefix plus the causal part of the chunk). out: fp32 [rows][num_heads]
  * [head_dim]. kv_dtype must be PKV_DTYPE_BF16, head_dim 256, num_heads / num_kv_heads in
- * {1, 2, 4}, block_size >= 8 (the engine uses 16). max_q bounds q_off[s+1]-q_off[s] (it sizes the grid) and max_pos bounds
+ * {1, 2, 4}, block_size >= 8 (the engine uses 16). max_q bounds q_off[s+1]-q_off[s] (it
+ * sizes the grid: batch * num_kv_heads * ceil(max_q * G / 128) workgroups, at most
+ * 2^32 / 512, else PKV_ERR_UNSUPPORTED) and max_pos bounds
  * pos[s] + its query count - 1; a sequence violating either, or whose table holds an
  * entry outside [0, num_blocks), gets NaN outputs; pos[s] < 0 gives zeros. One launch,
  * no workspace. q_off: int32 [batch + 1] (device). Paged pools only: ring_size > 0
