@@ -79,8 +79,8 @@ def run_gpu(sched, data, steps, warmup, log):
 
     B = sched.B
     stream = hip.Stream()
-    layers = [LayerSpec(sched.HQ, sched.HKV, sched.D, window=sched.WINDOW),
-              LayerSpec(sched.HQ, sched.HKV, sched.D, window=0)]
+    L = sched.L
+    layers = [LayerSpec(sched.HQ, sched.HKV, sched.D, window=w) for w in sched.windows]
     cache = PagedKVCache(layers, block_size=sched.BS, num_blocks=sched.num_blocks,
                          max_seqs=B, max_blocks_per_seq=sched.table_stride, max_q_len=1,
                          max_pos=sched.max_pos, scale=sched.SCALE, stream=stream)
@@ -91,7 +91,7 @@ def run_gpu(sched, data, steps, warmup, log):
     init = {"tables": D(sched.tables0), "lens": D(sched.lens0), "free": D(fl),
             "count": D(np.array([sched.free0.size], np.int32))}
     pristine = []
-    for layer in range(2):
+    for layer in range(L):
         for kv, pool in enumerate((cache.k_pools[layer], cache.v_pools[layer])):
             pristine.append((pool, data["pools"][layer][kv]))
     q, k_new, v_new = data["q"], data["k_new"], data["v_new"]
@@ -103,12 +103,12 @@ def run_gpu(sched, data, steps, warmup, log):
         e = data["event_index"][j]
         ev[j] = dict(new_len=D(sched.retire_new_len(j)), pos=D(sched.admit_pos(j)),
                      off=D(sched.admit_tok_off(j)),
-                     k=[data["admit_k"].ptr + (e * 2 + l) * sched.admit_rows * row_bytes
-                        for l in range(2)],
-                     v=[data["admit_v"].ptr + (e * 2 + l) * sched.admit_rows * row_bytes
-                        for l in range(2)])
-    outs = hip.DeviceArray((sched.STEPS, 2, B, 1, sched.HQ, sched.D), np.float32)
-    scratch_out = hip.DeviceArray((2, B, 1, sched.HQ, sched.D), np.float32)
+                     k=[data["admit_k"].ptr + (e * L + l) * sched.admit_rows * row_bytes
+                        for l in range(L)],
+                     v=[data["admit_v"].ptr + (e * L + l) * sched.admit_rows * row_bytes
+                        for l in range(L)])
+    outs = hip.DeviceArray((sched.STEPS, L, B, 1, sched.HQ, sched.D), np.float32)
+    scratch_out = hip.DeviceArray((L, B, 1, sched.HQ, sched.D), np.float32)
     qstep = B * sched.HQ * sched.D * 4
     kvstep = B * row_bytes
     st = stream.handle
@@ -127,11 +127,11 @@ def run_gpu(sched, data, steps, warmup, log):
         if j in sched.events:
             e = ev[j]
             cache.rollback(e["new_len"].ptr)
-            for layer in range(2):
+            for layer in range(L):
                 cache.append(layer, e["pos"].ptr, e["off"].ptr, e["k"][layer], e["v"][layer],
                              sched.ADMIT_CTX, sched.admit_rows)
-        for layer in range(2):
-            off = j * 2 + layer
+        for layer in range(L):
+            off = j * L + layer
             out = (outs.ptr + off * qstep) if first_pass else (scratch_out.ptr + layer * qstep)
             if events is None:
                 # the step as an engine runs it: append + attention in one call, whose
@@ -185,14 +185,14 @@ def run_gpu(sched, data, steps, warmup, log):
     wall, gpu_ms = timed(None)
     restore_all()
     fence_free = hip.hipEventDisableSystemFence
-    evs = [[(hip.Event(fence_free), hip.Event(fence_free)) for _ in range(2)]
+    evs = [[(hip.Event(fence_free), hip.Event(fence_free)) for _ in range(L)]
            for _ in range(steps)]
     _, gpu_ms_ev = timed(evs)
     log(f"timed {steps} steps: {gpu_ms:.2f} ms (with per-launch events {gpu_ms_ev:.2f} ms)")
-    dur = np.zeros((steps, 2))
-    nbytes = np.zeros((steps, 2))
+    dur = np.zeros((steps, L))
+    nbytes = np.zeros((steps, L))
     for i in range(steps):
-        for layer in range(2):
+        for layer in range(L):
             dur[i, layer] = evs[i][layer][0].elapsed_ms(evs[i][layer][1])
             nbytes[i, layer] = sched.attend_bytes(i % sched.STEPS, layer)
     status = cache.status.numpy()
@@ -241,10 +241,10 @@ def run_cpu(sched, data, seconds, nthreads, log, par=0):
     from oracle import oracle as O
     O.use_host_build()
 
-    B = sched.B
-    st = O.CacheState(2, sched.kv_stride, sched.BS, sched.num_blocks, B, sched.table_stride,
+    B, L = sched.B, sched.L
+    st = O.CacheState(L, sched.kv_stride, sched.BS, sched.num_blocks, B, sched.table_stride,
                       alloc_pools=False)
-    for layer in range(2):
+    for layer in range(L):
         st.k_pools[layer] = data["pools"][layer][0].numpy().reshape(-1)
         st.v_pools[layer] = data["pools"][layer][1].numpy().reshape(-1)
     qh, kh, vh = data["q"].numpy(), data["k_new"].numpy(), data["v_new"].numpy()
@@ -263,24 +263,24 @@ def run_cpu(sched, data, seconds, nthreads, log, par=0):
         if j in sched.events:
             e = data["event_index"][j]
             st.rollback(sched.retire_new_len(j))
-            for layer in range(2):
+            for layer in range(L):
                 st.append(layer, sched.admit_pos(j), sched.admit_tok_off(j), ak[e, layer],
                           av[e, layer], sched.ADMIT_CTX)
         step_out = []
-        for layer in range(2):
+        for layer in range(L):
             st.append(layer, sched.pos[j], dec_off, kh[j, layer], vh[j, layer], 1)
             o = O.attend(qh[j, layer], st.k_pools[layer], st.v_pools[layer], st.tables,
                          st.table_lens, sched.pos[j], 1, sched.HQ, sched.HKV, sched.D, sched.BS,
-                         sched.WINDOW if layer == 0 else 0, scale=sched.SCALE,
+                         sched.windows[layer], scale=sched.SCALE,
                          nthreads=nthreads, par=par)
             step_out.append(o)
         elapsed += time.perf_counter() - t0
         if j < 2 and par == 0:  # float64 attention of the same inputs (outside the sample)
-            for layer in range(2):
+            for layer in range(L):
                 exact.append((j, layer, O.attend_f64(
                     qh[j, layer], st.k_pools[layer], st.v_pools[layer], st.tables,
                     sched.pos[j], 1, sched.HQ, sched.HKV, sched.D, sched.BS,
-                    sched.WINDOW if layer == 0 else 0, scale=sched.SCALE)))
+                    sched.windows[layer], scale=sched.SCALE)))
         outs.append(step_out)
         done += 1
         if elapsed >= seconds:
@@ -1051,55 +1051,23 @@ def bench_wo(args, log):
     return res
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256, help="timed decode steps")
-    ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0,
-                    help="bound on the CPU-baseline sample (0 disables it)")
-    ap.add_argument("--cpu-threads", type=int, default=8,
-                    help="threads of the reference-faithful CPU mode (8 = its Hq/2 head-pair "
-                         "tasks); the all-cores mode uses the job's OpenMP share of the host")
-    ap.add_argument("--quiet", action="store_true")
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
-                    help="BASELINE.json configuration (2, the default, is the headline)")
-    ap.add_argument("--leg", choices=["producer", "lsa", "wo"], default=None,
-                    help="measure a path beside the configurations instead: 'producer' = "
-                         "pkv_append_qkv (norm + RoPE + append), 'lsa' = pkv_attend_sparse, "
-                         "'wo' = pkv_q4_matmul")
-    args = ap.parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print("bench.py measures the paged KV path on one GPU only: every GPU box here has "
-              "one GPU and this path has no multi-GPU leg (splitting sequences or heads "
-              "across GPUs is not built). Run with --gpus 1.", file=sys.stderr)
-        return 2
+def kernel_name(sched):
+    """The attention kernels a decode schedule's launches run (stream kernel + merge)."""
+    if sched.D == 512:
+        return "stream_attend_kernel<512, float, 2, 4> + stream_merge_kernel<512, double>"
+    return "stream_attend_kernel<256, float, 2> + stream_merge_kernel<256, double>"
 
-    def log(msg):
-        if not args.quiet:
-            print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
+def bench_decode(args, log, sched, metric, workload, traffic_profile):
+    """A DecodeSchedule (config 2, or its schedule on another geometry) through
+    pkv_append_attend per layer and step; returns the JSON line's dict."""
     from pkv import hip
-    from pkv.workloads import DecodeSchedule
 
-    if hip.device_count() < 1:
-        print("bench.py needs a GPU: no HIP device visible", file=sys.stderr)
-        return 1
-    if args.leg is not None:
-        leg = {"producer": bench_producer, "lsa": bench_lsa, "wo": bench_wo}[args.leg]
-        print(json.dumps(leg(args, log)), flush=True)
-        return 0
-    legs = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}
-    if args.config in legs:
-        print(json.dumps(legs[args.config](args, log)), flush=True)
-        return 0
     t = time.perf_counter()
-    sched = DecodeSchedule(seed=args.seed)
     data = sched.device_data()
     hip.synchronize()
-    log(f"config 2 built in {time.perf_counter() - t:.1f}s: {sched.num_blocks} blocks, "
+    L = sched.L
+    log(f"decode schedule built in {time.perf_counter() - t:.1f}s: {sched.num_blocks} blocks, "
         f"contexts {sched.ctx0.min()}..{sched.ctx0.max()}")
     g = run_gpu(sched, data, args.steps, args.warmup, log)
     steps = args.steps
@@ -1107,32 +1075,22 @@ def main() -> int:
     tok_s = sched.B * steps / (g["gpu_ms"] / 1e3)
     dur, nb = g["dur_ms"], g["bytes"]
     achieved = nb.sum() / (dur.sum() / 1e3) / 1e9
-    glob_gbs = nb[:, 1].sum() / (dur[:, 1].sum() / 1e3) / 1e9
-    slide_gbs = nb[:, 0].sum() / (dur[:, 0].sum() / 1e3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                 "traffic": None,
-                "kernel": "stream_attend_kernel<256, float, 2> + stream_merge_kernel<256, double>",
+                "kernel": kernel_name(sched),
                 "avg_launch_us": round(dur.mean() * 1e3, 2),
                 "algorithmic_bytes_per_launch": int(nb.mean())}
-    _set_traffic(roofline, "stream_attend_decode_cfg2_traffic.md")
+    _set_traffic(roofline, traffic_profile)
     result = {
-        "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "metric": metric, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic: seeded N(0,1) K/V/Q, seeded contexts U[128,8192], seeded "
                 "random non-overlapping block tables",
-        "config": {"workload": "BASELINE config 2: continuous-batching decode, 32 sequences, "
-                               "sliding(1024)+global layers, 16q/8kv/256, block 16, fp32 KV, "
-                               "retire 4 / admit 4 (256 tok) every 8 steps, 64-step schedule",
-                   "batch": sched.B, "num_blocks": sched.num_blocks, "head_dim": sched.D,
+        "config": {"workload": workload, "batch": sched.B, "num_blocks": sched.num_blocks, "head_dim": sched.D,
                    "kv_heads": sched.HKV, "q_heads": sched.HQ, "block_size": sched.BS},
         "roofline": roofline,
-        "attn_global_gbs": round(glob_gbs, 1),
-        "attn_global_frac": round(glob_gbs / PEAK_HBM_GBS, 4),
-        "attn_sliding_gbs": round(slide_gbs, 1),
-        "attn_global_avg_us": round(dur[:, 1].mean() * 1e3, 2),
-        "attn_sliding_avg_us": round(dur[:, 0].mean() * 1e3, 2),
         "ms_per_step_with_launch_events": round(g["gpu_ms_ev"] / steps, 4),
         "step_calls": "per layer pkv_append_attend (the attention launch also writes the "
                       "appended rows); roofline pass: pkv_append, then the event pair around "
@@ -1140,6 +1098,12 @@ def main() -> int:
         "wall_s": round(g["wall_s"], 4),
         "append_status_ok": bool(np.all(g["status"] == 0)),
     }
+    for layer, win in enumerate(sched.windows):  # per layer: its own bytes over its own launches
+        name = "global" if win <= 0 else "sliding"
+        gbs = nb[:, layer].sum() / (dur[:, layer].sum() / 1e3) / 1e9
+        result[f"attn_{name}_gbs"] = round(gbs, 1)
+        result[f"attn_{name}_frac"] = round(gbs / PEAK_HBM_GBS, 4)
+        result[f"attn_{name}_avg_us"] = round(dur[:, layer].mean() * 1e3, 2)
     if args.cpu_seconds > 0:
         from oracle import oracle as O
 
@@ -1150,14 +1114,14 @@ def main() -> int:
         c = run_cpu(sched, data, args.cpu_seconds / 2, args.cpu_threads, log, par=0)
         cb = run_cpu(sched, data, args.cpu_seconds / 2, all_threads, log, par=3)
         errs = [O.max_rel_err(g["outs"][j, layer], c["outs"][j][layer])
-                for j in range(min(c["steps"], steps)) for layer in range(2)]
+                for j in range(min(c["steps"], steps)) for layer in range(L)]
         same = all(np.array_equal(c["outs"][j][layer], cb["outs"][j][layer])
-                   for j in range(min(c["steps"], cb["steps"])) for layer in range(2))
+                   for j in range(min(c["steps"], cb["steps"])) for layer in range(L))
         faithful = round(sched.B * c["steps"] / c["seconds"], 2)
         batched = round(sched.B * cb["steps"] / cb["seconds"], 2)
         result["cpu_baseline"] = {
             "value": batched, "unit": "tokens/s", "cores": all_threads, "kind": "port",
-            "sample": f"first {cb['steps']} steps of the same 64-step schedule (both layers, "
+            "sample": f"first {cb['steps']} steps of the same 64-step schedule (every layer, "
                       f"appends + attention), all-cores batched: every (sequence, head pair) "
                       f"task of a step on {all_threads} threads; the oracle's "
                       f"{os.path.basename(lib_path)} build",
@@ -1181,8 +1145,75 @@ def main() -> int:
                 "steps": min(c["steps"], steps), "max_rel_err_vs_cpu_fp32": float(f"{max(errs):.3g}"),
                 "max_rel_err_vs_float64": float(f"{max(e64):.3g}"),
                 "cpu_fp32_vs_float64": float(f"{max(own):.3g}"),
-                "float64_steps": len(c["exact"]) // 2,
+                "float64_steps": len(c["exact"]) // L,
                 "metric": "max |x-ref|/(|ref|+1e-3)"}
+    return result
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode steps")
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="bound on the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--cpu-threads", type=int, default=8,
+                    help="threads of the reference-faithful CPU mode (8 = its Hq/2 head-pair "
+                         "tasks); the all-cores mode uses the job's OpenMP share of the host")
+    ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
+                    help="BASELINE.json configuration (2, the default, is the headline)")
+    ap.add_argument("--leg", choices=["producer", "lsa", "wo", "global512"], default=None,
+                    help="measure a path beside the configurations instead: 'producer' = "
+                         "pkv_append_qkv (norm + RoPE + append), 'lsa' = pkv_attend_sparse, "
+                         "'wo' = pkv_q4_matmul, 'global512' = config 2's decode schedule on "
+                         "the engine's global-layer geometry (16q/2kv/512)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures the paged KV path on one GPU only: every GPU box here has "
+              "one GPU and this path has no multi-GPU leg (splitting sequences or heads "
+              "across GPUs is not built). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    def log(msg):
+        if not args.quiet:
+            print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    from pkv import hip
+    from pkv.workloads import DecodeSchedule
+
+    if hip.device_count() < 1:
+        print("bench.py needs a GPU: no HIP device visible", file=sys.stderr)
+        return 1
+    if args.leg in ("producer", "lsa", "wo"):
+        leg = {"producer": bench_producer, "lsa": bench_lsa, "wo": bench_wo}[args.leg]
+        print(json.dumps(leg(args, log)), flush=True)
+        return 0
+    legs = {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}
+    if args.config in legs:
+        print(json.dumps(legs[args.config](args, log)), flush=True)
+        return 0
+    if args.leg == "global512":
+        sched = DecodeSchedule.engine_global(seed=args.seed)
+        result = bench_decode(
+            args, log, sched,
+            metric="engine global-layer paged decode tokens/s (16q/2kv/512, B=32, 1 GPU)",
+            workload="config 2's schedule on the engine's global-layer geometry: 32 sequences, "
+                     "contexts U[128,8192], one full-attention layer, 16q/2kv/512 "
+                     "(model_speculative_moe_batched.mojo:1905-1907), block 16, fp32 KV, "
+                     "scale 2^-4, retire 4 / admit 4 (256 tok) every 8 steps, "
+                     "64-step schedule",
+            traffic_profile="stream_decode_global512_traffic.md")
+    else:
+        sched = DecodeSchedule(seed=args.seed)
+        result = bench_decode(
+            args, log, sched, metric=METRIC,
+            workload="BASELINE config 2: continuous-batching decode, 32 sequences, "
+                     "sliding(1024)+global layers, 16q/8kv/256, block 16, fp32 KV, "
+                     "retire 4 / admit 4 (256 tok) every 8 steps, 64-step schedule",
+            traffic_profile="stream_attend_decode_cfg2_traffic.md")
     print(json.dumps(result), flush=True)
     return 0
 

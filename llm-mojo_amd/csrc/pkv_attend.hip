@@ -824,7 +824,10 @@ int32_t pkv_attend_sparse(void* stream, const pkv_params* p, const float* q, con
     if ((int64_t)p->num_blocks * p->block_size > INT32_MAX)
         return fail(PKV_ERR_UNSUPPORTED, "pool rows must fit in int32");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (stream_eligible(p, G) && workspace_bytes >= stream_layout(p, batch, 1).total) {
+    // Lists of more than kStreamMaxBatch sequences take the chunk kernel (the stream
+    // kernels keep a per-sequence plan in LDS).
+    if (stream_eligible(p, G) && batch <= kStreamMaxBatch &&
+        workspace_bytes >= stream_layout(p, batch, 1).total) {
         rc = stream_attend(p, q, k_pool, v_pool, block_tables, table_stride, nullptr, 0, 0, 1,
                            nullptr, batch, 0, keys, key_off, max_keys, out, workspace, st);
         if (rc != PKV_OK) return rc;

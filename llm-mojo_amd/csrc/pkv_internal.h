@@ -68,6 +68,10 @@ AttendLayout attend_layout(const pkv_params* p, int32_t batch, int32_t q_len, in
 // slots = min(nwg_cap, kStreamMaxSlots) + batch, rows = num_heads * q_len: piece (w, s) of
 // workgroup w < nwg <= nwg_cap and sequence s uses slot w + s.
 constexpr int kStreamMaxSlots = 1024;  // workgroups along the keys, at most
+// LDS of one CU; the stream kernels keep 5 ints per sequence there (8 with a fused append),
+// so a launch takes at most kStreamMaxBatch sequences.
+constexpr size_t kStreamLdsMax = 160 * 1024;
+constexpr int kStreamMaxBatch = 8191;
 struct StreamLayout {
     size_t plan_off;
     size_t ml_off;

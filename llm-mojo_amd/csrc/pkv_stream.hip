@@ -961,34 +961,44 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     }
 }
 
-// ---- fp64 MFMA path: fp32 pools, head_dim 256, 3..8 query rows per KV head ------------
+// ---- fp64 MFMA path: fp32 pools, head_dim 256 or 512, 5..8 query rows per KV head --------
 //
 // v_mfma_f64_4x4x4_4b computes four independent 4x4x4 double products per instruction
 // at the full fp64 rate. Lane l = 4b + x + 16y holds block b's elements (b = lane bits
 // 2-3); inside a block (layouts checked on the device) A[i][k] sits at x = i, y = k,
-// B[k][j] at x = j, y = k, and C[i][j] at x = j, y = i. One wave per KV head; its query
-// rows form RG groups of 4 (row 4rg + x of lane x).
+// B[k][j] at x = j, y = k, and C[i][j] at x = j, y = i. WPH waves per KV head split its
+// rows; each wave's rows form RG groups of 4 (row rb + 4rg + x of lane x). head_dim 256:
+// one wave of 8 rows (RG 2); head_dim 512 (the engine's 16q/2kv global layers): two waves
+// of 4 rows (RG 1), which keeps the accumulators of a wave at 32 doubles per lane.
 //   S^T = K Q^T for each group of 4 tokens tg and row group rg: A = K (x = token, y = d
-//     slot), B = Q (x = row, y = d slot). Over the 16 steps (q, e) block b contracts
+//     slot), B = Q (x = row, y = d slot). Over the steps (q, e) block b contracts
 //     d = 64q + 16b + 4y + e, so the four blocks hold partial sums over disjoint d, added
 //     by two DPP rotations. Lane (b, x, y) then holds S[row 4rg + x][token 4tg + y] --
 //     the B operand of PV as it stands.
 //   O^T += V^T P^T: A = V (x = d slot, y = token), B = P; tile (rg, q, e) of lane
 //     (b, x, y) accumulates O[4rg + x][64q + 16b + 4y + e].
-// Each load is 16 bytes of one token's row, so a load instruction reads 4 tokens x 256
-// contiguous bytes. Products of fp32 values are exact in double and every sum is a
-// double sum, as in the vector path; the matrix cores take the 2 x rows x 256
+// Each load moves 16 bytes per lane of one token's row slice (64 lanes: 1 KiB), so a
+// head_dim-512 slice takes two. Products of fp32 values are exact in double and every
+// sum is a double sum, as in the vector path; the matrix cores take the 2 x rows x D
 // multiply-adds per token off the vector ALUs, and the dot products need no cross-lane
 // reduction beyond the block sum.
+// Fused append (pkv_append_attend): as the vector kernel -- the allocation plan from the
+// state as it stands, the appended rows copied into the pool by the launch and read from
+// k_new / v_new, the state written by the merge launch.
 typedef __attribute__((address_space(3))) void lds_void;
 // s_waitcnt with only lgkmcnt = 0 (vmcnt and expcnt at their maxima).
 constexpr int kLgkm0 = 0xC07F;
-// LDS of the MFMA kernel: s_pre / s_lo / s_meta, then one staging area per wave.
-__host__ __device__ constexpr size_t mfma_stage_offset(int batch) {
-    return ((size_t)stream_seq_ints(batch) * sizeof(int) + 15) & ~(size_t)15;
+// LDS of the MFMA kernel: s_pre / s_lo / s_meta (and the allocation plan of a fused
+// append), then one staging area per wave.
+__host__ __device__ constexpr size_t mfma_stage_offset(int batch, bool fused) {
+    return ((size_t)(stream_seq_ints(batch) + (fused ? 3 * batch + 2 : 0)) * sizeof(int) + 15) &
+           ~(size_t)15;
 }
-constexpr int kSlot = 1024 + 16;  // one token's 1 KiB slice plus bank padding
-__host__ __device__ constexpr size_t mfma_stage_bytes(int tg) { return (size_t)tg * 8 * kSlot; }
+// One token's row slice plus 16 bytes of bank padding.
+__host__ __device__ constexpr int mfma_slot(int D) { return D * 4 + 16; }
+__host__ __device__ constexpr size_t mfma_stage_bytes(int D, int tg) {
+    return (size_t)tg * 8 * mfma_slot(D);
+}
 
 __device__ inline double mfma4(double a, double b, double c) {
     return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
@@ -999,16 +1009,24 @@ __device__ inline double block_sum(double v) {
     return v + dpp<ror_ctrl<8>()>(v);
 }
 
-template <int RG, int TG, int ADDR>
+// FUSED: the launch of a fused append (paged pools); a separate instance, so the scalar
+// state of the appended rows costs the other launches nothing.
+template <int D, int RG, int TG, int WPH, int ADDR, bool FUSED>
 __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs a) {
-    constexpr int D = 256;
+    constexpr int NQ = D / 64;  // 64-d chunks of a row
+    constexpr int kSlot = mfma_slot(D);
     constexpr int U = 4 * TG;  // tokens per batch
     constexpr bool RING = ADDR == kAddrRing;
     constexpr bool SPARSE = ADDR == kAddrSparse;
+    constexpr bool PAGED = ADDR == kAddrPaged;
+    // Rows that one wave alone reads are loaded with the NT bit; with WPH > 1 the other
+    // waves of the head read them in turn from the L2.
+    constexpr int kCpol = WPH == 1 ? kCpolNT : 0;
     extern __shared__ int smem[];
     int* s_pre = smem;               // [batch + 1]
     int* s_lo = smem + a.batch + 1;  // [batch]
-    int* s_meta = smem + 2 * a.batch + 1;  // [3 batch + 1] (stream_setup)
+    int* s_meta = smem + 2 * a.batch + 1;         // [3 batch + 1] (stream_setup)
+    int* s_al = smem + stream_seq_ints(a.batch);  // fused append: the allocation plan
 
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
@@ -1016,12 +1034,16 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int w = blockIdx.y;
     const int B = a.batch;
 
-    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, nullptr);  // never a fused append
+    static_assert(!FUSED || PAGED, "appended rows: paged pools only");
+    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, s_al);
+    constexpr bool fused = FUSED;  // the launcher passes the rows exactly when FUSED
+    if (fused) copy_new_rows<D, float, WPH>(a, s_meta, s_al, wave, lane);
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
     const int k1 = min(total, sp.start(w + 1));
-    const int g = blockIdx.x * kMaxWaves + wave;  // this wave's KV head
+    const int g = blockIdx.x * (kMaxWaves / WPH) + wave / WPH;  // this wave's KV head
+    const int rb = (wave % WPH) * 4 * RG;  // first of this wave's rows of the head
     if (g >= a.Hkv) return;
 
     const int rows = a.G * a.q_cnt;
@@ -1032,7 +1054,13 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int kdo = 64 * b + 16 * y;  // bytes of d = 16b + 4y in a 64-d chunk (K operand)
     const int vdo = 64 * b + 16 * x;  // bytes of d = 16b + 4x (V operand)
     const int bs_mask = (1 << a.bs_shift) - 1;
-    char* stage = reinterpret_cast<char*>(smem) + mfma_stage_offset(B) + (size_t)wave * mfma_stage_bytes(TG);
+    char* stage = reinterpret_cast<char*>(smem) + mfma_stage_offset(B, fused) +
+                  (size_t)wave * mfma_stage_bytes(D, TG);
+    // Waves w and w + 4 of an 8-wave workgroup share a SIMD, whose issue slots bound the
+    // batch loop; the arbiter favours the older wave, which left the other one alone for
+    // the last ~15% of a piece. Alternating their priorities every batch keeps the two in
+    // step.
+    const bool toggle = blockDim.x == kMaxWaves * kSW;
 
     int s = 0;
     {
@@ -1060,6 +1088,24 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         const int rows_s = a.G * ufirst(s_meta[B + s]);
         const int32_t* trow = a.tables + (size_t)s * a.table_stride;
         const int last_page = (tb - 1) >> a.bs_shift;
+        // Fused append: table indices [g_lo, g_hi) are the blocks granted in this call,
+        // whose ids come from the free list (g_top - index); positions [pn_lo, pn_hi) are
+        // read from k_new / v_new (row nr0 + t - pn_lo).
+        int g_lo = INT32_MAX, g_hi = INT32_MIN, g_top = 0;
+        int pn_lo = INT32_MAX, pn_hi = INT32_MIN, nr0 = 0;
+        if (fused) {
+            const SeqAlloc al = seq_alloc(s_al, B, a.num_blocks, s);
+            g_lo = ufirst(al.len);
+            g_hi = g_lo + ufirst(al.granted);
+            g_top = ufirst(al.fc) - 1 - ufirst(al.pref) + g_lo;
+            const int r0 = ufirst(s_meta[2 * B + s]);
+            const int n = ufirst(s_meta[2 * B + s + 1]) - r0;
+            if (new_rows_written(ufirst(al.code)) && pos0 >= 0 && n > 0) {
+                pn_lo = pos0;
+                pn_hi = pos0 + n;
+                nr0 = r0;
+            }
+        }
 
         // The piece's first loads are all requested before any of them is used (one round
         // trip): the first 64 page ids (sparse: listed keys) and the query rows. Each is
@@ -1068,36 +1114,39 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         int first_raw = 0;
         if constexpr (SPARSE) {
             first_raw = a.keys[kbeg + min(ta + lane, tb - 1)];
-        } else if constexpr (ADDR == kAddrPaged) {
-            first_raw = trow[min((ta >> a.bs_shift) + lane, last_page)];
+        } else if constexpr (PAGED) {
+            const int pg = min((ta >> a.bs_shift) + lane, last_page);
+            const int32_t* src = trow + pg;
+            if constexpr (FUSED) src = (pg >= g_lo && pg < g_hi) ? a.nr.free_list + (g_top - pg) : src;
+            first_raw = *src;
         }
         asm volatile("" ::: "memory");  // issued before the query rows
-        // this lane's rows 4rg + x: Q slice (B operand), query position, first key
-        float4 qf[RG][4];  // fp32: converted at each use, which saves registers
+        // this lane's rows rb + 4rg + x: Q slice (B operand), query position, first key
+        float4 qf[RG][NQ];  // fp32: converted at each use, which saves registers
         int pq[RG], wsr[RG];
         bool live[RG];
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
-            const int r = 4 * rg + x;
+            const int r = rb + 4 * rg + x;
             live[rg] = r < rows_s;
             pq[rg] = SPARSE ? INT32_MAX : pos0 + a.j0 + r / a.G;
             wsr[rg] = SPARSE ? 0 : window_start(pq[rg], a.window);
             const float* qp = a.q + out_row(a, s, g, min(r, rows - 1)) * D + 16 * b + 4 * y;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) qf[rg][q] = *reinterpret_cast<const float4*>(qp + 64 * q);
+            for (int q = 0; q < NQ; ++q) qf[rg][q] = *reinterpret_cast<const float4*>(qp + 64 * q);
         }
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (4 * rg + x >= rows) qf[rg][q] = make_float4(0.f, 0.f, 0.f, 0.f);
-        double m[RG], l[RG], o[RG][4][4];
+            for (int q = 0; q < NQ; ++q)
+                if (rb + 4 * rg + x >= rows) qf[rg][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+        double m[RG], l[RG], o[RG][NQ][4];
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
             m[rg] = -INFINITY;
             l[rg] = 0.0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < NQ; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) o[rg][q][e] = 0.0;
         }
@@ -1124,7 +1173,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
             const bool id_ok = phys >= 0 && phys < a.num_blocks;
             bad = bad || (lane_ok && !id_ok);
             vpg = lane_ok && id_ok ? (phys << a.bs_shift) | (key & bs_mask) : 0;
-        } else if constexpr (ADDR == kAddrPaged) {
+        } else if constexpr (PAGED) {
             pgbase = ta >> a.bs_shift;
             const bool lane_ok = pgbase + lane <= last_page;
             const bool id_ok = first_raw >= 0 && first_raw < a.num_blocks;
@@ -1133,7 +1182,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         }
 
         // Batch staging: each token's K and V slices go from global memory straight into
-        // this wave's LDS slots (one 1 KiB row per slot, slots kSlot bytes apart), so the
+        // this wave's LDS slots (one row slice per slot, slots kSlot bytes apart), so the
         // next batch's loads are in flight while the current one is computed from registers.
         // The operand reads take 16 bytes of token 4tg + x (K) or 4tg + y (V); the 16-byte
         // slot padding puts the 16 lanes of each read phase on distinct banks.
@@ -1151,11 +1200,13 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                 }
                 vpg = row;
             }
-            if (ADDR == kAddrPaged && (tl >> a.bs_shift) - pgbase >= kSW) {  // next 64 page ids
+            if (PAGED && (tl >> a.bs_shift) - pgbase >= kSW) {  // next 64 page ids
                 pgbase = t >> a.bs_shift;
                 int pg = 0;
                 if (pgbase + lane <= last_page) {
-                    pg = trow[pgbase + lane];
+                    const int pi = pgbase + lane;
+                    if constexpr (FUSED) pg = (pi >= g_lo && pi < g_hi) ? a.nr.free_list[g_top - pi] : trow[pi];
+                    else pg = trow[pi];
                     if (pg < 0 || pg >= a.num_blocks) {
                         bad = true;
                         pg = 0;
@@ -1163,12 +1214,14 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                 }
                 vpg = pg;
             }
-            // One token's slice (64 lanes x 16 bytes, contiguous) per load; the address is
+            // One token's slice (64 lanes x 16 bytes per load, contiguous); the address is
             // wave-uniform: page id by readlane, offsets in scalar registers.
 #pragma unroll
             for (int j = 0; j < U; ++j) {
                 const int tt = min(t + j, tb - 1);  // tokens past the piece re-read its last row
                 size_t off;
+                const char* kb = kbase;
+                const char* vb = vbase;
                 if constexpr (RING) {
                     off = (size_t)ring_key_row(rbase, r0, tt - ta, a.ring_size) * row_bytes;
                 } else if constexpr (SPARSE) {
@@ -1176,27 +1229,36 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                 } else {
                     const int pg = __builtin_amdgcn_readlane(vpg, (tt >> a.bs_shift) - pgbase);
                     off = (((size_t)pg << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
+                    if (FUSED && tt >= pn_lo && tt < pn_hi) {  // an appended row: from k_new / v_new
+                        off = (size_t)(nr0 + (tt - pn_lo)) * row_bytes;
+                        kb = a.nr.k_new + (size_t)g * D * 4;
+                        vb = a.nr.v_new + (size_t)g * D * 4;
+                    }
                 }
-                __builtin_amdgcn_global_load_lds(uniform_ptr(kbase + off) + 16 * lane,
-                                                 (lds_void*)(buf + (2 * j) * kSlot), 16, 0, kCpolNT);
-                __builtin_amdgcn_global_load_lds(uniform_ptr(vbase + off) + 16 * lane,
-                                                 (lds_void*)(buf + (2 * j + 1) * kSlot), 16, 0, kCpolNT);
+#pragma unroll
+                for (int c = 0; c < D / 256; ++c) {
+                    __builtin_amdgcn_global_load_lds(uniform_ptr(kb + off + 1024 * c) + 16 * lane,
+                                                     (lds_void*)(buf + (2 * j) * kSlot + 1024 * c),
+                                                     16, 0, kCpol);
+                    __builtin_amdgcn_global_load_lds(uniform_ptr(vb + off + 1024 * c) + 16 * lane,
+                                                     (lds_void*)(buf + (2 * j + 1) * kSlot + 1024 * c),
+                                                     16, 0, kCpol);
+                }
             }
         };
 
         issue(ta, stage);
         for (int t = ta; t < tb; t += U) {
-            // Waves w and w + 4 share a SIMD, whose issue slots bound this loop. The arbiter
-            // favours the older wave, which left the other one alone for the last ~15% of the
-            // piece; alternating their priorities every batch keeps the two in step.
-            if ((((t - ta) / U) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
-            else __builtin_amdgcn_s_setprio(0);
+            if (toggle) {
+                if ((((t - ta) / U) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+                else __builtin_amdgcn_s_setprio(0);
+            }
             __builtin_amdgcn_s_waitcnt(0);  // this batch's slices are in LDS
-            float4 kw[TG][4], vw[TG][4];
+            float4 kw[TG][NQ], vw[TG][NQ];
 #pragma unroll
             for (int tg = 0; tg < TG; ++tg)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < NQ; ++q) {
                     kw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + x)) * kSlot + kdo + 256 * q);
                     vw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + y) + 1) * kSlot + vdo + 256 * q);
                 }
@@ -1210,7 +1272,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
 #pragma unroll
                 for (int rg = 0; rg < RG; ++rg) sc[tg][rg] = 0.0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < NQ; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     double qd[RG];
@@ -1279,13 +1341,13 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
 #pragma unroll
                 for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
+                    for (int q = 0; q < NQ; ++q)
 #pragma unroll
                         for (int e = 0; e < 4; ++e) o[rg][q][e] *= scl[rg];
             }
             // PV
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < NQ; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -1301,19 +1363,19 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         for (int rg = 0; rg < RG; ++rg) {
             // keep the last accumulations ahead of the stores' branches
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < NQ; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(o[rg][q][e]));
         }
         if (single) {
 #pragma unroll
             for (int rg = 0; rg < RG; ++rg) {
-                const int r = 4 * rg + x;
+                const int r = rb + 4 * rg + x;
                 if (r < rows_s) {
                     const double inv = 1.0 / (l[rg] + 1e-10);
                     float* op = a.out + out_row(a, s, g, r) * D + 16 * b + 4 * y;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
+                    for (int q = 0; q < NQ; ++q) {
                         float4 v;
                         v.x = bad ? __builtin_nanf("") : (float)(o[rg][q][0] * inv);
                         v.y = bad ? __builtin_nanf("") : (float)(o[rg][q][1] * inv);
@@ -1329,12 +1391,12 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
             double* pml = static_cast<double*>(a.part_ml);
 #pragma unroll
             for (int rg = 0; rg < RG; ++rg) {
-                const int r = 4 * rg + x;
+                const int r = rb + 4 * rg + x;
                 if (r < rows) {
                     const int row = (r / a.G) * a.Hq + g * a.G + r % a.G;
                     double* dst = po + (slot + row) * D + 16 * b + 4 * y;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
+                    for (int q = 0; q < NQ; ++q) {
                         double2* d2 = reinterpret_cast<double2*>(dst + 64 * q);
                         d2[0] = make_double2(o[rg][q][0], o[rg][q][1]);
                         d2[1] = make_double2(o[rg][q][2], o[rg][q][3]);
@@ -1506,6 +1568,12 @@ __global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
 
 constexpr int kMaxSlots = kStreamMaxSlots;  // workgroups along the keys, at most (merge LDS bound)
 
+// Dynamic LDS of the vector stream kernel: the per-sequence ints, plus the allocation plan
+// of a fused append.
+size_t stream_vector_lds(int batch, bool fused) {
+    return (size_t)(stream_seq_ints(batch) + (fused ? 3 * batch + 2 : 0)) * sizeof(int);
+}
+
 // Workgroups that fill the device once (all resident together), capped at kMaxSlots.
 int fill_workgroups(const void* fn, int threads, size_t lds) {
     return device_fill_workgroups(fn, threads, lds, kMaxSlots);
@@ -1517,8 +1585,15 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     const int waves = a.Hkv * WPH < kMaxWaves ? a.Hkv * WPH : kMaxWaves;
     const int threads = waves * kSW;
     const bool fused = ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0;
-    const size_t lds = (size_t)(stream_seq_ints(a.batch) + (fused ? 3 * a.batch + 2 : 0)) * sizeof(int);
+    const size_t lds = stream_vector_lds(a.batch, fused);
     const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH, ADDR>);
+    if (lds > kStreamLdsMax)  // stream_attend refuses such batches before any launch
+        return fail(PKV_ERR_UNSUPPORTED, "pkv_attend: batch too large for the kernel's LDS");
+    // Above 64 KiB of dynamic LDS a kernel must opt in (once per kernel and device).
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStreamLdsMax) !=
+            hipSuccess)
+        return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
     // Resident workgroups only: the head groups share the slots, and each workgroup
@@ -1530,6 +1605,9 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     dim3 grid(groups, a.nwg);
     hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, ADDR>), grid, dim3(threads), lds, st,
                        a);
+    // the merge reads the plan this launch writes
+    if (hipGetLastError() != hipSuccess)
+        return fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
     hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch + (fused ? 1 : 0)),
                        dim3(kMergeNT), 0, st, a);
     return PKV_OK;
@@ -1537,28 +1615,39 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
 
 template <int D, typename KV, int R, int WPH = 1>
 int32_t launch_r(StreamArgs a, hipStream_t st);
-constexpr size_t kMfmaLdsMax = 160 * 1024;  // LDS of one CU
+constexpr size_t kMfmaLdsMax = kStreamLdsMax;
 
-template <int RG, int TG, int ADDR>
+template <int D, int RG, int TG, int WPH, int ADDR>
 int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
-    const int waves = a.Hkv < kMaxWaves ? a.Hkv : kMaxWaves;
+    const int waves = a.Hkv * WPH < kMaxWaves ? a.Hkv * WPH : kMaxWaves;
     const int threads = waves * kSW;
-    const size_t lds = mfma_stage_offset(a.batch) + (size_t)waves * mfma_stage_bytes(TG);
-    if (lds > kMfmaLdsMax) return launch_r<256, float, 4, 2>(a, st);  // very large batches
-    const void* fn = reinterpret_cast<const void*>(&stream_mfma_kernel<RG, TG, ADDR>);
+    const bool fused = ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0;
+    const size_t lds = mfma_stage_offset(a.batch, fused) + (size_t)waves * mfma_stage_bytes(D, TG);
+    if (lds > kMfmaLdsMax) {  // very large batches: the vector kernel
+        if constexpr (D == 256) return launch_r<256, float, 4, 2>(a, st);
+        else return launch_r<512, float, 2, 4>(a, st);
+    }
+    constexpr bool kFusable = ADDR == kAddrPaged;
+    const void* fn = fused ? reinterpret_cast<const void*>(&stream_mfma_kernel<D, RG, TG, WPH, ADDR, kFusable>)
+                           : reinterpret_cast<const void*>(&stream_mfma_kernel<D, RG, TG, WPH, ADDR, false>);
     // Above 64 KiB of dynamic LDS a kernel must opt in (once per kernel and device).
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLdsMax) !=
         hipSuccess)
         return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
-    const int groups = (a.Hkv + kMaxWaves - 1) / kMaxWaves;
+    const int groups = (a.Hkv * WPH + kMaxWaves - 1) / kMaxWaves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
     if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
     dim3 grid(groups, a.nwg);
-    hipLaunchKernelGGL((stream_mfma_kernel<RG, TG, ADDR>), grid, dim3(threads), lds, st, a);
-    hipLaunchKernelGGL((stream_merge_kernel<256, double>), dim3(a.rows_seq, a.batch),
+    if (fused)
+        hipLaunchKernelGGL((stream_mfma_kernel<D, RG, TG, WPH, ADDR, kFusable>), grid, dim3(threads), lds, st, a);
+    else
+        hipLaunchKernelGGL((stream_mfma_kernel<D, RG, TG, WPH, ADDR, false>), grid, dim3(threads), lds, st, a);
+    if (hipGetLastError() != hipSuccess)
+        return fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
+    hipLaunchKernelGGL((stream_merge_kernel<D, double>), dim3(a.rows_seq, a.batch + (fused ? 1 : 0)),
                        dim3(kMergeNT), 0, st, a);
     return PKV_OK;
 }
@@ -1566,11 +1655,14 @@ int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
 #ifndef PKV_MFMA_TG
 #define PKV_MFMA_TG 1
 #endif
-template <int RG>
+// head_dim 256: one wave of up to 8 rows per kv head; 512: two waves of 4.
+template <int D>
 int32_t launch_mfma(StreamArgs a, hipStream_t st) {
-    if (a.keys) return launch_mfma_addr<RG, PKV_MFMA_TG, kAddrSparse>(a, st);
-    return a.ring_size > 0 ? launch_mfma_addr<RG, PKV_MFMA_TG, kAddrRing>(a, st)
-                           : launch_mfma_addr<RG, PKV_MFMA_TG, kAddrPaged>(a, st);
+    constexpr int RG = D == 256 ? 2 : 1;
+    constexpr int WPH = D == 256 ? 1 : 2;
+    if (a.keys) return launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrSparse>(a, st);
+    return a.ring_size > 0 ? launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrRing>(a, st)
+                           : launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrPaged>(a, st);
 }
 
 template <int D, typename KV, int R, int WPH>
@@ -1581,20 +1673,24 @@ int32_t launch_r(StreamArgs a, hipStream_t st) {
 }
 
 // One launch (attention + merge) for `rows` <= 8 query rows per kv head. head_dim 256:
-// one wave holds up to 4 rows (two waves of 4 for 5..8); head_dim 512: waves of 2 rows.
+// one wave holds up to 4 rows (bf16 pools: two waves of 4 for 5..8); head_dim 512: waves of
+// 2 rows. fp32 pools with 5..8 rows run on the fp64 matrix cores.
 template <typename KV>
 int32_t launch_rows(StreamArgs a, int D, int rows, hipStream_t st) {
     if (D == 256) {
         if (rows <= 1) return launch_r<256, KV, 1>(a, st);
         if (rows <= 2) return launch_r<256, KV, 2>(a, st);
         if constexpr (sizeof(KV) == 4) {  // fp32 pools: the fp64 matrix cores
-            if (rows > 4) return launch_mfma<2>(a, st);
+            if (rows > 4) return launch_mfma<256>(a, st);
         }
         if (rows <= 4) return launch_r<256, KV, 4>(a, st);
         return launch_r<256, KV, 4, 2>(a, st);
     }
     if (rows <= 1) return launch_r<512, KV, 1>(a, st);
     if (rows <= 2) return launch_r<512, KV, 2>(a, st);
+    if constexpr (sizeof(KV) == 4) {
+        if (rows > 4) return launch_mfma<512>(a, st);
+    }
     if (rows <= 4) return launch_r<512, KV, 2, 2>(a, st);
     return launch_r<512, KV, 2, 4>(a, st);
 }
@@ -1623,10 +1719,12 @@ bool stream_takes_new_rows(const pkv_params* p, int32_t q_len, int32_t batch) {
     const int rows = G * q_len;
     if (rows > 8) return false;  // one launch (no query groups)
     const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
-    if (p->head_dim == 256 && !bf16 && rows > 4) return false;  // the fp64 MFMA kernel
-    // one head group: every kv head's waves in one workgroup
+    // one head group: every kv head's waves in one workgroup (vector kernel, or the fp64
+    // MFMA kernel for fp32 pools with 5..8 rows: one wave per kv head at head_dim 256, two
+    // at 512)
     int wph = 1;
     if (p->head_dim == 256) wph = (!bf16 || rows <= 4) ? 1 : 2;
+    else if (!bf16 && rows > 4) wph = 2;
     else wph = rows <= 2 ? 1 : (rows <= 4 ? 2 : 4);
     return p->num_kv_heads * wph <= kMaxWaves;
 }
@@ -1673,9 +1771,13 @@ int32_t stream_attend(const pkv_params* p, const float* q, const void* k_pool,
     a.out = out;
     if (nr) {
         if (!stream_takes_new_rows(p, q_len, batch))
-            return fail(PKV_ERR_UNSUPPORTED, "stream path: appended rows need one vector-kernel launch");
+            return fail(PKV_ERR_UNSUPPORTED, "stream path: appended rows need one launch");
         a.nr = *nr;
     }
+    // Every launch below fits the CU's LDS if the first (the largest) does: refuse before
+    // any launch otherwise.
+    if (stream_vector_lds(batch, nr != nullptr) > kStreamLdsMax)
+        return fail(PKV_ERR_UNSUPPORTED, "stream path: batch too large for the kernel's LDS");
     const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
     // Queries in groups of at most 8 query rows per kv head, one launch pair each; the
     // launches share the workspace in stream order.

@@ -33,10 +33,20 @@ class DecodeSchedule:
     SCALE = 0.0625
 
     def __init__(self, seed: int = 0, batch: int = 32, ctx_lo: int = 128, ctx_hi: int = 8192,
-                 steps: int = 64):
+                 steps: int = 64, hkv: int | None = None, d: int | None = None,
+                 windows: tuple | None = None, scale: float | None = None):
         self.seed = seed
         self.B = batch
         self.STEPS = steps
+        if hkv is not None:
+            self.HKV = hkv
+        if d is not None:
+            self.D = d
+        # one entry per layer: its window (0 = global); the same block table serves all
+        self.windows = tuple(windows) if windows is not None else (self.WINDOW, 0)
+        self.L = len(self.windows)
+        if scale is not None:
+            self.SCALE = scale
         rng = np.random.default_rng(seed)
         B, bs = self.B, self.BS
         self.kv_stride = self.HKV * self.D
@@ -66,10 +76,21 @@ class DecodeSchedule:
         self.max_pos = int(self.pos.max())
         base = int(rng.integers(1, 2**40))
         # seeds of the float streams
-        self.seed_pool = [[base + 10 * layer + kv for kv in range(2)] for layer in range(2)]
+        self.seed_pool = [[base + 10 * layer + kv for kv in range(2)] for layer in range(self.L)]
         self.seed_q = base + 100
         self.seed_knew, self.seed_vnew = base + 101, base + 102
         self.seed_admit_k, self.seed_admit_v = base + 103, base + 104
+
+    @classmethod
+    def engine_global(cls, seed: int = 0, **kw) -> "DecodeSchedule":
+        """Config 2's schedule on the engine's own global-layer geometry: 16 q / 2 kv heads,
+        head_dim 512 (model_speculative_moe_batched.mojo:1905-1907; the MTP assistant's
+        last layer reads that pool too, :756-760), one full-attention layer, fp32 pools.
+        Softmax scale 2^-4, as config 2 (the engine's RMS-normed Q and K take scale 1; N(0, 1)
+        data needs a scale near 1/sqrt(D) to keep the softmax from collapsing onto one key,
+        and a power of two keeps the scaled query exact in fp32 for the reference path,
+        which multiplies q by the scale in fp32)."""
+        return cls(seed=seed, hkv=2, d=512, windows=(0,), scale=0.0625, **kw)
 
     @property
     def admit_rows(self) -> int:
@@ -78,18 +99,19 @@ class DecodeSchedule:
     def device_data(self, stream=None) -> dict:
         """All float inputs on the device, generated from their seeds."""
         rows = self.num_blocks * self.BS
+        L = self.L
         d = {"pools": [[synth.normal((rows, self.kv_stride), self.seed_pool[l][kv],
-                                     stream=stream) for kv in range(2)] for l in range(2)],
-             "q": synth.normal((self.STEPS, 2, self.B, 1, self.HQ, self.D), self.seed_q,
+                                     stream=stream) for kv in range(2)] for l in range(L)],
+             "q": synth.normal((self.STEPS, L, self.B, 1, self.HQ, self.D), self.seed_q,
                                stream=stream),
-             "k_new": synth.normal((self.STEPS, 2, self.B, self.kv_stride), self.seed_knew,
+             "k_new": synth.normal((self.STEPS, L, self.B, self.kv_stride), self.seed_knew,
                                    stream=stream),
-             "v_new": synth.normal((self.STEPS, 2, self.B, self.kv_stride), self.seed_vnew,
+             "v_new": synth.normal((self.STEPS, L, self.B, self.kv_stride), self.seed_vnew,
                                    stream=stream)}
         ne = max(len(self.events), 1)
-        d["admit_k"] = synth.normal((ne, 2, self.admit_rows, self.kv_stride),
+        d["admit_k"] = synth.normal((ne, L, self.admit_rows, self.kv_stride),
                                     self.seed_admit_k, stream=stream)
-        d["admit_v"] = synth.normal((ne, 2, self.admit_rows, self.kv_stride),
+        d["admit_v"] = synth.normal((ne, L, self.admit_rows, self.kv_stride),
                                     self.seed_admit_v, stream=stream)
         d["event_index"] = {j: i for i, j in enumerate(sorted(self.events))}
         return d
@@ -114,9 +136,10 @@ class DecodeSchedule:
         return np.arange(self.B + 1, dtype=np.int32)
 
     def keys_attended(self, j: int, layer: int) -> np.ndarray:
-        """Keys each sequence's query attends at step j (window 1024 on layer 0)."""
+        """Keys each sequence's query attends at step j (the layer's window, 0 = all)."""
         n = self.pos[j].astype(np.int64) + 1
-        return np.minimum(n, self.WINDOW) if layer == 0 else n
+        w = self.windows[layer]
+        return np.minimum(n, w) if w > 0 else n
 
     def attend_bytes(self, j: int, layer: int, elt: int = 4) -> int:
         """Algorithmic HBM bytes of one attention launch: each attended K and V row

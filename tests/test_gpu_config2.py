@@ -20,7 +20,11 @@ Checked:
     float64 attention, by the parity rule of tests/parity.py. The test prints the largest
     error against the fp32 reference next to the literal 1e-4 bound, together with that
     reference's own distance from the float64 attention (on these long contexts the fp32
-    reference itself sits ~1.2e-4 from exact; the GPU accumulates in double)."""
+    reference itself sits ~1.2e-4 from exact; the GPU accumulates in double).
+
+test_engine_global512_schedule_append_attend runs the same schedule on the engine's
+global-layer geometry (16q / 2kv / 512, one full-attention layer): bench.py --leg
+global512."""
 import numpy as np
 import pytest
 
@@ -43,19 +47,18 @@ def _compare_state(cache, st, what):
 
 
 def _compare_pools(cache, st, what):
-    for layer in range(2):
+    for layer in range(len(cache.k_pools)):
         for name, dev, ref in (("K", cache.k_pools[layer], st.k_pools[layer]),
                                ("V", cache.v_pools[layer], st.v_pools[layer])):
             assert np.array_equal(dev.numpy().reshape(-1), ref), \
                 f"{what}: layer {layer} {name} pool differs"
 
 
-def test_config2_full_schedule_append_attend(gpu):
-    print("[config2] building the 64-step schedule (seed 0)", flush=True)
-    w = DecodeSchedule(seed=0)
-    B = w.B
+def _run_schedule(w, tag):
+    """Every call of the schedule through the C ABI, replayed on the oracle's state."""
+    B, L = w.B, w.L
     d = w.device_data()
-    layers = [LayerSpec(w.HQ, w.HKV, w.D, window=w.WINDOW), LayerSpec(w.HQ, w.HKV, w.D, window=0)]
+    layers = [LayerSpec(w.HQ, w.HKV, w.D, window=win) for win in w.windows]
     cache = PagedKVCache(layers, block_size=w.BS, num_blocks=w.num_blocks, max_seqs=B,
                          max_blocks_per_seq=w.table_stride, max_q_len=1, max_pos=w.max_pos,
                          scale=w.SCALE)
@@ -65,12 +68,12 @@ def test_config2_full_schedule_append_attend(gpu):
     fl[:w.free0.size] = w.free0
     cache.free_list.upload(fl)
     cache.free_count.upload(np.array([w.free0.size], np.int32))
-    st = O.CacheState(2, w.kv_stride, w.BS, w.num_blocks, B, w.table_stride, alloc_pools=False)
+    st = O.CacheState(L, w.kv_stride, w.BS, w.num_blocks, B, w.table_stride, alloc_pools=False)
     st.tables[:] = w.tables0
     st.table_lens[:] = w.lens0
     st.bm.free_list[:w.free0.size] = w.free0
     st.bm.count[0] = w.free0.size
-    for layer in range(2):
+    for layer in range(L):
         cache.k_pools[layer].copy_from(d["pools"][layer][0])
         cache.v_pools[layer].copy_from(d["pools"][layer][1])
         st.k_pools[layer] = d["pools"][layer][0].numpy().reshape(-1)
@@ -93,8 +96,8 @@ def test_config2_full_schedule_append_attend(gpu):
             st.rollback(nl)
             assert np.all(rc == 0), f"{what}: rollback status {rc}"
             _compare_state(cache, st, f"{what} after rollback")
-            for layer in range(2):
-                base = (e * 2 + layer) * w.admit_rows * row_bytes
+            for layer in range(L):
+                base = (e * L + layer) * w.admit_rows * row_bytes
                 sts = cache.append(layer, w.admit_pos(j), w.admit_tok_off(j),
                                    d["admit_k"].ptr + base, d["admit_v"].ptr + base,
                                    w.ADMIT_CTX, w.admit_rows).numpy()
@@ -103,9 +106,10 @@ def test_config2_full_schedule_append_attend(gpu):
                 assert np.array_equal(sts, ref) and np.all(sts == 0), f"{what}: admit status"
                 _compare_state(cache, st, f"{what} after admission, layer {layer}")
             _compare_pools(cache, st, what)
-        for layer in range(2):
-            what = f"step {j} layer {'sliding' if layer == 0 else 'global'}"
-            off = j * 2 + layer
+        for layer in range(L):
+            window = w.windows[layer]
+            what = f"step {j} layer {layer} ({'sliding' if window > 0 else 'global'})"
+            off = j * L + layer
             sts = cache.append_attend(layer, w.pos[j], dec_off, d["k_new"].ptr + off * kvstep,
                                       d["v_new"].ptr + off * kvstep, 1, B,
                                       d["q"].ptr + off * qstep, 1, out).numpy()
@@ -113,7 +117,6 @@ def test_config2_full_schedule_append_attend(gpu):
             assert np.array_equal(sts, ref_st) and np.all(sts == 0), f"{what}: status {sts}"
             _compare_state(cache, st, what)
             got = out.numpy()
-            window = w.WINDOW if layer == 0 else 0
             ref = O.attend(qh[j, layer], st.k_pools[layer], st.v_pools[layer], st.tables,
                            st.table_lens, w.pos[j], 1, w.HQ, w.HKV, w.D, w.BS, window,
                            scale=w.SCALE, nthreads=nthreads, par=1)
@@ -124,12 +127,26 @@ def test_config2_full_schedule_append_attend(gpu):
             worst32, worst64 = max(worst32, e32), max(worst64, e64)
             worst_own = max(worst_own, O.max_rel_err(ref, exact))
         if j % 8 == 7:
-            print(f"[config2] steps 0..{j} green: max rel err {worst32:.3g} vs the fp32 "
+            print(f"[{tag}] steps 0..{j} green: max rel err {worst32:.3g} vs the fp32 "
                   f"reference (literal bound {parity.TOL_F32:g}; that reference's own error "
                   f"vs float64 {worst_own:.3g}), {worst64:.3g} vs float64 (bound "
                   f"{parity.TOL_EXACT:g})", flush=True)
     _compare_pools(cache, st, "after the last step")
-    print(f"[config2] 64 steps x 2 layers: state and pools bit-exact; max rel err "
+    print(f"[{tag}] {w.STEPS} steps x {L} layers: state and pools bit-exact; max rel err "
           f"{worst32:.3g} vs the fp32 reference (literal 1e-4; reference's own error "
           f"{worst_own:.3g}), {worst64:.3g} vs float64", flush=True)
     cache.free()
+
+
+def test_config2_full_schedule_append_attend(gpu):
+    print("[config2] building the 64-step schedule (seed 0)", flush=True)
+    _run_schedule(DecodeSchedule(seed=0), "config2")
+
+
+def test_engine_global512_schedule_append_attend(gpu):
+    """The same 64-step schedule on the engine's global-layer geometry (16 q / 2 kv heads,
+    head_dim 512, model_speculative_moe_batched.mojo:1905-1907; the MTP assistant's last
+    layer reads that pool, :756-760): one full-attention fp32 layer, B = 32, contexts
+    U[128, 8192], the bench's --leg global512 workload."""
+    print("[global512] building the 64-step schedule (seed 0)", flush=True)
+    _run_schedule(DecodeSchedule.engine_global(seed=0), "global512")
