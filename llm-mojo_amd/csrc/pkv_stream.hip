@@ -53,6 +53,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "pkv_internal.h"
 
 namespace pkv {
@@ -1009,6 +1011,40 @@ __device__ inline double block_sum(double v) {
     return v + dpp<ror_ctrl<8>()>(v);
 }
 
+// LDS reads the compiler does not track. It cannot tell which LDS words a direct-to-LDS
+// copy in flight writes, so before any LDS read it sees it waits for every copy
+// (vmcnt(0)) -- including the next batch's, which must stay in flight. These reads are
+// inline assembly, and lgkm_tie0 ties their values to an explicit s_waitcnt lgkmcnt(0),
+// so no use is scheduled above it.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+template <int OFF>
+__device__ inline i32x4 lds_b128(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    i32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+template <int N>
+__device__ inline void lgkm_tie0(i32x4 (&k)[N], i32x4 (&v)[N]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k[0]), "+v"(v[0]));
+#pragma unroll
+    for (int i = 1; i < N; ++i) asm volatile("" : "+v"(k[i]), "+v"(v[i]));
+}
+// s_waitcnt vmcnt(N), the other counters at their maxima.
+template <int N>
+__device__ inline void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+template <int I, int N, typename F>
+__device__ inline void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
 // FUSED: the launch of a fused append (paged pools); a separate instance, so the scalar
 // state of the appended rows costs the other launches nothing.
 template <int D, int RG, int TG, int WPH, int ADDR, bool FUSED>
@@ -1042,9 +1078,14 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int k0 = sp.start(w);
     if (k0 >= total) return;
     const int k1 = min(total, sp.start(w + 1));
-    const int g = blockIdx.x * (kMaxWaves / WPH) + wave / WPH;  // this wave's KV head
+    // this wave's KV head. With WPH > 1 the waves of a head share its staging and meet at
+    // barriers, so a wave past the last head (a head group with fewer heads) does the work of
+    // the last head and stores nothing, instead of leaving.
+    const int g_raw = blockIdx.x * (kMaxWaves / WPH) + wave / WPH;
+    if (WPH == 1 && g_raw >= a.Hkv) return;
+    const bool idle = g_raw >= a.Hkv;
+    const int g = idle ? a.Hkv - 1 : g_raw;
     const int rb = (wave % WPH) * 4 * RG;  // first of this wave's rows of the head
-    if (g >= a.Hkv) return;
 
     const int rows = a.G * a.q_cnt;
     const size_t row_bytes = (size_t)a.Hkv * D * 4;
@@ -1054,8 +1095,15 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int kdo = 64 * b + 16 * y;  // bytes of d = 16b + 4y in a 64-d chunk (K operand)
     const int vdo = 64 * b + 16 * x;  // bytes of d = 16b + 4x (V operand)
     const int bs_mask = (1 << a.bs_shift) - 1;
+    // Staging. WPH 1: one buffer per wave, loaded and read by that wave. WPH > 1: two
+    // buffers per head (batches i and i + 1 in flight together), each wave of the head
+    // copying its share of every row slice (CPW of the slice's 1 KiB chunks).
+    constexpr int CPW = (D / 256) / WPH;
+    static_assert(WPH == 1 || CPW * WPH == D / 256, "chunks per wave");
     char* stage = reinterpret_cast<char*>(smem) + mfma_stage_offset(B, fused) +
-                  (size_t)wave * mfma_stage_bytes(D, TG);
+                  (WPH == 1 ? (size_t)wave * mfma_stage_bytes(D, TG)
+                            : (size_t)(wave / WPH) * 2 * mfma_stage_bytes(D, TG));
+    const int c0 = WPH == 1 ? 0 : (wave % WPH) * CPW;  // first chunk this wave copies
     // Waves w and w + 4 of an 8-wave workgroup share a SIMD, whose issue slots bound the
     // batch loop; the arbiter favours the older wave, which left the other one alone for
     // the last ~15% of a piece. Alternating their priorities every batch keeps the two in
@@ -1236,7 +1284,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                     }
                 }
 #pragma unroll
-                for (int c = 0; c < D / 256; ++c) {
+                for (int cc = 0; cc < (WPH == 1 ? D / 256 : CPW); ++cc) {
+                    const int c = c0 + cc;
                     __builtin_amdgcn_global_load_lds(uniform_ptr(kb + off + 1024 * c) + 16 * lane,
                                                      (lds_void*)(buf + (2 * j) * kSlot + 1024 * c),
                                                      16, 0, kCpol);
@@ -1247,23 +1296,56 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
             }
         };
 
+        constexpr int kBufBytes = (int)mfma_stage_bytes(D, TG);
         issue(ta, stage);
-        for (int t = ta; t < tb; t += U) {
-            if (toggle) {
-                if ((((t - ta) / U) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
-                else __builtin_amdgcn_s_setprio(0);
-            }
-            __builtin_amdgcn_s_waitcnt(0);  // this batch's slices are in LDS
+        if (WPH > 1 && ta + U < tb) issue(ta + U, stage + kBufBytes);
+        int it = 0;  // batch index in the piece (WPH > 1: buffer it % 2)
+        for (int t = ta; t < tb; t += U, ++it) {
             float4 kw[TG][NQ], vw[TG][NQ];
+            if constexpr (WPH == 1) {
+                if (toggle) {
+                    if ((((t - ta) / U) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+                    else __builtin_amdgcn_s_setprio(0);
+                }
+                __builtin_amdgcn_s_waitcnt(0);  // this batch's slices are in LDS
 #pragma unroll
-            for (int tg = 0; tg < TG; ++tg)
+                for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q) {
+                        kw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + x)) * kSlot + kdo + 256 * q);
+                        vw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + y) + 1) * kSlot + vdo + 256 * q);
+                    }
+                __builtin_amdgcn_s_waitcnt(kLgkm0);  // read out before the slots are refilled
+                if (t + U < tb) issue(t + U, stage);
+            } else {
+                // This wave's copies of batch it have landed (those of batch it + 1, if issued,
+                // stay in flight); the barrier then covers the other waves' copies. It carries no
+                // fence, which would wait for the copies in flight.
+                constexpr int kCopies = U * 2 * CPW;  // copies per batch and wave
+                if (t + U < tb) wait_vm<kCopies>();
+                else wait_vm<0>();
+                __builtin_amdgcn_s_barrier();
+                char* buf = stage + (it & 1) * kBufBytes;
+                const uint32_t ka = lds_addr(buf) + (2 * x) * kSlot + kdo;
+                const uint32_t va = lds_addr(buf) + (2 * y + 1) * kSlot + vdo;
+                static_assert(TG == 1, "one 4-token group per batch");
+                i32x4 kr[NQ], vr[NQ];
+                static_for<0, NQ>([&](auto Q) {
+                    constexpr int q = decltype(Q)::value;
+                    kr[q] = lds_b128<256 * q>(ka);
+                    vr[q] = lds_b128<256 * q>(va);
+                });
+                lgkm_tie0(kr, vr);
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) {
-                    kw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + x)) * kSlot + kdo + 256 * q);
-                    vw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + y) + 1) * kSlot + vdo + 256 * q);
+                    kw[0][q] = __builtin_bit_cast(float4, kr[q]);
+                    vw[0][q] = __builtin_bit_cast(float4, vr[q]);
                 }
-            __builtin_amdgcn_s_waitcnt(kLgkm0);  // read out before the slots are refilled
-            if (t + U < tb) issue(t + U, stage);
+                // every wave of the head has read the buffer: refill it with batch it + 2
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                if (t + 2 * U < tb) issue(t + 2 * U, buf);
+            }
 
             // S^T, then the block sums
             double sc[TG][RG];
@@ -1367,7 +1449,9 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
 #pragma unroll
                 for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(o[rg][q][e]));
         }
-        if (single) {
+        if (idle) {
+            // a wave past the last head: nothing to store
+        } else if (single) {
 #pragma unroll
             for (int rg = 0; rg < RG; ++rg) {
                 const int r = rb + 4 * rg + x;
