@@ -583,10 +583,10 @@ __device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_
 // (held: the table, granted: the free list), so this launch reads no state it writes.
 template <int D, typename KV, int WPH>
 __device__ inline void copy_new_rows(const StreamArgs& a, const int* s_meta, const int* s_al,
-                                     int wave, int lane) {
+                                     int g_first, int wave, int lane) {
     constexpr int kElt = SKV<KV>::kElt;
     constexpr int kVec = D * kElt / 16;  // 16-byte vectors per head slice
-    const int g = wave / WPH;
+    const int g = g_first + wave / WPH;
     if (wave % WPH != 0 || g >= a.Hkv) return;
     const size_t row_bytes = (size_t)a.Hkv * D * kElt;
     const size_t head_off = (size_t)g * D * kElt;
@@ -664,7 +664,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
 
     const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, s_al);
     const bool fused = PAGED && fused_append(a);
-    if (fused) copy_new_rows<D, KV, WPH>(a, s_meta, s_al, wave, lane);
+    if (fused) copy_new_rows<D, KV, WPH>(a, s_meta, s_al, blockIdx.x * (kMaxWaves / WPH), wave, lane);
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
@@ -1055,9 +1055,11 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     constexpr bool RING = ADDR == kAddrRing;
     constexpr bool SPARSE = ADDR == kAddrSparse;
     constexpr bool PAGED = ADDR == kAddrPaged;
-    // Rows that one wave alone reads are loaded with the NT bit; with WPH > 1 the other
-    // waves of the head read them in turn from the L2.
-    constexpr int kCpol = WPH == 1 ? kCpolNT : 0;
+    // Every chunk of a row slice is copied by one wave only (WPH > 1: the waves of a head
+    // share the staging), so the rows are loaded with the NT bit: a launch streams ~1 GB
+    // once, which would otherwise displace what is reused (partials, tables, Q). Head_dim
+    // 512, 2 kv heads, B = 32: 215.8 -> 207.6 us per launch (same box).
+    constexpr int kCpol = kCpolNT;
     extern __shared__ int smem[];
     int* s_pre = smem;               // [batch + 1]
     int* s_lo = smem + a.batch + 1;  // [batch]
@@ -1073,7 +1075,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     static_assert(!FUSED || PAGED, "appended rows: paged pools only");
     const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, s_al);
     constexpr bool fused = FUSED;  // the launcher passes the rows exactly when FUSED
-    if (fused) copy_new_rows<D, float, WPH>(a, s_meta, s_al, wave, lane);
+    const int hpw = ufirst((int)(blockDim.x / kSW) / WPH);  // kv heads per workgroup
+    if (fused) copy_new_rows<D, float, WPH>(a, s_meta, s_al, blockIdx.x * hpw, wave, lane);
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
@@ -1081,7 +1084,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     // this wave's KV head. With WPH > 1 the waves of a head share its staging and meet at
     // barriers, so a wave past the last head (a head group with fewer heads) does the work of
     // the last head and stores nothing, instead of leaving.
-    const int g_raw = blockIdx.x * (kMaxWaves / WPH) + wave / WPH;
+    const int g_raw = blockIdx.x * hpw + wave / WPH;
     if (WPH == 1 && g_raw >= a.Hkv) return;
     const bool idle = g_raw >= a.Hkv;
     const int g = idle ? a.Hkv - 1 : g_raw;
@@ -1701,9 +1704,15 @@ template <int D, typename KV, int R, int WPH = 1>
 int32_t launch_r(StreamArgs a, hipStream_t st);
 constexpr size_t kMfmaLdsMax = kStreamLdsMax;
 
+#ifndef PKV_MFMA_HEADS_PER_WG
+#define PKV_MFMA_HEADS_PER_WG 2
+#endif
 template <int D, int RG, int TG, int WPH, int ADDR>
 int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
-    const int waves = a.Hkv * WPH < kMaxWaves ? a.Hkv * WPH : kMaxWaves;
+    // WPH > 1: the waves of a head meet at a barrier every batch, so a workgroup holds few
+    // heads (a barrier waits for every wave of the workgroup).
+    constexpr int kHeadsMax = WPH == 1 ? kMaxWaves : PKV_MFMA_HEADS_PER_WG;
+    const int waves = (a.Hkv < kHeadsMax ? a.Hkv : kHeadsMax) * WPH;
     const int threads = waves * kSW;
     const bool fused = ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0;
     const size_t lds = mfma_stage_offset(a.batch, fused) + (size_t)waves * mfma_stage_bytes(D, TG);
@@ -1720,7 +1729,7 @@ int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
         return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
-    const int groups = (a.Hkv * WPH + kMaxWaves - 1) / kMaxWaves;
+    const int groups = (a.Hkv * WPH + waves - 1) / waves;
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
     if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
@@ -1803,12 +1812,10 @@ bool stream_takes_new_rows(const pkv_params* p, int32_t q_len, int32_t batch) {
     const int rows = G * q_len;
     if (rows > 8) return false;  // one launch (no query groups)
     const bool bf16 = p->kv_dtype == PKV_DTYPE_BF16;
-    // one head group: every kv head's waves in one workgroup (vector kernel, or the fp64
-    // MFMA kernel for fp32 pools with 5..8 rows: one wave per kv head at head_dim 256, two
-    // at 512)
+    if (!bf16 && rows > 4) return true;  // the fp64 MFMA kernel (any number of head groups)
+    // vector kernel: one head group, every kv head's waves in one workgroup
     int wph = 1;
-    if (p->head_dim == 256) wph = (!bf16 || rows <= 4) ? 1 : 2;
-    else if (!bf16 && rows > 4) wph = 2;
+    if (p->head_dim == 256) wph = rows <= 4 ? 1 : 2;
     else wph = rows <= 2 ? 1 : (rows <= 4 ? 2 : 4);
     return p->num_kv_heads * wph <= kMaxWaves;
 }
