@@ -1098,9 +1098,11 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int kdo = 64 * b + 16 * y;  // bytes of d = 16b + 4y in a 64-d chunk (K operand)
     const int vdo = 64 * b + 16 * x;  // bytes of d = 16b + 4x (V operand)
     const int bs_mask = (1 << a.bs_shift) - 1;
-    // Staging. WPH 1: one buffer per wave, loaded and read by that wave. WPH > 1: two
-    // buffers per head (batches i and i + 1 in flight together), each wave of the head
-    // copying its share of every row slice (CPW of the slice's 1 KiB chunks).
+    // Staging. WPH 1: one buffer per wave, loaded and read by that wave (two buffers, with
+    // the reads untracked, measured no faster: 129.5-130.9 against 128.0-128.4 us for the
+    // config 5 verify launch). WPH > 1: two buffers per head (batches i and i + 1 in flight
+    // together), each wave of the head copying its share of every row slice (CPW of the
+    // slice's 1 KiB chunks).
     constexpr int CPW = (D / 256) / WPH;
     static_assert(WPH == 1 || CPW * WPH == D / 256, "chunks per wave");
     char* stage = reinterpret_cast<char*>(smem) + mfma_stage_offset(B, fused) +
@@ -1753,7 +1755,9 @@ template <int D>
 int32_t launch_mfma(StreamArgs a, hipStream_t st) {
     constexpr int RG = D == 256 ? 2 : 1;
     constexpr int WPH = D == 256 ? 1 : 2;
-    if (a.keys) return launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrSparse>(a, st);
+    if constexpr (D == 256) {
+        if (a.keys) return launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrSparse>(a, st);
+    }
     return a.ring_size > 0 ? launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrRing>(a, st)
                            : launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrPaged>(a, st);
 }
@@ -1782,7 +1786,9 @@ int32_t launch_rows(StreamArgs a, int D, int rows, hipStream_t st) {
     if (rows <= 1) return launch_r<512, KV, 1>(a, st);
     if (rows <= 2) return launch_r<512, KV, 2>(a, st);
     if constexpr (sizeof(KV) == 4) {
-        if (rows > 4) return launch_mfma<512>(a, st);
+        // Key lists (LSA) are a few hundred keys per sequence, pieces of a few dozen keys:
+        // there the vector kernel's shorter start wins (LSA shape 40 against 51 us).
+        if (rows > 4 && !a.keys) return launch_mfma<512>(a, st);
     }
     if (rows <= 4) return launch_r<512, KV, 2, 2>(a, st);
     return launch_r<512, KV, 2, 4>(a, st);
