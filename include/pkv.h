@@ -182,14 +182,15 @@ int32_t pkv_decode(void* stream, const pkv_params* p, const float* q, const void
  * writes the new tokens' K/V into the paged cache and attends over it
  * (model_speculative_moe_batched.mojo:1996, :2625, :3111 write sites; :3090-3123 verify).
  * Block tables, table lengths, free list, status, every pool byte and out are those of the
- * two separate calls, with one exception: a sequence whose allocation fails
- * (PKV_SEQ_OUT_OF_BLOCKS, or PKV_SEQ_BAD_BLOCK from a free count out of range) attends
- * positions its append did not write, through table entries past its length; if such an
- * entry names another sequence's block, the fused launch may read that row before or
- * after this call's append writes it.
- * When one launch of the stream kernel's vector path covers the call (paged pools,
- * head_dim 256 or 512, G * q_len <= 8 on the vector kernel, every kv head in one
- * workgroup, batch <= 1024), that launch also computes the block allocation from the
+ * two separate calls, with one exception: a sequence whose append fails (status
+ * PKV_SEQ_OUT_OF_BLOCKS, PKV_SEQ_TABLE_FULL, PKV_SEQ_BAD_ARGS, or PKV_SEQ_BAD_BLOCK from a
+ * free count out of range) is not attended -- the engine skips its attention
+ * (model_speculative_moe_batched.mojo:1989-1992) -- and gets NaN rows where the separate
+ * calls would attend positions the append did not write.
+ * When one launch of the stream kernel covers the call (paged pools, head_dim 256 or 512,
+ * G * q_len <= 8, batch <= 1024; on the vector kernel, fp32 pools with up to 4 rows per kv
+ * head or bf16 pools, every kv head in one workgroup; fp32 pools with 5..8 rows per kv
+ * head run the fp64 MFMA kernel), that launch also computes the block allocation from the
  * state as it stands before the call, copies the appended rows into the pool and reads
  * them from k_new / v_new; the merge launch after it writes the new table entries,
  * table_lens, free_count and status. No allocation or scatter launch is made, and no

@@ -716,6 +716,11 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         const bool live_own = row_live && rb + r_own < rows_s;
         int pgbase = -kSW;  // page index (sparse: list index) held by lane 0 of vpg
         int vpg = 0;
+        // NaN rows: a table entry outside the pool, or (fused append) a sequence whose append
+        // fails -- OUT_OF_BLOCKS, TABLE_FULL, BAD_ARGS, BAD_BLOCK from a free count out of
+        // range. The engine skips the attention of such a sequence
+        // (model_speculative_moe_batched.mojo:1989-1992); its pieces still run, so the key
+        // split of the others is that of the separate calls.
         bool bad = false;
         // Fused append: table indices [g_lo, g_hi) are the blocks granted in this call, whose
         // entries the merge launch writes: their ids come from the free list (g_top - index).
@@ -725,6 +730,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             g_lo = ufirst(al.len);
             g_hi = g_lo + ufirst(al.granted);
             g_top = ufirst(al.fc) - 1 - ufirst(al.pref) + g_lo;
+            bad = ufirst(al.code) != PKV_SEQ_OK;  // a failed append: NaN rows (see below)
         }
         // Pool rows of the 64 keys from t on: sparse, lane l reads listed key t + l and its
         // block's table entry; paged, lane l reads the page id of page (t >> bs_shift) + l.
@@ -1146,8 +1152,10 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         // read from k_new / v_new (row nr0 + t - pn_lo).
         int g_lo = INT32_MAX, g_hi = INT32_MIN, g_top = 0;
         int pn_lo = INT32_MAX, pn_hi = INT32_MIN, nr0 = 0;
+        bool failed = false;  // a failed append: NaN rows, as in the vector kernel
         if (fused) {
             const SeqAlloc al = seq_alloc(s_al, B, a.num_blocks, s);
+            failed = ufirst(al.code) != PKV_SEQ_OK;
             g_lo = ufirst(al.len);
             g_hi = g_lo + ufirst(al.granted);
             g_top = ufirst(al.fc) - 1 - ufirst(al.pref) + g_lo;
@@ -1212,7 +1220,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         }
         int pgbase = -kSW;  // page index (sparse: list index) held by lane 0 of vpg
         int vpg = 0;
-        bool bad = false;
+        bool bad = failed;
         asm volatile("" ::: "memory");  // the query rows go out before the table lookup
         // (branch-free, so the compiler does not move a load into a branch)
         if constexpr (SPARSE) {  // the first listed keys' table entries (one more round trip)

@@ -46,11 +46,12 @@ def _same(a, b, what):
 
 
 @pytest.mark.parametrize("geom,kv_dtype,q_len", [
-    ((16, 8, 256), F32, 1),     # decode: fused
-    ((16, 8, 256), BF16, 2),    # bf16, 4 rows: fused
-    ((16, 2, 512), F32, 1),     # 8 rows per kv head at 512: fused (4 waves per head)
-    ((16, 8, 256), F32, 4),     # fp64 MFMA verify: appends first
-], ids=["f32-decode", "bf16-q2", "d512-g8", "mfma-verify"])
+    ((16, 8, 256), F32, 1),     # decode: fused, vector kernel
+    ((16, 8, 256), BF16, 2),    # bf16, 4 rows: fused, vector kernel
+    ((16, 2, 512), F32, 1),     # 8 rows per kv head at 512: fused, fp64 MFMA kernel
+    ((16, 8, 256), F32, 4),     # verify, 8 rows per kv head: fused, fp64 MFMA kernel
+    ((16, 2, 512), BF16, 1),    # bf16 at 512, 8 rows: fused, vector kernel (4 waves per head)
+], ids=["f32-decode", "bf16-q2", "d512-g8", "mfma-verify", "d512-g8-bf16"])
 def test_append_attend_matches_append_then_attend(gpu, geom, kv_dtype, q_len):
     print(f"[append_attend] {geom} {kv_dtype} q_len={q_len}", flush=True)
     rng = np.random.default_rng(q_len * 13 + geom[2])
@@ -97,11 +98,13 @@ def test_append_attend_matches_append_then_attend(gpu, geom, kv_dtype, q_len):
         _same(a["free_list"], b["free_list"], f"{what}: free list")
         _same(fused.k_pools[0].numpy(), sep.k_pools[0].numpy(), f"{what}: K pool")
         _same(fused.v_pools[0].numpy(), sep.v_pools[0].numpy(), f"{what}: V pool")
-        # A sequence that ran out of blocks attends positions its append did not write,
-        # through stale table entries (pkv.h: the one case where the fused launch may
-        # read another sequence's row before or after its write); every other row matches.
+        # A sequence that ran out of blocks is not attended by the fused call: NaN rows
+        # (the separate calls attend positions its append did not write, through stale
+        # table entries); every other row matches.
         keep = st_s != lib.PKV_SEQ_OUT_OF_BLOCKS
-        _same(out_f.numpy()[keep], out_s.numpy()[keep], f"{what}: outputs")
+        got = out_f.numpy()
+        _same(got[keep], out_s.numpy()[keep], f"{what}: outputs")
+        assert np.all(np.isnan(got[~keep])), f"{what}: rows of a failed append"
         assert st_f[3] == lib.PKV_SEQ_BAD_BLOCK, "the out-of-pool entry is reported"
         pos = np.where(pos >= 0, pos + q_len, pos).astype(np.int32)
     fused.free()
@@ -141,8 +144,13 @@ def test_append_attend_unsupported_geometry_changes_nothing(gpu):
     c.free()
 
 
-@pytest.mark.parametrize("kv_dtype,q_len", [(F32, 1), (BF16, 2)], ids=["f32-decode", "bf16-q2"])
-def test_append_attend_allocation_follows_oracle(gpu, kv_dtype, q_len):
+@pytest.mark.parametrize("kv_dtype,q_len,geom", [
+    (F32, 1, (16, 8, 256)),   # vector kernel
+    (BF16, 2, (16, 8, 256)),  # vector kernel, two waves per kv head
+    (F32, 4, (16, 8, 256)),   # fp64 MFMA kernel (8 rows per kv head)
+    (F32, 1, (16, 2, 512)),   # fp64 MFMA kernel at the engine's global geometry
+], ids=["f32-decode", "bf16-q2", "f32-q4-mfma", "g512-decode-mfma"])
+def test_append_attend_allocation_follows_oracle(gpu, kv_dtype, q_len, geom):
     """The fused launch computes the block allocation itself (the merge launch writes the
     state): every status the allocation gives -- a new table, a block opened mid-batch,
     TABLE_FULL, an inactive slot, a free list that runs dry part-way (OUT_OF_BLOCKS),
@@ -150,10 +158,12 @@ def test_append_attend_allocation_follows_oracle(gpu, kv_dtype, q_len):
     oracle's block manager (O.CacheState) and the pools against its append; then a free
     count outside [0, num_blocks] (BAD_BLOCK for the sequences that need blocks, count
     left as is) against pkv_append + pkv_attend on a second cache. Outputs equal the two
-    separate calls wherever the allocation gave OK."""
-    print(f"[append_attend] allocation statuses {kv_dtype} q_len={q_len}", flush=True)
+    separate calls wherever the allocation gave OK; a sequence whose append failed is not
+    attended and its rows are NaN (the engine skips its attention,
+    model_speculative_moe_batched.mojo:1989-1992)."""
+    print(f"[append_attend] allocation statuses {kv_dtype} q_len={q_len} geom={geom}", flush=True)
     rng = np.random.default_rng(40 + q_len)
-    hq, hkv, d = 16, 8, 256
+    hq, hkv, d = geom
     B, stride, nb = 6, 3, 16
     spec = LayerSpec(hq, hkv, d, window=0, kv_dtype=kv_dtype)
     kvs = spec.kv_stride
@@ -222,7 +232,11 @@ def test_append_attend_allocation_follows_oracle(gpu, kv_dtype, q_len):
         _same(fused.k_pools[0].numpy(), sep.k_pools[0].numpy(), f"round {rnd}: K pool")
         _same(fused.v_pools[0].numpy(), sep.v_pools[0].numpy(), f"round {rnd}: V pool")
         ok = st_f == lib.PKV_SEQ_OK
-        _same(out_f.numpy()[ok], out_s.numpy()[ok], f"round {rnd}: outputs of OK sequences")
+        got = out_f.numpy()
+        _same(got[ok], out_s.numpy()[ok], f"round {rnd}: outputs of OK sequences")
+        failed = ~ok & (pos >= 0)
+        assert failed.any(), "the round has a failed append"
+        assert np.all(np.isnan(got[failed])), f"round {rnd}: failed appends give NaN rows"
         if rnd == 0:
             ref = st.append(0, pos, tok_off, k_new, v_new, q_len)
             _same(st_f, ref, "status vs oracle")
