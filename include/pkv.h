@@ -221,7 +221,10 @@ int32_t pkv_append_attend(void* stream, const pkv_params* p, void* k_pool, void*
  * call on each device; the call allocates nothing. A call whose partials cannot fit
  * (batch + 1 slots of num_heads * q_len rows of (head_dim + 2) doubles) gives
  * PKV_ERR_WORKSPACE. Every call on one GPU shares that array: calls that overlap on a
- * GPU (other streams, other host threads) race, so order them on one stream. */
+ * GPU (other streams, other host threads) race, so order them on one stream. Under HIP
+ * graph capture (relaxed mode): make one call with the same shape on the device first
+ * (the first call on a device looks up the array's address and the kernels' occupancy);
+ * the captured graph then replays with whatever the inputs hold at each launch. */
 int32_t pkv_attend_noalloc(void* stream, const pkv_params* p, const float* q,
                            const void* k_pool, const void* v_pool, const int32_t* block_tables,
                            int32_t table_stride, const int32_t* pos, int32_t q_len,

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "pkv_internal.h"
@@ -74,19 +75,19 @@ int32_t pkv_attend_noalloc(void* stream, const pkv_params* p, const float* q, co
     if (!stream_eligible(p, G))
         return fail(PKV_ERR_UNSUPPORTED, "pkv_attend_noalloc: head_dim 256 or 512 with "
                                          "num_heads / num_kv_heads <= 8");
-    // Slots the scratch holds for this call's rows: the plan, then (m, l) and o[D] in
-    // double per (slot, row), each region 256-byte aligned.
+    // Workgroups along the keys the scratch holds partials for: the largest cap whose
+    // layout (the plan, then (m, l) and o[D] in double per (slot, row), slots = cap +
+    // batch) fits. The layout grows by per_slot bytes (plus alignment) per slot.
     const size_t rows = (size_t)p->num_heads * q_len;
     const size_t per_slot = rows * (2 + (size_t)p->head_dim) * sizeof(double);
-    const size_t fixed = (((size_t)(batch + 2) * sizeof(int32_t) + 255) & ~(size_t)255) + 512;
-    const size_t slots = kScratchBytes > fixed ? (kScratchBytes - fixed) / per_slot : 0;
-    if (slots < (size_t)batch + 1)
+    const size_t base = stream_layout(p, batch, q_len, 0).total;  // batch slots, no cap
+    int32_t cap = base < kScratchBytes
+                      ? (int32_t)std::min<size_t>((kScratchBytes - base) / per_slot, kStreamMaxSlots)
+                      : 0;
+    while (cap > 0 && stream_layout(p, batch, q_len, cap).total > kScratchBytes) --cap;
+    if (cap < 1)
         return fail(PKV_ERR_WORKSPACE, "pkv_attend_noalloc: the call's split-K partials exceed "
                                        "the 64 MiB scratch (use pkv_attend with a workspace)");
-    const int32_t cap = (int32_t)(slots - batch < (size_t)kStreamMaxSlots ? slots - batch
-                                                                          : kStreamMaxSlots);
-    if (stream_layout(p, batch, q_len, cap).total > kScratchBytes)
-        return fail(PKV_ERR_WORKSPACE, "pkv_attend_noalloc: scratch layout");
     void* ws = nullptr;
     rc = scratch_address(&ws);
     if (rc != PKV_OK) return rc;
