@@ -281,8 +281,10 @@ class VerifySchedule:
     LAYERS = 2
 
     def __init__(self, seed: int = 0, batch: int | None = None, iters: int | None = None,
-                 ctx_lo: int = 512, ctx_hi: int = 4096):
+                 ctx_lo: int = 512, ctx_hi: int = 4096, bf16: bool = False):
         rng = np.random.default_rng(seed)
+        self.bf16 = bf16  # bf16 pools and appended rows (the bf16 variant); fp32 by default
+        self.elt = 2 if bf16 else 4
         if batch is not None:
             self.B = batch
         if iters is not None:
@@ -310,17 +312,18 @@ class VerifySchedule:
     def device_data(self, stream=None) -> dict:
         rows = self.num_blocks * self.BS
         n = self.ITERS * self.LAYERS
-        return {"pools": [[synth.normal((rows, self.kv_stride), self.seed_pool[l][kv],
-                                        stream=stream) for kv in range(2)]
+        kv = np.uint16 if self.bf16 else np.float32
+        return {"pools": [[synth.normal((rows, self.kv_stride), self.seed_pool[l][i], kv,
+                                        stream=stream) for i in range(2)]
                           for l in range(self.LAYERS)],
                 "q": synth.normal((n, self.B, self.DRAFT, self.HQ, self.D), self.seed_q,
                                   stream=stream),
                 "mtp_q": synth.normal((n, self.DRAFT, self.B, 1, self.HQ, self.D),
                                       self.seed_mtp_q, stream=stream),
                 "k_new": synth.normal((n, self.B * self.DRAFT, self.kv_stride), self.seed_knew,
-                                      stream=stream),
+                                      kv, stream=stream),
                 "v_new": synth.normal((n, self.B * self.DRAFT, self.kv_stride), self.seed_vnew,
-                                      stream=stream)}
+                                      kv, stream=stream)}
 
     def pos(self, it: int) -> np.ndarray:
         return self.length[it].astype(np.int32)
@@ -331,9 +334,10 @@ class VerifySchedule:
     def tok_off(self) -> np.ndarray:
         return (np.arange(self.B + 1) * self.DRAFT).astype(np.int32)
 
-    def verify_bytes(self, it: int, elt: int = 4) -> int:
+    def verify_bytes(self, it: int, elt: int | None = None) -> int:
         """Algorithmic bytes of one verify attention launch (one layer): each K/V row
         slice of prefix + draft once, Q in, O out, table entries."""
+        elt = self.elt if elt is None else elt
         n = self.length[it] + self.DRAFT
         kv = int(n.sum()) * 2 * self.kv_stride * elt
         qo = 2 * self.B * self.DRAFT * self.HQ * self.D * 4

@@ -269,6 +269,17 @@ def test_verify_inactive_and_bad_table_mfma(gpu):
     assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[0])) and np.all(np.isfinite(o[2]))
 
 
+@pytest.mark.parametrize("q_len", [1, 4], ids=["decode-vector", "verify-mfma"])
+def test_batch_4096_large_lds(gpu, q_len):
+    """The largest batch pkv_attend takes: the stream kernels keep 5 ints per sequence in
+    LDS, ~80 KiB at 4096, above the 64 KiB a kernel gets without opting in (the vector
+    kernel for decode; the fp64 MFMA kernel, 8 rows per kv head, for 4 queries)."""
+    print(f"[attend] batch 4096, q_len {q_len}", flush=True)
+    rng = np.random.default_rng(4096 + q_len)
+    ctx = rng.integers(1, 48, 4096)
+    _batched_case(rng, 4096, q_len, ctx, 2, 1, 256, 16, 0, F32, 0.0625)
+
+
 def test_gqa8_d512(gpu):
     rng = np.random.default_rng(12)
     ctx = rng.integers(1, 4000, 4)
