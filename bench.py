@@ -581,7 +581,7 @@ def bench_config4(args, log):
     return res
 
 
-VERIFY_BF16_KERNEL = "stream_attend_kernel<256, bf16, 4, 2> + stream_merge_kernel<256, float>"
+VERIFY_BF16_KERNEL = "stream_bf16_mfma_kernel<paged> (bf16 MFMA) + stream_merge_kernel<256, float>"
 
 
 def bench_config5(args, log):

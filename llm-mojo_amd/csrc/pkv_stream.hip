@@ -1508,6 +1508,313 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     }
 }
 
+// ---- bf16 MFMA path: bf16 pools, head_dim 256, 5..8 query rows per KV head -------------
+//
+// One wave per KV head, up to 8 query rows (a 4-token verify at G = 2), batches of 16
+// tokens staged in LDS, all products on v_mfma_f32_16x16x32_bf16 (QK^T) and
+// v_mfma_f32_16x16x16_bf16 (PV) with fp32 accumulation. Q is fp32, so it enters as
+// Q = Q_hi + Q_lo (both bf16, |q - Q_hi - Q_lo| <= 2^-16 |q|), and so does P (P_hi = p
+// truncated to bf16, P_lo = the remainder rounded to nearest, |p - P_hi - P_lo| <= 2^-16
+// p): a single bf16 rounding of either would break the 2e-2 output bound near zero. The
+// 8 rows use half of the MFMA's 16 columns; the other half carries the low parts, so one
+// instruction forms both: column j < 8 holds row j's hi part, column j + 8 its lo part.
+// Lane layouts (v_mfma_f32_16x16x32_bf16, checked on the device; the x16 form is its
+// K = 16 counterpart): A[i][k] lane i + 16 (k / 8) element k % 8 (x16: lane i + 16 (k / 4)
+// element k % 4); B[k][j] likewise with j for i; C[i][j] lane j + 16 (i / 4) register i % 4.
+//   S^T[token][col] = K Q^T: A = K (16 tokens x 32 dims per step), B = Q^T. Lane L then
+//     holds tokens 4 (L / 16) + r of column L % 16; the hi and lo halves are added by one
+//     DPP rotation (lane L ^ 8), after which lanes L and L ^ 8 hold S of row L % 8.
+//   O^T[d][col] += V^T P^T (16 dims x 16 tokens per d-tile): B = P^T is exactly what lane
+//     L holds (tokens 4 (L / 16) + r): P_hi in the columns below 8, P_lo above; A = V^T
+//     comes from one ds_read_b64_tr_b16 per d-tile (input lane a addresses dims
+//     4 (a % 4) .. + 3 of token 4 (L / 16) + a / 4; inside each 16-lane group output lane j
+//     element e is element j % 4 of what input lane 4e + j / 4 addressed). The hi and lo
+//     columns are added once, at the end.
+// LDS per wave: K and V of 16 tokens, rows of 512 bytes; K's 16-byte chunk c of token r
+// sits at c ^ r and V's 32-byte chunk c at c ^ r, so the operand reads land on distinct
+// banks. A copy instruction moves two tokens (1 KiB): the batches start on even positions
+// (a piece starting on an odd key also copies the key before it, masked), so a pair lies
+// in one block and its address is one scalar base plus a per-lane offset. The row after a
+// sequence's last key may be copied (never used): its V row is zeroed in LDS, so a
+// non-finite value there cannot reach PV through a zero weight.
+constexpr int kBfTok = 16;                       // tokens per batch
+constexpr int kBfRow = 512;                      // bytes per token row slice (256 bf16)
+constexpr size_t kBfStage = 2 * kBfTok * kBfRow; // K and V of a batch, per wave
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+template <int OFF>
+__device__ inline i32x2 lds_tr16(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    i32x2 v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+__device__ inline uint16_t bf16_rne_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ inline float bf16_bits_to_float(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+template <int ADDR>
+__global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(StreamArgs a) {
+    constexpr int D = 256;
+    static_assert(ADDR == kAddrPaged, "paged pools");
+    constexpr float kLog2e = 1.4426950408889634f;
+    constexpr float kLn2 = 0.6931471805599453f;
+    extern __shared__ int smem[];
+    int* s_pre = smem;               // [batch + 1]
+    int* s_lo = smem + a.batch + 1;  // [batch]
+    int* s_meta = smem + 2 * a.batch + 1;  // [3 batch + 1] (stream_setup)
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kSW - 1);
+    const int wave = ufirst(tid / kSW);
+    const int w = blockIdx.y;
+    const int B = a.batch;
+    const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, nullptr);  // no fused append
+    const int total = ufirst(s_pre[B]);
+    const int k0 = sp.start(w);
+    if (k0 >= total) return;
+    const int k1 = min(total, sp.start(w + 1));
+    const int g = blockIdx.x * kMaxWaves + wave;  // this wave's KV head
+    if (g >= a.Hkv) return;
+
+    const int rows = a.G * a.q_cnt;
+    const uint32_t row_bytes = (uint32_t)a.Hkv * D * 2;
+    const char* kbase = a.k_pool + (size_t)g * D * 2;
+    const char* vbase = a.v_pool + (size_t)g * D * 2;
+    const int grp = lane >> 4, l16 = lane & 15;
+    const int rr = l16 & 7;           // the row of this lane's column
+    const bool hi_col = l16 < 8;      // column holds the row's hi part (else its lo part)
+    const int bs_mask = (1 << a.bs_shift) - 1;
+    const float sl2 = a.scale * kLog2e;
+    char* sK = reinterpret_cast<char*>(smem) + mfma_stage_offset(B, false) + (size_t)wave * kBfStage;
+    char* sV = sK + kBfTok * kBfRow;
+
+    // Copy offsets: instruction j moves tokens 2j, 2j + 1 of the batch (lanes 0-31, 32-63);
+    // lane p of a row loads the global chunk that belongs at its LDS position.
+    uint32_t k_off[8], v_off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int r = 2 * j + (lane >> 5), p16 = lane & 31;
+        const uint32_t hb = (uint32_t)(lane >> 5) * row_bytes;
+        k_off[j] = hb + 16u * (uint32_t)(p16 ^ r);
+        v_off[j] = hb + 16u * (uint32_t)((((p16 >> 1) ^ r) << 1) | (p16 & 1));
+    }
+    // LDS operand addresses. K, 32-dim step c: token l16, 16-byte chunk (4c + grp) ^ l16 =
+    // byte 512 l16 + 16 (grp ^ (l16 & 3)) + 64 ((c & 3) ^ (l16 >> 2)) + 256 (c >> 2).
+    const uint32_t k_lane = lds_addr(sK) + 512u * l16 + 16u * (grp ^ (l16 & 3));
+    uint32_t k_addr[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) k_addr[q] = k_lane + 64u * (q ^ (l16 >> 2));
+    // V, d-tile u: token z = 4 grp + l16 / 4, byte 512 z + 32 (u ^ z) + 8 (l16 & 3).
+    const int z = 4 * grp + (l16 >> 2);
+    const uint32_t v_lane = lds_addr(sV) + 512u * z + 8u * (l16 & 3);
+
+    int s = 0;
+    {
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (ufirst(s_pre[mid]) <= k0) lo = mid;
+            else hi = mid - 1;
+        }
+        s = lo;
+    }
+    for (; s < B; ++s) {
+        const int ps = ufirst(s_pre[s]);
+        const int pe = ufirst(s_pre[s + 1]);
+        if (ps >= k1) break;
+        if (pe == ps) continue;
+        const int lo_key = ufirst(s_lo[s]);
+        const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
+        const int tb = lo_key + min(k1, pe) - ps;  // one past the last
+        const bool single = sp.owner(ps) == sp.owner(pe - 1);
+        const int pos0 = ufirst(s_meta[s]);
+        const int rows_s = a.G * ufirst(s_meta[B + s]);
+        const int32_t* trow = a.tables + (size_t)s * a.table_stride;
+        const int t0 = ta & ~1;  // batches start on even positions
+        const int last_page = (tb - 1) >> a.bs_shift;
+
+        // first 64 page ids and the query rows, requested together
+        int first_raw = trow[min((t0 >> a.bs_shift) + lane, last_page)];
+        asm volatile("" ::: "memory");
+        // Q^T as the B operand of step c: column l16 = row rr, dims 32c + 8 grp + e; its hi
+        // (column < 8) or lo part, zero for rows past `rows`.
+        bf16x8 qreg[8];
+        {
+            const float* qp = a.q + out_row(a, s, g, min(rr, rows - 1)) * D + 8 * grp;
+            const bool qlive = rr < rows;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * c);
+                const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * c + 4);
+                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = qlive ? xv[e] : 0.f;
+                    const uint16_t h = bf16_rne_bits(x);
+                    const uint16_t b16 = hi_col ? h : bf16_rne_bits(x - bf16_bits_to_float(h));
+                    qreg[c][e] = __builtin_bit_cast(__bf16, b16);
+                }
+            }
+        }
+        const int pq = pos0 + a.j0 + rr / a.G;  // query position of this lane's row
+        const int wsr = window_start(pq, a.window);
+        const bool row_live = rr < rows_s;
+        int pgbase = t0 >> a.bs_shift;
+        bool bad = false;
+        int vpg;
+        {
+            const bool lane_ok = pgbase + lane <= last_page;
+            const bool id_ok = first_raw >= 0 && first_raw < a.num_blocks;
+            bad = bad || (lane_ok && !id_ok);
+            vpg = lane_ok && id_ok ? first_raw : 0;
+        }
+        float m = -INFINITY;  // reference max of this lane's row (log2 units)
+        float l = 0.f;        // this lane's share of the row sum (its 4 of every 16 tokens)
+        f32x4 o[16];          // O^T: d-tile u holds dims 16u + 4 grp + r of column l16
+#pragma unroll
+        for (int u = 0; u < 16; ++u) o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        auto issue = [&](int t) {
+            const int tl = min(t + kBfTok - 1, tb - 1);
+            if ((tl >> a.bs_shift) - pgbase >= kSW) {  // next 64 page ids
+                pgbase = t >> a.bs_shift;
+                int pg = 0;
+                if (pgbase + lane <= last_page) {
+                    pg = trow[pgbase + lane];
+                    if (pg < 0 || pg >= a.num_blocks) {
+                        bad = true;
+                        pg = 0;
+                    }
+                }
+                vpg = pg;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                // pairs past the piece re-read its last pair (masked)
+                const int tt = min(t + 2 * j, (tb - 1) & ~1);
+                const int pg = __builtin_amdgcn_readlane(vpg, (tt >> a.bs_shift) - pgbase);
+                const size_t off = (((size_t)pg << a.bs_shift) | (size_t)(tt & bs_mask)) * row_bytes;
+                __builtin_amdgcn_global_load_lds(uniform_ptr(kbase + off) + k_off[j],
+                                                 (lds_void*)(sK + 2 * j * kBfRow), 16, 0, kCpolNT);
+                __builtin_amdgcn_global_load_lds(uniform_ptr(vbase + off) + v_off[j],
+                                                 (lds_void*)(sV + 2 * j * kBfRow), 16, 0, kCpolNT);
+            }
+        };
+
+        issue(t0);
+        for (int t = t0; t < tb; t += kBfTok) {
+            __builtin_amdgcn_s_waitcnt(0);  // this batch is in LDS
+            if (t + kBfTok > tb - 1 && (tb & 1)) {
+                // the batch holds the row after the sequence's last key: zero its V rows
+                const int r_bad = tb - t;  // first LDS row past the piece
+                for (int r = r_bad; r < kBfTok; r += 2) {  // r_bad is odd: its pair's second row
+                    if (lane >= 32) *reinterpret_cast<uint4*>(sV + r * kBfRow + 16 * (lane - 32)) = make_uint4(0, 0, 0, 0);
+                }
+                __builtin_amdgcn_s_waitcnt(kLgkm0);
+            }
+            i32x4 kr[8];
+            i32x2 vr[16];
+            static_for<0, 8>([&](auto C) {
+                constexpr int c = decltype(C)::value;
+                kr[c] = lds_b128<256 * (c >> 2)>(k_addr[c & 3]);
+            });
+            static_for<0, 16>([&](auto U) {
+                constexpr int u = decltype(U)::value;
+                vr[u] = lds_tr16<0>(v_lane + ((uint32_t)(u ^ z) << 5));
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kr[0]), "+v"(kr[1]), "+v"(kr[2]), "+v"(kr[3]));
+#pragma unroll
+            for (int i = 4; i < 8; ++i) asm volatile("" : "+v"(kr[i]));
+#pragma unroll
+            for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(vr[i]));
+            if (t + kBfTok < tb) issue(t + kBfTok);
+
+            // S^T over the 8 steps of 32 dims, then hi + lo
+            f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[c]), qreg[c], st, 0, 0, 0);
+            float sv[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float full = st[r] + dpp<kRor8>(st[r]);
+                const int tok = t + 4 * grp + r;
+                const bool ok = row_live && tok >= ta && tok < tb && tok <= pq && tok >= wsr;
+                sv[r] = ok ? full * sl2 : -INFINITY;
+                mx = fmaxf(mx, sv[r]);
+            }
+            mx = allreduce_hi<16>(mx, OpMax());
+            // lazy reference max (log2 units): p = exp2(s - m) <= 256
+            const bool move = mx > m + 8.f;
+            const float m_new = move ? mx : m;
+            const float alpha = move ? exp2f(m - m_new) : 1.f;  // m = -inf gives 0
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            float p[4];
+            s16x4 pb;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p[r] = exp2f(sv[r] - m_use);  // masked: exp2(-inf) = 0
+                const uint32_t u = __float_as_uint(p[r]);
+                const uint16_t h = (uint16_t)(u >> 16);  // P_hi: p truncated to bf16
+                pb[r] = (short)(hi_col ? h : bf16_rne_bits(p[r] - __uint_as_float(u & 0xffff0000u)));
+            }
+            l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+            m = m_new;
+            if (__any(move)) {
+#pragma unroll
+                for (int u = 0; u < 16; ++u) o[u] *= alpha;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                o[u] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vr[u]), pb, o[u], 0, 0, 0);
+        }
+        bad = __any(bad);
+
+        // O^T hi + lo columns; the row sum over the four lane groups
+        l = allreduce_hi<16>(l, OpSum());
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[u][r] += dpp<kRor8>(o[u][r]);
+        if (single) {
+            if (hi_col && rr < rows_s) {
+                const float inv = 1.f / (l + 1e-10f);
+                float* op = a.out + out_row(a, s, g, rr) * D + 4 * grp;
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    float4 v;
+                    v.x = bad ? __builtin_nanf("") : o[u][0] * inv;
+                    v.y = bad ? __builtin_nanf("") : o[u][1] * inv;
+                    v.z = bad ? __builtin_nanf("") : o[u][2] * inv;
+                    v.w = bad ? __builtin_nanf("") : o[u][3] * inv;
+                    *reinterpret_cast<float4*>(op + 16 * u) = v;
+                }
+            }
+        } else {
+            const size_t slot = (size_t)(w + s) * a.rows_seq;
+            float* po = static_cast<float*>(a.part_o);
+            float* pml = static_cast<float*>(a.part_ml);
+            if (hi_col && rr < rows) {
+                const int row = (rr / a.G) * a.Hq + g * a.G + rr % a.G;
+                float* dst = po + (slot + row) * D + 4 * grp;
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    *reinterpret_cast<float4*>(dst + 16 * u) = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
+                if (grp == 0) {  // the merge takes natural-log units
+                    pml[(slot + row) * 2 + 0] = bad ? __builtin_nanf("") : m * kLn2;
+                    pml[(slot + row) * 2 + 1] = l;
+                }
+            }
+        }
+    }
+}
+
 // Combines the pieces of every sequence that spans more than one workgroup:
 //   out = sum_c o_c e^(m_c - M) / (sum_c l_c e^(m_c - M) + 1e-10),  M = max_c m_c,
 // the reference's softmax(x)_i = e^(x_i - max) / (sum + 1e-10). One workgroup per
@@ -1770,6 +2077,33 @@ int32_t launch_mfma(StreamArgs a, hipStream_t st) {
                            : launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrPaged>(a, st);
 }
 
+// bf16 pools, head_dim 256, 5..8 rows per kv head: the bf16 matrix cores (paged pools,
+// block_size >= 2: a copy pair lies in one block); else two vector waves of 4 rows.
+int32_t launch_bf16_mfma(StreamArgs a, hipStream_t st) {
+    const int waves = a.Hkv < kMaxWaves ? a.Hkv : kMaxWaves;
+    const int threads = waves * kSW;
+    const size_t lds = mfma_stage_offset(a.batch, false) + (size_t)waves * kBfStage;
+    if (lds > kMfmaLdsMax || a.keys || a.ring_size > 0 || a.bs_shift < 1 || a.nr.k_new)
+        return launch_r<256, uint16_t, 4, 2>(a, st);
+    const void* fn = reinterpret_cast<const void*>(&stream_bf16_mfma_kernel<kAddrPaged>);
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLdsMax) !=
+        hipSuccess)
+        return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
+    const int slots = fill_workgroups(fn, threads, lds);
+    if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
+    const int groups = (a.Hkv + kMaxWaves - 1) / kMaxWaves;
+    a.nwg = slots / groups > 0 ? slots / groups : 1;
+    if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
+    if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
+    hipLaunchKernelGGL((stream_bf16_mfma_kernel<kAddrPaged>), dim3(groups, a.nwg), dim3(threads), lds,
+                       st, a);
+    if (hipGetLastError() != hipSuccess)
+        return fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
+    hipLaunchKernelGGL((stream_merge_kernel<256, float>), dim3(a.rows_seq, a.batch), dim3(kMergeNT), 0,
+                       st, a);
+    return PKV_OK;
+}
+
 template <int D, typename KV, int R, int WPH>
 int32_t launch_r(StreamArgs a, hipStream_t st) {
     if (a.keys) return launch_addr<D, KV, R, WPH, kAddrSparse>(a, st);
@@ -1785,11 +2119,11 @@ int32_t launch_rows(StreamArgs a, int D, int rows, hipStream_t st) {
     if (D == 256) {
         if (rows <= 1) return launch_r<256, KV, 1>(a, st);
         if (rows <= 2) return launch_r<256, KV, 2>(a, st);
-        if constexpr (sizeof(KV) == 4) {  // fp32 pools: the fp64 matrix cores
-            if (rows > 4) return launch_mfma<256>(a, st);
+        if (rows > 4) {  // fp32 pools: the fp64 matrix cores; bf16 pools: the bf16 ones
+            if constexpr (sizeof(KV) == 4) return launch_mfma<256>(a, st);
+            else return launch_bf16_mfma(a, st);
         }
-        if (rows <= 4) return launch_r<256, KV, 4>(a, st);
-        return launch_r<256, KV, 4, 2>(a, st);
+        return launch_r<256, KV, 4>(a, st);
     }
     if (rows <= 1) return launch_r<512, KV, 1>(a, st);
     if (rows <= 2) return launch_r<512, KV, 2>(a, st);

@@ -269,6 +269,27 @@ def test_verify_inactive_and_bad_table_mfma(gpu):
     assert np.all(np.isnan(o[1])) and np.all(np.isfinite(o[0])) and np.all(np.isfinite(o[2]))
 
 
+@pytest.mark.parametrize("hq,hkv,q_len,bs,window", [
+    (16, 8, 4, 16, 0),     # config 5's shape with bf16 pools: 8 rows per kv head
+    (16, 8, 4, 16, 1024),  # the sliding layers' window
+    (16, 8, 3, 16, 0),     # 6 rows: two columns of each half unused
+    (16, 16, 8, 16, 0),    # G = 1, 8 queries; 16 kv heads: two workgroup head groups
+    (16, 4, 2, 16, 0),     # G = 4
+    (16, 2, 1, 16, 0),     # G = 8 decode at head_dim 256
+    (16, 8, 4, 2, 0),      # smallest block size the kernel takes (a copy pair in one block)
+    (16, 8, 4, 64, 33),    # large blocks, an odd window
+], ids=["cfg5", "window", "rows6", "g1-q8", "g4", "g8", "bs2", "bs64-w33"])
+def test_verify_bf16_mfma(gpu, hq, hkv, q_len, bs, window):
+    """bf16 pools with 5..8 query rows per kv head (stream_bf16_mfma_kernel: QK^T and PV on
+    the bf16 matrix cores with Q and P split into hi + lo bf16 parts): mixed contexts from a
+    single key to multi-piece sequences, odd and even first and last keys (the kernel's copy
+    pairs start on even positions), against the oracle on the same bf16 values (2e-2)."""
+    print(f"[attend] bf16 mfma {hq}q/{hkv}kv q_len {q_len} bs {bs} window {window}", flush=True)
+    rng = np.random.default_rng(hq * 100 + hkv * 10 + q_len + bs + window)
+    ctx = np.concatenate([[0, 1, 2, 3, 16, 17, 31], rng.integers(40, 5000, 9)])
+    _batched_case(rng, ctx.size, q_len, ctx, hq, hkv, 256, bs, window, BF16, 0.0625)
+
+
 @pytest.mark.parametrize("q_len", [1, 4], ids=["decode-vector", "verify-mfma"])
 def test_batch_4096_large_lds(gpu, q_len):
     """The largest batch pkv_attend takes: the stream kernels keep 5 ints per sequence in
