@@ -1074,8 +1074,8 @@ def bench_wo(args, log):
 
 def kernel_name(sched):
     """The attention kernels a decode schedule's launches run (stream kernel + merge)."""
-    if sched.D == 512:
-        return "stream_attend_kernel<512, float, 2, 4> + stream_merge_kernel<512, double>"
+    if sched.D == 512:  # 8 rows per kv head on the fp64 matrix cores
+        return "stream_mfma_kernel<512, 1, 1, 2, paged> (fp64 MFMA) + stream_merge_kernel<512, double>"
     return "stream_attend_kernel<256, float, 2> + stream_merge_kernel<256, double>"
 
 

@@ -69,7 +69,9 @@ namespace {
 
 constexpr int kSW = 64;                          // wavefront
 constexpr int kMaxWaves = PKV_STREAM_WAVES;      // KV heads handled by one workgroup
-constexpr int kMergeNT = 256;                    // merge kernel threads
+// merge kernel threads: one per element of a row (head_dim 256 or 512)
+template <int D>
+constexpr int merge_threads() { return D; }
 constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
 #ifndef PKV_STREAM_EVEN_W
 #define PKV_STREAM_EVEN_W 530
@@ -1861,7 +1863,8 @@ __device__ inline void write_alloc_state(const StreamArgs& a) {
 // grid (rows_seq, batch), plus one row of workgroups (blockIdx.y == batch) with a fused
 // append, whose first workgroup writes the state.
 template <int D, typename Acc>
-__global__ __launch_bounds__(kMergeNT) void stream_merge_kernel(StreamArgs a) {
+__global__ __launch_bounds__(merge_threads<D>()) void stream_merge_kernel(StreamArgs a) {
+    constexpr int kMergeNT = merge_threads<D>();
     constexpr int kMaxPieces = 1024;
     constexpr int kMergeRegs = 16;          // pieces whose o rows are held in registers
     constexpr int DPT = D / kMergeNT;       // elements per thread
@@ -2013,7 +2016,7 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     if (hipGetLastError() != hipSuccess)
         return fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
     hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch + (fused ? 1 : 0)),
-                       dim3(kMergeNT), 0, st, a);
+                       dim3(merge_threads<D>()), 0, st, a);
     return PKV_OK;
 }
 
@@ -2058,7 +2061,7 @@ int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
     if (hipGetLastError() != hipSuccess)
         return fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
     hipLaunchKernelGGL((stream_merge_kernel<D, double>), dim3(a.rows_seq, a.batch + (fused ? 1 : 0)),
-                       dim3(kMergeNT), 0, st, a);
+                       dim3(merge_threads<D>()), 0, st, a);
     return PKV_OK;
 }
 
@@ -2099,7 +2102,7 @@ int32_t launch_bf16_mfma(StreamArgs a, hipStream_t st) {
                        st, a);
     if (hipGetLastError() != hipSuccess)
         return fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
-    hipLaunchKernelGGL((stream_merge_kernel<256, float>), dim3(a.rows_seq, a.batch), dim3(kMergeNT), 0,
+    hipLaunchKernelGGL((stream_merge_kernel<256, float>), dim3(a.rows_seq, a.batch), dim3(merge_threads<256>()), 0,
                        st, a);
     return PKV_OK;
 }
