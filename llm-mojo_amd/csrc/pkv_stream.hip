@@ -1109,14 +1109,14 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     // Staging. WPH 1: one buffer per wave, loaded and read by that wave (two buffers, with
     // the reads untracked, measured no faster: 129.5-130.9 against 128.0-128.4 us for the
     // config 5 verify launch). WPH > 1: two buffers per head (batches i and i + 1 in flight
-    // together), each wave of the head copying its share of every row slice (CPW of the
-    // slice's 1 KiB chunks).
-    constexpr int CPW = (D / 256) / WPH;
-    static_assert(WPH == 1 || CPW * WPH == D / 256, "chunks per wave");
+    // together), each wave of the head copying its share of the batch's 1 KiB row chunks.
+    constexpr int CPT = D / 256;  // 1 KiB chunks per row slice
+    // copy i = j * CPT + c (token j, chunk c) of a batch is made by wave i % WPH of the head
+    static_assert((4 * TG * CPT) % WPH == 0, "copies split evenly over a head's waves");
     char* stage = reinterpret_cast<char*>(smem) + mfma_stage_offset(B, fused) +
                   (WPH == 1 ? (size_t)wave * mfma_stage_bytes(D, TG)
                             : (size_t)(wave / WPH) * 2 * mfma_stage_bytes(D, TG));
-    const int c0 = WPH == 1 ? 0 : (wave % WPH) * CPW;  // first chunk this wave copies
+    const int hw = WPH == 1 ? 0 : wave % WPH;  // this wave's share of the copies
     // Waves w and w + 4 of an 8-wave workgroup share a SIMD, whose issue slots bound the
     // batch loop; the arbiter favours the older wave, which left the other one alone for
     // the last ~15% of a piece. Alternating their priorities every batch keeps the two in
@@ -1277,10 +1277,13 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                 }
                 vpg = pg;
             }
-            // One token's slice (64 lanes x 16 bytes per load, contiguous); the address is
-            // wave-uniform: page id by readlane, offsets in scalar registers.
+            // Copy k of this wave: 1 KiB chunk c of token j's row slice (64 lanes x 16 bytes,
+            // contiguous), i = j * CPT + c = k * WPH + hw. The address is wave-uniform: page id by
+            // readlane, offsets in scalar registers.
 #pragma unroll
-            for (int j = 0; j < U; ++j) {
+            for (int k = 0; k < U * CPT / WPH; ++k) {
+                const int i = k * WPH + hw;
+                const int j = i / CPT, c = i % CPT;
                 const int tt = min(t + j, tb - 1);  // tokens past the piece re-read its last row
                 size_t off;
                 const char* kb = kbase;
@@ -1298,16 +1301,12 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                         vb = a.nr.v_new + (size_t)g * D * 4;
                     }
                 }
-#pragma unroll
-                for (int cc = 0; cc < (WPH == 1 ? D / 256 : CPW); ++cc) {
-                    const int c = c0 + cc;
-                    __builtin_amdgcn_global_load_lds(uniform_ptr(kb + off + 1024 * c) + 16 * lane,
-                                                     (lds_void*)(buf + (2 * j) * kSlot + 1024 * c),
-                                                     16, 0, kCpol);
-                    __builtin_amdgcn_global_load_lds(uniform_ptr(vb + off + 1024 * c) + 16 * lane,
-                                                     (lds_void*)(buf + (2 * j + 1) * kSlot + 1024 * c),
-                                                     16, 0, kCpol);
-                }
+                __builtin_amdgcn_global_load_lds(uniform_ptr(kb + off + 1024 * c) + 16 * lane,
+                                                 (lds_void*)(buf + (2 * j) * kSlot + 1024 * c), 16, 0,
+                                                 kCpol);
+                __builtin_amdgcn_global_load_lds(uniform_ptr(vb + off + 1024 * c) + 16 * lane,
+                                                 (lds_void*)(buf + (2 * j + 1) * kSlot + 1024 * c), 16,
+                                                 0, kCpol);
             }
         };
 
@@ -1336,7 +1335,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                 // This wave's copies of batch it have landed (those of batch it + 1, if issued,
                 // stay in flight); the barrier then covers the other waves' copies. It carries no
                 // fence, which would wait for the copies in flight.
-                constexpr int kCopies = U * 2 * CPW;  // copies per batch and wave
+                constexpr int kCopies = U * 2 * CPT / WPH;  // copies per batch and wave
                 if (t + U < tb) wait_vm<kCopies>();
                 else wait_vm<0>();
                 __builtin_amdgcn_s_barrier();
@@ -2068,11 +2067,13 @@ int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
 #ifndef PKV_MFMA_TG
 #define PKV_MFMA_TG 1
 #endif
-// head_dim 256: one wave of up to 8 rows per kv head; 512: two waves of 4.
+// head_dim 256: one wave of 8 rows per kv head. (Two waves of 4 rows sharing the staging,
+// two 8-wave workgroups per CU at 128 registers, spilled 24 registers and ran the config 5
+// verify launch at 176 against 126 us.) head_dim 512: two waves of 4 rows.
 template <int D>
 int32_t launch_mfma(StreamArgs a, hipStream_t st) {
-    constexpr int RG = D == 256 ? 2 : 1;
     constexpr int WPH = D == 256 ? 1 : 2;
+    constexpr int RG = 2 / WPH;  // 8 rows per head over WPH waves
     if constexpr (D == 256) {
         if (a.keys) return launch_mfma_addr<D, RG, PKV_MFMA_TG, WPH, kAddrSparse>(a, st);
     }
