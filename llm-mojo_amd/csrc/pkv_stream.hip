@@ -1736,6 +1736,10 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
             if (t + kBfTok < tb) issue(t + kBfTok);
 
             // S^T over the 8 steps of 32 dims, then hi + lo
+            // The two waves of a SIMD (w, w + 4) take turns at the higher priority, batch by
+            // batch, so one runs ahead on the matrix cores while the other computes its softmax.
+            if ((((t - t0) / kBfTok) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
             f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 8; ++c)
