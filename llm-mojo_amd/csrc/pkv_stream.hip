@@ -1133,6 +1133,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         }
         s = lo;
     }
+    int pre_s = -1, pre_raw = 0;  // the next piece's first page ids (pre_s: its sequence)
     for (; s < B; ++s) {
         const int ps = ufirst(s_pre[s]);
         const int pe = ufirst(s_pre[s + 1]);
@@ -1181,7 +1182,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
             const int pg = min((ta >> a.bs_shift) + lane, last_page);
             const int32_t* src = trow + pg;
             if constexpr (FUSED) src = (pg >= g_lo && pg < g_hi) ? a.nr.free_list + (g_top - pg) : src;
-            first_raw = *src;
+            first_raw = (!FUSED && pre_s == s) ? pre_raw : *src;
         }
         asm volatile("" ::: "memory");  // issued before the query rows
         // this lane's rows rb + 4rg + x: Q slice (B operand), query position, first key
@@ -1197,6 +1198,16 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
             const float* qp = a.q + out_row(a, s, g, min(r, rows - 1)) * D + 16 * b + 4 * y;
 #pragma unroll
             for (int q = 0; q < NQ; ++q) qf[rg][q] = *reinterpret_cast<const float4*>(qp + 64 * q);
+        }
+        // The next sequence's first 64 page ids, for its piece after this one (a piece starts
+        // at its sequence's first key).
+        if (PAGED && !FUSED && s + 1 < B && ufirst(s_pre[s + 1]) < k1 &&
+            ufirst(s_pre[s + 2]) > ufirst(s_pre[s + 1])) {
+            const int lo_n = ufirst(s_lo[s + 1]);
+            const int tb_n = lo_n + min(k1, ufirst(s_pre[s + 2])) - ufirst(s_pre[s + 1]);
+            pre_raw = a.tables[(size_t)(s + 1) * a.table_stride +
+                               min((lo_n >> a.bs_shift) + lane, (tb_n - 1) >> a.bs_shift)];
+            pre_s = s + 1;
         }
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg)
@@ -1624,6 +1635,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         }
         s = lo;
     }
+    int pre_s = -1, pre_raw = 0;  // the next piece's first page ids (pre_s: its sequence)
     for (; s < B; ++s) {
         const int ps = ufirst(s_pre[s]);
         const int pe = ufirst(s_pre[s + 1]);
@@ -1639,28 +1651,31 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         const int t0 = ta & ~1;  // batches start on even positions
         const int last_page = (tb - 1) >> a.bs_shift;
 
-        // first 64 page ids and the query rows, requested together
-        int first_raw = trow[min((t0 >> a.bs_shift) + lane, last_page)];
+        // The first 64 page ids (requested while the previous piece ran, if there was one)
+        // and the query rows, requested together; the first batch's copies go out before
+        // the query rows are split, which waits for them.
+        const int first_raw =
+            pre_s == s ? pre_raw : trow[min((t0 >> a.bs_shift) + lane, last_page)];
         asm volatile("" ::: "memory");
-        // Q^T as the B operand of step c: column l16 = row rr, dims 32c + 8 grp + e; its hi
-        // (column < 8) or lo part, zero for rows past `rows`.
-        bf16x8 qreg[8];
+        float4 qraw[8][2];
         {
             const float* qp = a.q + out_row(a, s, g, min(rr, rows - 1)) * D + 8 * grp;
-            const bool qlive = rr < rows;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * c);
-                const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * c + 4);
-                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float x = qlive ? xv[e] : 0.f;
-                    const uint16_t h = bf16_rne_bits(x);
-                    const uint16_t b16 = hi_col ? h : bf16_rne_bits(x - bf16_bits_to_float(h));
-                    qreg[c][e] = __builtin_bit_cast(__bf16, b16);
-                }
+                qraw[c][0] = *reinterpret_cast<const float4*>(qp + 32 * c);
+                qraw[c][1] = *reinterpret_cast<const float4*>(qp + 32 * c + 4);
             }
+        }
+        asm volatile("" ::: "memory");
+        // The next sequence's first 64 page ids, for its piece after this one (a piece
+        // starts at its sequence's first key).
+        if (s + 1 < B && ufirst(s_pre[s + 1]) < k1 && ufirst(s_pre[s + 2]) > ufirst(s_pre[s + 1])) {
+            const int lo_n = ufirst(s_lo[s + 1]);
+            const int t0_n = lo_n & ~1;
+            const int tb_n = lo_n + min(k1, ufirst(s_pre[s + 2])) - ufirst(s_pre[s + 1]);
+            pre_raw = a.tables[(size_t)(s + 1) * a.table_stride +
+                               min((t0_n >> a.bs_shift) + lane, (tb_n - 1) >> a.bs_shift)];
+            pre_s = s + 1;
         }
         const int pq = pos0 + a.j0 + rr / a.G;  // query position of this lane's row
         const int wsr = window_start(pq, a.window);
@@ -1708,6 +1723,24 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         };
 
         issue(t0);
+        // Q^T as the B operand of step c: column l16 = row rr, dims 32c + 8 grp + e; its hi
+        // (column < 8) or lo part, zero for rows past `rows`.
+        bf16x8 qreg[8];
+        {
+            const bool qlive = rr < rows;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const float xv[8] = {qraw[c][0].x, qraw[c][0].y, qraw[c][0].z, qraw[c][0].w,
+                                     qraw[c][1].x, qraw[c][1].y, qraw[c][1].z, qraw[c][1].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = qlive ? xv[e] : 0.f;
+                    const uint16_t h = bf16_rne_bits(x);
+                    const uint16_t b16 = hi_col ? h : bf16_rne_bits(x - bf16_bits_to_float(h));
+                    qreg[c][e] = __builtin_bit_cast(__bf16, b16);
+                }
+            }
+        }
         for (int t = t0; t < tb; t += kBfTok) {
             __builtin_amdgcn_s_waitcnt(0);  // this batch is in LDS
             if (t + kBfTok > tb - 1 && (tb & 1)) {
