@@ -35,12 +35,27 @@ namespace {
 struct Occ {
     std::mutex mu;
     std::map<std::tuple<const void*, int, int, size_t>, int> blocks;  // -> workgroups
+    std::map<std::pair<const void*, int>, int> lds_limit;           // (kernel, device) -> bytes set
 };
 Occ& occ() {
     static Occ o;
     return o;
 }
 }  // namespace
+
+bool reserve_lds(const void* fn, int bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    Occ& o = occ();
+    std::lock_guard<std::mutex> lk(o.mu);
+    const auto key = std::make_pair(fn, dev);
+    const auto it = o.lds_limit.find(key);
+    if (it != o.lds_limit.end() && it->second >= bytes) return true;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+        return false;
+    o.lds_limit[key] = bytes;
+    return true;
+}
 
 int device_fill_workgroups(const void* fn, int threads, size_t lds, int cap) {
     int dev = 0;

@@ -37,6 +37,9 @@ int32_t check_launch(const char* what);
 // resident on the current device at once (CUs x occupancy), at most `cap`; -1 if the
 // runtime query fails. Cached per (kernel, device, shape).
 int device_fill_workgroups(const void* fn, int threads, size_t lds, int cap);
+// Lets kernel fn use up to `bytes` of dynamic LDS on the current device (above 64 KiB a
+// kernel must opt in). The attribute is set once per kernel and device; false on failure.
+bool reserve_lds(const void* fn, int bytes);
 
 // Validates the geometry shared by every entry point. Returns PKV_OK or an error code
 // (message set).

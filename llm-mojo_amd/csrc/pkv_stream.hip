@@ -2034,8 +2034,7 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
         return fail(PKV_ERR_UNSUPPORTED, "pkv_attend: batch too large for the kernel's LDS");
     // Above 64 KiB of dynamic LDS a kernel must opt in (once per kernel and device).
     if (lds > 64 * 1024 &&
-        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStreamLdsMax) !=
-            hipSuccess)
+        !reserve_lds(fn, (int)kStreamLdsMax))
         return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
@@ -2080,8 +2079,7 @@ int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
     const void* fn = fused ? reinterpret_cast<const void*>(&stream_mfma_kernel<D, RG, TG, WPH, ADDR, kFusable>)
                            : reinterpret_cast<const void*>(&stream_mfma_kernel<D, RG, TG, WPH, ADDR, false>);
     // Above 64 KiB of dynamic LDS a kernel must opt in (once per kernel and device).
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLdsMax) !=
-        hipSuccess)
+    if (!reserve_lds(fn, (int)kMfmaLdsMax))
         return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
@@ -2127,8 +2125,7 @@ int32_t launch_bf16_mfma(StreamArgs a, hipStream_t st) {
     if (lds > kMfmaLdsMax || a.keys || a.ring_size > 0 || a.bs_shift < 1 || a.nr.k_new)
         return launch_r<256, uint16_t, 4, 2>(a, st);
     const void* fn = reinterpret_cast<const void*>(&stream_bf16_mfma_kernel<kAddrPaged>);
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMfmaLdsMax) !=
-        hipSuccess)
+    if (!reserve_lds(fn, (int)kMfmaLdsMax))
         return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
     const int slots = fill_workgroups(fn, threads, lds);
     if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
