@@ -1902,7 +1902,11 @@ template <int D, typename Acc>
 __global__ __launch_bounds__(merge_threads<D>()) void stream_merge_kernel(StreamArgs a) {
     constexpr int kMergeNT = merge_threads<D>();
     constexpr int kMaxPieces = 1024;
-    constexpr int kMergeRegs = 16;          // pieces whose o rows are held in registers
+    // Pieces whose o rows are held in registers, requested with the (m, l) loads. At head_dim
+    // 256 a 16-sequence verify or MTP read splits each sequence into ~17 pieces, so 32 keep
+    // them in one round trip (config 5's step: 1.134 -> 1.121 ms); at head_dim 512 (the LSA
+    // shape's ~9 pieces) 32 measured slower than 16.
+    constexpr int kMergeRegs = D == 256 ? 32 : 16;
     constexpr int DPT = D / kMergeNT;       // elements per thread
     static_assert(DPT * kMergeNT == D, "head_dim a multiple of the merge width");
     __shared__ Acc s_w[kMaxPieces];
