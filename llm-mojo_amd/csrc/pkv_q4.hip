@@ -275,11 +275,11 @@ __device__ inline f32x4 load16_system(const float* p) {
     asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
     return v;
 }
-constexpr int kQ4RedLoads = 8;  // partials requested at once per thread
+constexpr int kQ4RedLoads = 12;  // partials requested at once per thread (the 11 splits of the engine shapes: one round trip)
 __device__ inline void wait_loads(f32x4 (&v)[kQ4RedLoads]) {
-    asm volatile("s_waitcnt vmcnt(0)"
-                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),
-                   "+v"(v[7]));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < kQ4RedLoads; ++i) asm volatile("" : "+v"(v[i]));
 }
 
 // TILES column tiles of 16 sequences; RH row halves of 64 rows (row group = 64 RH rows);
