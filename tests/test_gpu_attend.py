@@ -179,7 +179,7 @@ def _batched_case(rng, B, q_len, ctx, hq, hkv, d, bs, window, kv_dtype, scale):
 def test_single_sequence_over_many_pieces(gpu):
     # One kv head keeps the stream kernel's workgroups small, so up to 1024 of them split
     # 40,000 keys of one sequence: the merge then combines far more pieces than its
-    # register-held first 16 and more than one per thread of its workgroup.
+    # register-held first 32 and more than one per thread of its workgroup.
     print("[attend] one sequence, 40000 keys, 2q/1kv/256 fp32", flush=True)
     rng = np.random.default_rng(40000)
     _batched_case(rng, 1, 1, np.array([40000]), 2, 1, 256, 16, 0, F32, 0.0625)

@@ -6,16 +6,17 @@ for as many workgroups as pkv_attend's workspace, so both take the same key spli
 outputs are bit-identical. Then a 4-query verify on the fp64 MFMA kernel, whose rows need
 more scratch per workgroup: it is held to the parity rule against pkv_attend's output and
 the oracle (the two may split the keys differently). A call whose partials cannot fit the
-scratch is refused with PKV_ERR_WORKSPACE before anything is launched. Last, the entry
-point under HIP graph capture (relaxed mode) after one eager call: the graph replayed
-three times, with new queries written eagerly between replays, against pkv_attend."""
+scratch is refused with PKV_ERR_WORKSPACE before anything is launched. A bf16-pool verify
+runs the bf16 MFMA kernel (fp32 partials) through the scratch. Last, the entry point under
+HIP graph capture (relaxed mode) after one eager call: the graph replayed three times, with
+new queries written eagerly between replays, against pkv_attend."""
 import ctypes
 
 import numpy as np
 import pytest
 
 from oracle import oracle as O
-from pkv import F32, LayerSpec, PagedKVCache, hip, lib
+from pkv import BF16, F32, LayerSpec, PagedKVCache, hip, lib
 from pkv.engine import make_params
 from tests import parity
 
@@ -110,6 +111,48 @@ def test_noalloc_refuses_partials_beyond_the_scratch(gpu):
                                        buf.ptr, 4, buf.ptr, 16, 64, 63, buf.ptr)
     assert rc == lib.PKV_ERR_WORKSPACE, rc
     buf.free()
+
+
+def test_noalloc_bf16_verify(gpu):
+    """bf16 pools, 4 queries at G = 2 (8 rows per kv head: the bf16 MFMA kernel, whose
+    partials are fp32): pkv_attend_noalloc against pkv_attend with a workspace (within the
+    float64 bound of each other) and both against the oracle on the same bf16 values."""
+    print("[no_alloc] bf16 verify", flush=True)
+    rng = np.random.default_rng(55)
+    B, q_len, hq, hkv, d = 16, 4, 16, 8, 256
+    ctx = rng.integers(100, 3000, B).astype(np.int32)
+    blocks = (ctx + q_len + BS - 1) // BS
+    nb = int(blocks.sum()) + 4
+    stride = int(blocks.max()) + 1
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((B, stride), np.int32)
+    o = 0
+    for s in range(B):
+        tables[s, :blocks[s]] = perm[o:o + blocks[s]]
+        o += blocks[s]
+    k = O.to_bf16(rng.standard_normal(nb * BS * hkv * d, dtype=np.float32))
+    v = O.to_bf16(rng.standard_normal(nb * BS * hkv * d, dtype=np.float32))
+    q = rng.standard_normal((B, q_len, hq, d), dtype=np.float32)
+    p = make_params(LayerSpec(hq, hkv, d, 0, BF16), BS, nb, 0.0625)
+    max_pos = int(ctx.max()) + q_len - 1
+    dk, dv = hip.DeviceArray.from_numpy(k), hip.DeviceArray.from_numpy(v)
+    dt, dq, dpos = (hip.DeviceArray.from_numpy(x) for x in (tables, q, ctx))
+    out_ws = hip.DeviceArray(q.shape, np.float32)
+    out_na = hip.DeviceArray(q.shape, np.float32)
+    ws_bytes = lib.load().pkv_workspace_size(ctypes.byref(p), B, q_len, max_pos)
+    ws = hip.DeviceArray((ws_bytes,), np.uint8, zero=True)
+    lib.call("pkv_attend", None, ctypes.byref(p), dq.ptr, dk.ptr, dv.ptr, dt.ptr, stride,
+             dpos.ptr, q_len, B, max_pos, out_ws.ptr, ws.ptr, ws.nbytes)
+    lib.call("pkv_attend_noalloc", None, ctypes.byref(p), dq.ptr, dk.ptr, dv.ptr, dt.ptr, stride,
+             dpos.ptr, q_len, B, max_pos, out_na.ptr)
+    a, b = out_ws.numpy(), out_na.numpy()
+    assert np.all(np.isfinite(b)) and O.max_rel_err(b, a) <= parity.TOL_EXACT
+    lens = blocks.astype(np.int32)
+    ref = O.attend(q, k, v, tables, lens, ctx, q_len, hq, hkv, d, BS, 0, scale=0.0625,
+                   nthreads=O.max_threads(), par=1)
+    parity.check(b, ref, bf16=True, what="no-alloc bf16 verify")
+    for x in (dk, dv, dt, dq, dpos, out_ws, out_na, ws):
+        x.free()
 
 
 def _graph_api():
