@@ -76,6 +76,21 @@ constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
 #ifndef PKV_STREAM_EVEN_W
 #define PKV_STREAM_EVEN_W 530
 #endif
+// Lead-in: every sequence's run in the key concatenation starts with this many keys that
+// no piece reads, so a workgroup whose run crosses into a sequence is charged for that
+// piece's start (its page-id and Q round trip before the first batch lands, and its
+// partials) and takes that many fewer keys. Per kernel, in keys of its own batch rate:
+// config 5's verify 125.5 -> 121.5 us (fp64), 72.9 -> 68.4 us (bf16); LSA 41.6 -> 39.6 us;
+// config 2 unchanged. Larger values up to twice these measured the same.
+#ifndef PKV_LEAD_VEC
+#define PKV_LEAD_VEC 16
+#endif
+#ifndef PKV_LEAD_MFMA
+#define PKV_LEAD_MFMA 16
+#endif
+#ifndef PKV_LEAD_BF16
+#define PKV_LEAD_BF16 32
+#endif
 constexpr int kEvenW = PKV_STREAM_EVEN_W;        // even workgroup's share of a pair, / 1024
 
 template <typename KV>
@@ -367,6 +382,7 @@ struct StreamArgs {
     int32_t batch;
     int32_t nwg;       // P: workgroups along the keys
     int32_t nwg_cap;   // at most this many (the workspace holds nwg_cap + batch slots)
+    int32_t lead;      // keys of split work charged to each sequence's start (set by the launcher)
     int32_t rows_seq;  // Hq * q_cnt: workspace rows per sequence
     int32_t* plan;     // [0] per_pair, [1] even, [2 + s] key prefix of sequence s (s <= batch)
     void* part_ml;     // Acc (m, l) per (slot, row)
@@ -422,7 +438,8 @@ __device__ inline bool new_rows_written(int code) {
 }
 
 // Key split: workgroups in pairs (2p, 2p + 1); pair p takes per_pair consecutive keys
-// of the concatenation, its even workgroup the first `even` of them. The launchers make
+// of the concatenation (each sequence's run preceded by its lead-in), its even workgroup
+// the first `even` of them. The launchers make
 // the workgroup count even (or 1, which takes every key).
 struct KeySplit {
     int per_pair;
@@ -464,8 +481,9 @@ __device__ inline void wave_scan_counts(int* s_pre, int batch, int lane) {
     if (lane == 0) s_pre[batch] = carry;
 }
 
-// Key ranges of the launch, laid end to end: s_pre[s] = first key of sequence s in the
-// concatenation (s_pre[batch] = total), s_lo[s] = its first key position, or -1
+// Key ranges of the launch, laid end to end: s_pre[s] = start of sequence s's run in the
+// concatenation (its lead-in, then its keys; an empty sequence has neither; s_pre[batch] =
+// total), s_lo[s] = its first key position, or -1
 // (inactive: zeros), -2 (contract violation: NaN rows), -3 (no query of it in this
 // launch). Workgroup (0, 0) also writes the merge plan and fills the rows of inactive and
 // invalid sequences. Returns the key split.
@@ -492,7 +510,7 @@ __device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_
             const int kb = a.key_off[i], cnt = a.key_off[i + 1] - kb;
             if (cnt < 0 || cnt > a.max_keys || kb < 0) lo = -2;
             else if (cnt > 0) lo = 0, n = cnt;
-            s_pre[i] = n;
+            s_pre[i] = n > 0 ? n + a.lead : 0;
             s_lo[i] = lo;
             s_meta[i] = kb;
             s_meta[B + i] = seq_queries(a, i);
@@ -530,7 +548,7 @@ __device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_
                 lo = -2;
             }
         }
-        s_pre[i] = n;
+        s_pre[i] = n > 0 ? n + a.lead : 0;
         s_lo[i] = lo;
         if (ADDR == kAddrPaged && fused) {
             const int len = a.nr.table_lens[i];
@@ -704,10 +722,12 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         const int pe = ufirst(s_pre[s + 1]);
         if (ps >= k1) break;
         if (pe == ps) continue;
+        const int psr = ps + a.lead;  // the sequence's first key after its lead-in
+        if (psr >= k1) break;
         const int lo_key = ufirst(s_lo[s]);
-        const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
-        const int tb = lo_key + min(k1, pe) - ps;  // one past the last
-        const bool single = sp.owner(ps) == sp.owner(pe - 1);
+        const int ta = lo_key + max(k0, psr) - psr;  // first key of the piece
+        const int tb = lo_key + min(k1, pe) - psr;   // one past the last
+        const bool single = sp.owner(psr) == sp.owner(pe - 1);
         const int32_t* trow = a.tables + (size_t)s * a.table_stride;
         const int last_page = (tb - 1) >> a.bs_shift;
         // the sequence's position (sparse: its list's first index) and query count, from
@@ -1139,10 +1159,12 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         const int pe = ufirst(s_pre[s + 1]);
         if (ps >= k1) break;
         if (pe == ps) continue;
+        const int psr = ps + a.lead;  // the sequence's first key after its lead-in
+        if (psr >= k1) break;
         const int lo_key = ufirst(s_lo[s]);
-        const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
-        const int tb = lo_key + min(k1, pe) - ps;  // one past the last
-        const bool single = sp.owner(ps) == sp.owner(pe - 1);
+        const int ta = lo_key + max(k0, psr) - psr;  // first key of the piece
+        const int tb = lo_key + min(k1, pe) - psr;   // one past the last
+        const bool single = sp.owner(psr) == sp.owner(pe - 1);
         // the sequence's position (sparse: its list's first index) and query count, from
         // the setup's LDS copy
         const int kbeg = SPARSE ? ufirst(s_meta[s]) : 0;
@@ -1201,10 +1223,10 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         }
         // The next sequence's first 64 page ids, for its piece after this one (a piece starts
         // at its sequence's first key).
-        if (PAGED && !FUSED && s + 1 < B && ufirst(s_pre[s + 1]) < k1 &&
+        if (PAGED && !FUSED && s + 1 < B && ufirst(s_pre[s + 1]) + a.lead < k1 &&
             ufirst(s_pre[s + 2]) > ufirst(s_pre[s + 1])) {
             const int lo_n = ufirst(s_lo[s + 1]);
-            const int tb_n = lo_n + min(k1, ufirst(s_pre[s + 2])) - ufirst(s_pre[s + 1]);
+            const int tb_n = lo_n + min(k1, ufirst(s_pre[s + 2])) - ufirst(s_pre[s + 1]) - a.lead;
             pre_raw = a.tables[(size_t)(s + 1) * a.table_stride +
                                min((lo_n >> a.bs_shift) + lane, (tb_n - 1) >> a.bs_shift)];
             pre_s = s + 1;
@@ -1641,10 +1663,12 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         const int pe = ufirst(s_pre[s + 1]);
         if (ps >= k1) break;
         if (pe == ps) continue;
+        const int psr = ps + a.lead;  // the sequence's first key after its lead-in
+        if (psr >= k1) break;
         const int lo_key = ufirst(s_lo[s]);
-        const int ta = lo_key + max(k0, ps) - ps;  // first key of the piece
-        const int tb = lo_key + min(k1, pe) - ps;  // one past the last
-        const bool single = sp.owner(ps) == sp.owner(pe - 1);
+        const int ta = lo_key + max(k0, psr) - psr;  // first key of the piece
+        const int tb = lo_key + min(k1, pe) - psr;   // one past the last
+        const bool single = sp.owner(psr) == sp.owner(pe - 1);
         const int pos0 = ufirst(s_meta[s]);
         const int rows_s = a.G * ufirst(s_meta[B + s]);
         const int32_t* trow = a.tables + (size_t)s * a.table_stride;
@@ -1669,10 +1693,11 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         asm volatile("" ::: "memory");
         // The next sequence's first 64 page ids, for its piece after this one (a piece
         // starts at its sequence's first key).
-        if (s + 1 < B && ufirst(s_pre[s + 1]) < k1 && ufirst(s_pre[s + 2]) > ufirst(s_pre[s + 1])) {
+        if (s + 1 < B && ufirst(s_pre[s + 1]) + a.lead < k1 &&
+            ufirst(s_pre[s + 2]) > ufirst(s_pre[s + 1])) {
             const int lo_n = ufirst(s_lo[s + 1]);
             const int t0_n = lo_n & ~1;
-            const int tb_n = lo_n + min(k1, ufirst(s_pre[s + 2])) - ufirst(s_pre[s + 1]);
+            const int tb_n = lo_n + min(k1, ufirst(s_pre[s + 2])) - ufirst(s_pre[s + 1]) - a.lead;
             pre_raw = a.tables[(size_t)(s + 1) * a.table_stride +
                                min((t0_n >> a.bs_shift) + lane, (tb_n - 1) >> a.bs_shift)];
             pre_s = s + 1;
@@ -1927,7 +1952,7 @@ __global__ __launch_bounds__(merge_threads<D>()) void stream_merge_kernel(Stream
     sp.even = a.plan[1];
     const int ps = a.plan[2 + s], pe = a.plan[3 + s];
     if (pe == ps) return;
-    const int wf = sp.owner(ps), wl = sp.owner(pe - 1);
+    const int wf = sp.owner(ps + a.lead), wl = sp.owner(pe - 1);
     if (wf == wl) return;
     const int cnt = wl - wf + 1;  // <= nwg <= kMaxPieces
     const Acc* pml = static_cast<const Acc*>(a.part_ml);
@@ -2048,6 +2073,7 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
     if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
+    a.lead = PKV_LEAD_VEC;
     dim3 grid(groups, a.nwg);
     hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, ADDR>), grid, dim3(threads), lds, st,
                        a);
@@ -2091,6 +2117,7 @@ int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
     if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
+    a.lead = PKV_LEAD_MFMA;
     dim3 grid(groups, a.nwg);
     if (fused)
         hipLaunchKernelGGL((stream_mfma_kernel<D, RG, TG, WPH, ADDR, kFusable>), grid, dim3(threads), lds, st, a);
@@ -2137,6 +2164,7 @@ int32_t launch_bf16_mfma(StreamArgs a, hipStream_t st) {
     a.nwg = slots / groups > 0 ? slots / groups : 1;
     if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
     if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
+    a.lead = PKV_LEAD_BF16;
     hipLaunchKernelGGL((stream_bf16_mfma_kernel<kAddrPaged>), dim3(groups, a.nwg), dim3(threads), lds,
                        st, a);
     if (hipGetLastError() != hipSuccess)
