@@ -81,7 +81,10 @@ constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
 // piece's start (its page-id and Q round trip before the first batch lands, and its
 // partials) and takes that many fewer keys. Per kernel, in keys of its own batch rate:
 // config 5's verify 125.5 -> 121.5 us (fp64), 72.9 -> 68.4 us (bf16); LSA 41.6 -> 39.6 us;
-// config 2 unchanged. Larger values up to twice these measured the same.
+// config 2 unchanged. Larger values up to twice these measured the same. The interleaved
+// fp64 layout (eight waves on one kv head, a cross-wave exchange at each piece's end) pays
+// more per piece: config 5's verify 121.5 (16) / 118.2 (48) / 116.4-117.5 (96) /
+// 116.3 (128) / 118.8 (192) / 122.3 us (256), four traced runs each.
 #ifndef PKV_LEAD_VEC
 #define PKV_LEAD_VEC 16
 #endif
@@ -90,6 +93,9 @@ constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
 #endif
 #ifndef PKV_LEAD_BF16
 #define PKV_LEAD_BF16 32
+#endif
+#ifndef PKV_LEAD_IW
+#define PKV_LEAD_IW 128
 #endif
 constexpr int kEvenW = PKV_STREAM_EVEN_W;        // even workgroup's share of a pair, / 1024
 
@@ -603,7 +609,7 @@ __device__ inline KeySplit stream_setup(const StreamArgs& a, int* s_pre, int* s_
 // (held: the table, granted: the free list), so this launch reads no state it writes.
 template <int D, typename KV, int WPH>
 __device__ inline void copy_new_rows(const StreamArgs& a, const int* s_meta, const int* s_al,
-                                     int g_first, int wave, int lane) {
+                                     int g_first, int wave, int lane, int w) {
     constexpr int kElt = SKV<KV>::kElt;
     constexpr int kVec = D * kElt / 16;  // 16-byte vectors per head slice
     const int g = g_first + wave / WPH;
@@ -612,7 +618,7 @@ __device__ inline void copy_new_rows(const StreamArgs& a, const int* s_meta, con
     const size_t head_off = (size_t)g * D * kElt;
     const int bs_mask = (1 << a.bs_shift) - 1;
     const int B = a.batch;
-    for (int s = blockIdx.y; s < B; s += a.nwg) {
+    for (int s = w; s < B; s += a.nwg) {
         const int p0 = s_meta[s];
         const int r0 = s_meta[2 * B + s];
         const int n = s_meta[2 * B + s + 1] - r0;
@@ -684,7 +690,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
 
     const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, s_al);
     const bool fused = PAGED && fused_append(a);
-    if (fused) copy_new_rows<D, KV, WPH>(a, s_meta, s_al, blockIdx.x * (kMaxWaves / WPH), wave, lane);
+    if (fused) copy_new_rows<D, KV, WPH>(a, s_meta, s_al, blockIdx.x * (kMaxWaves / WPH), wave, lane, w);
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
@@ -1053,6 +1059,31 @@ __device__ inline i32x4 lds_b128(uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
     return v;
 }
+template <int OFF>
+__device__ inline double lds_r64(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    double v;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ inline int lds_r32(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    int v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+// Untracked LDS writes (as the reads above; ordered with them by the wave's LDS queue).
+__device__ inline void lds_w128(uint32_t addr, i32x4 v) {
+    asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ inline void lds_w64(uint32_t addr, double v) {
+    asm volatile("ds_write_b64 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ inline void lds_w32(uint32_t addr, int v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 template <int N>
 __device__ inline void lgkm_tie0(i32x4 (&k)[N], i32x4 (&v)[N]) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(k[0]), "+v"(v[0]));
@@ -1073,9 +1104,24 @@ __device__ inline void static_for(F&& f) {
     }
 }
 
+// Interleaved waves (IW; head_dim 256, paged or ring pools). Grid (nwg, Hkv): a workgroup
+// is one kv head over one key range, and its eight waves take the batches of each piece
+// in turn (wave v: batches v, v + 8, ...). At the end of a piece the waves' (m, l, o) are
+// combined through LDS: a common row max, then the scaled o and l summed in three rounds
+// (waves 4-7 into 0-3, 2-3 into 0-1, 1 into 0), and wave 0 writes the piece; this runs
+// once the next piece's first batch has been requested. So a piece leaves one partial per
+// kv head where one wave per kv head over an eighth of the keys left eight: config 5's
+// verify writes 5.9 instead of 35.6 MB of double partials, and its merge takes 6.2
+// instead of 9.7 us (verify launch 122.1 -> 116.1 us in the trace). Every kv head's
+// workgroups take the same key split, and column w of every head runs on XCD w mod 8, so
+// the heads of a token row are read at about the same time.
+constexpr int kRedRegion = 2048 * 8 + 128;  // o of one wave (8 rows x 256 doubles), then l
+constexpr int kRedO = 512 + 64;             // m [8 waves][8 rows] (doubles), 8 bad flags, pad
+__host__ __device__ constexpr size_t iw_red_bytes() { return kRedO + 4 * (size_t)kRedRegion; }
+
 // FUSED: the launch of a fused append (paged pools); a separate instance, so the scalar
 // state of the appended rows costs the other launches nothing.
-template <int D, int RG, int TG, int WPH, int ADDR, bool FUSED>
+template <int D, int RG, int TG, int WPH, int ADDR, bool FUSED, bool IW = false>
 __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs a) {
     constexpr int NQ = D / 64;  // 64-d chunks of a row
     constexpr int kSlot = mfma_slot(D);
@@ -1097,26 +1143,31 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
     const int wave = ufirst(tid / kSW);
-    const int w = blockIdx.y;
+    const int w = IW ? blockIdx.x : blockIdx.y;  // the workgroup's key range
     const int B = a.batch;
 
     static_assert(!FUSED || PAGED, "appended rows: paged pools only");
+    static_assert(!IW || (WPH == 1 && RG == 2 && TG == 1 && D == 256 && !SPARSE), "interleaved waves");
     const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, s_al);
     constexpr bool fused = FUSED;  // the launcher passes the rows exactly when FUSED
     const int hpw = ufirst((int)(blockDim.x / kSW) / WPH);  // kv heads per workgroup
-    if (fused) copy_new_rows<D, float, WPH>(a, s_meta, s_al, blockIdx.x * hpw, wave, lane);
+    if (fused) {
+        if constexpr (IW) copy_new_rows<D, float, kMaxWaves>(a, s_meta, s_al, blockIdx.y, wave, lane, w);
+        else copy_new_rows<D, float, WPH>(a, s_meta, s_al, blockIdx.x * hpw, wave, lane, w);
+    }
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
     const int k1 = min(total, sp.start(w + 1));
     // this wave's KV head. With WPH > 1 the waves of a head share its staging and meet at
     // barriers, so a wave past the last head (a head group with fewer heads) does the work of
-    // the last head and stores nothing, instead of leaving.
-    const int g_raw = blockIdx.x * hpw + wave / WPH;
+    // the last head and stores nothing, instead of leaving. IW: the workgroup's head, whose
+    // pieces wave 0 stores.
+    const int g_raw = IW ? (int)blockIdx.y : blockIdx.x * hpw + wave / WPH;
     if (WPH == 1 && g_raw >= a.Hkv) return;
-    const bool idle = g_raw >= a.Hkv;
-    const int g = idle ? a.Hkv - 1 : g_raw;
-    const int rb = (wave % WPH) * 4 * RG;  // first of this wave's rows of the head
+    const bool idle = IW ? wave != 0 : g_raw >= a.Hkv;
+    const int g = g_raw >= a.Hkv ? a.Hkv - 1 : g_raw;
+    const int rb = IW ? 0 : (wave % WPH) * 4 * RG;  // first of this wave's rows of the head
 
     const int rows = a.G * a.q_cnt;
     const size_t row_bytes = (size_t)a.Hkv * D * 4;
@@ -1137,6 +1188,9 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                   (WPH == 1 ? (size_t)wave * mfma_stage_bytes(D, TG)
                             : (size_t)(wave / WPH) * 2 * mfma_stage_bytes(D, TG));
     const int hw = WPH == 1 ? 0 : wave % WPH;  // this wave's share of the copies
+    // IW: the waves' exchange area for the end of a piece, after the eight staging buffers
+    char* const red = reinterpret_cast<char*>(smem) + mfma_stage_offset(B, fused) +
+                      (size_t)kMaxWaves * mfma_stage_bytes(D, TG);
     // Waves w and w + 4 of an 8-wave workgroup share a SIMD, whose issue slots bound the
     // batch loop; the arbiter favours the older wave, which left the other one alone for
     // the last ~15% of a piece. Alternating their priorities every batch keeps the two in
@@ -1153,6 +1207,179 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         }
         s = lo;
     }
+    // The piece's (m, l, o) per row. IW: a piece is finished (the waves' exchange, then
+    // wave 0's stores) once the next piece's first batch has been requested, so that batch's
+    // latency covers the exchange and the waves' wait for the slowest of them.
+    double m[RG], l[RG], o[RG][NQ][4];
+    int pend_s = -1, pend_rows = 0, pend_nb = 0;  // IW: the piece still to finish
+    bool pend_single = false, pend_bad = false;
+    // nb: the piece's batches (IW: waves past its last batch hold (-inf, 0, 0)).
+    auto finish = [&](int fs, bool fsingle, int frows, int nb, bool fbad) {
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            // keep the last accumulations ahead of the stores' branches
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(o[rg][q][e]));
+        }
+        if constexpr (IW) {
+            // The waves' (m, l, o) into wave 0's: the rows' common max, then the rescaled
+            // o and l summed in three rounds. The branches are uniform over the workgroup, so
+            // every wave meets the same barriers. The next piece's copies into the staging
+            // buffers are in flight: the exchange area's LDS accesses are untracked by the
+            // compiler (it would wait for the copies before each of them), and the barriers
+            // wait only for LDS (lgkmcnt), with no fence.
+            if (nb > 1) {
+                // per-lane offsets through an opaque copy, so the addresses below are formed
+                // here rather than kept in registers for the whole kernel
+                uint32_t lo = lane;
+                asm volatile("" : "+v"(lo));
+                const uint32_t rm = lds_addr(red);  // m of [wave][rg][x] (doubles)
+                const uint32_t rbad = rm + 512;     // [wave] (ints)
+                const uint32_t xo = lo & 3;
+                auto sync = [&]() {
+                    __builtin_amdgcn_s_waitcnt(kLgkm0);
+                    __builtin_amdgcn_s_barrier();
+                    asm volatile("" ::: "memory");
+                };
+                if (lane < 4) {  // x = lane (b = y = 0)
+                    lds_w64(rm + 64 * wave + 8 * lo, m[0]);
+                    lds_w64(rm + 64 * wave + 8 * lo + 32, m[1]);
+                }
+                if (lane == 0) lds_w32(rbad + 4 * wave, fbad ? 1 : 0);
+                sync();
+                double mv[2][kMaxWaves];
+                int bv[kMaxWaves];
+                static_for<0, kMaxWaves>([&](auto V) {
+                    constexpr int v = decltype(V)::value;
+                    mv[0][v] = lds_r64<64 * v>(rm + 8 * xo);
+                    mv[1][v] = lds_r64<64 * v + 32>(rm + 8 * xo);
+                    bv[v] = lds_r32<4 * v>(rbad + 0 * lo);
+                });
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(mv[0][0]));
+#pragma unroll
+                for (int v = 0; v < kMaxWaves; ++v) asm volatile("" : "+v"(mv[0][v]), "+v"(mv[1][v]), "+v"(bv[v]));
+                bool any_bad = false;
+#pragma unroll
+                for (int v = 0; v < kMaxWaves; ++v) any_bad = any_bad || bv[v] != 0;
+                fbad = any_bad;
+#pragma unroll
+                for (int rg = 0; rg < RG; ++rg) {
+                    double M = -INFINITY;
+#pragma unroll
+                    for (int v = 0; v < kMaxWaves; ++v) M = fmax(M, mv[rg][v]);
+                    const double f = m[rg] == -INFINITY ? 0.0 : exp_acc(m[rg] - M);
+                    l[rg] *= f;
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[rg][q][e] *= f;
+                    m[rg] = M;
+                }
+                // Region r: element pair k of o (k = 8 rg + 2 q + e / 2) of lane L at byte
+                // 16 (64 k + L) (16-byte accesses, consecutive over the lanes), then l [rg][x].
+                const uint32_t reg0 = lds_addr(red + kRedO);
+                auto put = [&](int r) {
+                    const uint32_t rs = reg0 + r * kRedRegion;  // uniform
+                    const uint32_t ro = rs + 16 * lo;
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) {
+                        const int rg = k >> 3, q = (k >> 1) & 3, e = 2 * (k & 1);
+                        lds_w128(ro + 1024 * k, __builtin_bit_cast(i32x4, f64x2{o[rg][q][e], o[rg][q][e + 1]}));
+                    }
+                    if (lane < 4) {
+                        const uint32_t rl = rs + 16384 + 8 * lo;
+                        lds_w64(rl, l[0]);
+                        lds_w64(rl + 32, l[1]);
+                    }
+                };
+                auto add = [&](int r) {  // in two halves of eight reads
+                    const uint32_t rs = reg0 + r * kRedRegion;  // uniform
+                    const uint32_t ro = rs + 16 * lo;
+                    static_for<0, 2>([&](auto H) {
+                        constexpr int h = decltype(H)::value;
+                        i32x4 v[8];
+                        static_for<0, 8>([&](auto K) {
+                            constexpr int k = decltype(K)::value;
+                            v[k] = lds_b128<1024 * (8 * h + k)>(ro);
+                        });
+                        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]));
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            asm volatile("" : "+v"(v[k]));
+                            const f64x2 d = __builtin_bit_cast(f64x2, v[k]);
+                            const int q = k >> 1, e = 2 * (k & 1);
+                            o[h][q][e] += d.x;
+                            o[h][q][e + 1] += d.y;
+                        }
+                    });
+                    const uint32_t rl = rs + 16384 + 8 * xo;
+                    double l0 = lds_r64<0>(rl), l1 = lds_r64<32>(rl);
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(l0), "+v"(l1));
+                    l[0] += l0;
+                    l[1] += l1;
+                };
+                if (nb > 4) {  // waves 4-7 into 0-3 (regions 0-3)
+                    if (wave >= 4) put(wave - 4);
+                    sync();
+                    if (wave < 4) add(wave);
+                }
+                if (nb > 2) {  // waves 2, 3 into 0, 1 (regions 2, 3, which only they read before)
+                    if (wave == 2 || wave == 3) put(wave);
+                    sync();
+                    if (wave < 2) add(wave + 2);
+                }
+                if (wave == 1) put(1);  // wave 1 into 0 (region 1, which only wave 1 read before)
+                sync();
+                if (wave == 0) add(1);
+            }
+        }
+        if (idle) {
+            // a wave past the last head (IW: every wave but 0): nothing to store
+        } else if (fsingle) {
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                const int r = rb + 4 * rg + x;
+                if (r < frows) {
+                    const double inv = 1.0 / (l[rg] + 1e-10);
+                    float* op = a.out + out_row(a, fs, g, r) * D + 16 * b + 4 * y;
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q) {
+                        float4 v;
+                        v.x = fbad ? __builtin_nanf("") : (float)(o[rg][q][0] * inv);
+                        v.y = fbad ? __builtin_nanf("") : (float)(o[rg][q][1] * inv);
+                        v.z = fbad ? __builtin_nanf("") : (float)(o[rg][q][2] * inv);
+                        v.w = fbad ? __builtin_nanf("") : (float)(o[rg][q][3] * inv);
+                        *reinterpret_cast<float4*>(op + 64 * q) = v;
+                    }
+                }
+            }
+        } else {
+            const size_t slot = (size_t)(w + fs) * a.rows_seq;
+            double* po = static_cast<double*>(a.part_o);
+            double* pml = static_cast<double*>(a.part_ml);
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                const int r = rb + 4 * rg + x;
+                if (r < rows) {
+                    const int row = (r / a.G) * a.Hq + g * a.G + r % a.G;
+                    double* dst = po + (slot + row) * D + 16 * b + 4 * y;
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q) {
+                        double2* d2 = reinterpret_cast<double2*>(dst + 64 * q);
+                        d2[0] = make_double2(o[rg][q][0], o[rg][q][1]);
+                        d2[1] = make_double2(o[rg][q][2], o[rg][q][3]);
+                    }
+                    if (b == 0 && y == 0) {
+                        pml[(slot + row) * 2 + 0] = fbad ? __builtin_nan("") : m[rg];
+                        pml[(slot + row) * 2 + 1] = l[rg];
+                    }
+                }
+            }
+        }
+    };
+
     int pre_s = -1, pre_raw = 0;  // the next piece's first page ids (pre_s: its sequence)
     for (; s < B; ++s) {
         const int ps = ufirst(s_pre[s]);
@@ -1211,16 +1438,24 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         float4 qf[RG][NQ];  // fp32: converted at each use, which saves registers
         int pq[RG], wsr[RG];
         bool live[RG];
+        // IW: requested after the piece before is finished (fewer registers live there)
+        auto load_q = [&]() {
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                const int r = rb + 4 * rg + x;
+                const float* qp = a.q + out_row(a, s, g, min(r, rows - 1)) * D + 16 * b + 4 * y;
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) qf[rg][q] = *reinterpret_cast<const float4*>(qp + 64 * q);
+            }
+        };
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
             const int r = rb + 4 * rg + x;
             live[rg] = r < rows_s;
             pq[rg] = SPARSE ? INT32_MAX : pos0 + a.j0 + r / a.G;
             wsr[rg] = SPARSE ? 0 : window_start(pq[rg], a.window);
-            const float* qp = a.q + out_row(a, s, g, min(r, rows - 1)) * D + 16 * b + 4 * y;
-#pragma unroll
-            for (int q = 0; q < NQ; ++q) qf[rg][q] = *reinterpret_cast<const float4*>(qp + 64 * q);
         }
+        if constexpr (!IW) load_q();
         // The next sequence's first 64 page ids, for its piece after this one (a piece starts
         // at its sequence's first key).
         if (PAGED && !FUSED && s + 1 < B && ufirst(s_pre[s + 1]) + a.lead < k1 &&
@@ -1231,22 +1466,14 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                                min((lo_n >> a.bs_shift) + lane, (tb_n - 1) >> a.bs_shift)];
             pre_s = s + 1;
         }
+        auto zero_q = [&]() {
 #pragma unroll
-        for (int rg = 0; rg < RG; ++rg)
+            for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-            for (int q = 0; q < NQ; ++q)
-                if (rb + 4 * rg + x >= rows) qf[rg][q] = make_float4(0.f, 0.f, 0.f, 0.f);
-        double m[RG], l[RG], o[RG][NQ][4];
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) {
-            m[rg] = -INFINITY;
-            l[rg] = 0.0;
-#pragma unroll
-            for (int q = 0; q < NQ; ++q)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[rg][q][e] = 0.0;
-        }
-
+                for (int q = 0; q < NQ; ++q)
+                    if (rb + 4 * rg + x >= rows) qf[rg][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+        };
+        if constexpr (!IW) zero_q();
         int64_t rbase = 0;  // ring mode: first row of the sequence's ring
         int r0 = 0;         // ring mode: ring row of key ta
         if constexpr (RING) {
@@ -1344,14 +1571,30 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
         };
 
         constexpr int kBufBytes = (int)mfma_stage_bytes(D, TG);
-        issue(ta, stage);
+        constexpr int kStepT = IW ? kMaxWaves * U : U;  // tokens from one of a wave's batches to the next
+        const int t1 = IW ? ta + U * wave : ta;          // this wave's first batch
+        if (t1 < tb) issue(t1, stage);
         if (WPH > 1 && ta + U < tb) issue(ta + U, stage + kBufBytes);
-        int it = 0;  // batch index in the piece (WPH > 1: buffer it % 2)
-        for (int t = ta; t < tb; t += U, ++it) {
+        if constexpr (IW) {  // the piece before, while this one's first batch is on its way
+            if (pend_s >= 0) finish(pend_s, pend_single, pend_rows, pend_nb, pend_bad);
+            load_q();
+            zero_q();
+        }
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            m[rg] = -INFINITY;
+            l[rg] = 0.0;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[rg][q][e] = 0.0;
+        }
+        int it = 0;  // this wave's batch index in the piece (WPH > 1: buffer it % 2)
+        for (int t = t1; t < tb; t += kStepT, ++it) {
             float4 kw[TG][NQ], vw[TG][NQ];
             if constexpr (WPH == 1) {
                 if (toggle) {
-                    if ((((t - ta) / U) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+                    if ((it + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
                     else __builtin_amdgcn_s_setprio(0);
                 }
                 __builtin_amdgcn_s_waitcnt(0);  // this batch's slices are in LDS
@@ -1363,7 +1606,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                         vw[tg][q] = *reinterpret_cast<const float4*>(stage + (2 * (4 * tg + y) + 1) * kSlot + vdo + 256 * q);
                     }
                 __builtin_amdgcn_s_waitcnt(kLgkm0);  // read out before the slots are refilled
-                if (t + U < tb) issue(t + U, stage);
+                if (t + kStepT < tb) issue(t + kStepT, stage);
             } else {
                 // This wave's copies of batch it have landed (those of batch it + 1, if issued,
                 // stay in flight); the barrier then covers the other waves' copies. It carries no
@@ -1487,58 +1730,18 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_mfma_kernel(StreamArgs
                     }
         }
         bad = __any(bad);
-
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) {
-            // keep the last accumulations ahead of the stores' branches
-#pragma unroll
-            for (int q = 0; q < NQ; ++q)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(o[rg][q][e]));
-        }
-        if (idle) {
-            // a wave past the last head: nothing to store
-        } else if (single) {
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg) {
-                const int r = rb + 4 * rg + x;
-                if (r < rows_s) {
-                    const double inv = 1.0 / (l[rg] + 1e-10);
-                    float* op = a.out + out_row(a, s, g, r) * D + 16 * b + 4 * y;
-#pragma unroll
-                    for (int q = 0; q < NQ; ++q) {
-                        float4 v;
-                        v.x = bad ? __builtin_nanf("") : (float)(o[rg][q][0] * inv);
-                        v.y = bad ? __builtin_nanf("") : (float)(o[rg][q][1] * inv);
-                        v.z = bad ? __builtin_nanf("") : (float)(o[rg][q][2] * inv);
-                        v.w = bad ? __builtin_nanf("") : (float)(o[rg][q][3] * inv);
-                        *reinterpret_cast<float4*>(op + 64 * q) = v;
-                    }
-                }
-            }
+        if constexpr (IW) {
+            pend_s = s;
+            pend_single = single;
+            pend_rows = rows_s;
+            pend_nb = (tb - ta + U - 1) / U;
+            pend_bad = bad;
         } else {
-            const size_t slot = (size_t)(w + s) * a.rows_seq;
-            double* po = static_cast<double*>(a.part_o);
-            double* pml = static_cast<double*>(a.part_ml);
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg) {
-                const int r = rb + 4 * rg + x;
-                if (r < rows) {
-                    const int row = (r / a.G) * a.Hq + g * a.G + r % a.G;
-                    double* dst = po + (slot + row) * D + 16 * b + 4 * y;
-#pragma unroll
-                    for (int q = 0; q < NQ; ++q) {
-                        double2* d2 = reinterpret_cast<double2*>(dst + 64 * q);
-                        d2[0] = make_double2(o[rg][q][0], o[rg][q][1]);
-                        d2[1] = make_double2(o[rg][q][2], o[rg][q][3]);
-                    }
-                    if (b == 0 && y == 0) {
-                        pml[(slot + row) * 2 + 0] = bad ? __builtin_nan("") : m[rg];
-                        pml[(slot + row) * 2 + 1] = l[rg];
-                    }
-                }
-            }
+            finish(s, single, rows_s, 1, bad);
         }
+    }
+    if constexpr (IW) {
+        if (pend_s >= 0) finish(pend_s, pend_single, pend_rows, pend_nb, pend_bad);
     }
 }
 
@@ -2092,8 +2295,54 @@ constexpr size_t kMfmaLdsMax = kStreamLdsMax;
 #ifndef PKV_MFMA_HEADS_PER_WG
 #define PKV_MFMA_HEADS_PER_WG 2
 #endif
+// Interleaved waves (head_dim 256, paged or ring pools): grid (nwg, Hkv), eight waves per
+// kv head. False when the batch's LDS does not fit it (the caller then takes the launch
+// below).
+template <int ADDR>
+bool launch_mfma_iw(StreamArgs& a, hipStream_t st, int32_t* rc) {
+    constexpr int D = 256, RG = 2, TG = 1;
+    const bool fused = ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0;
+    const size_t lds = mfma_stage_offset(a.batch, fused) + (size_t)kMaxWaves * mfma_stage_bytes(D, TG) +
+                       iw_red_bytes();
+    if (lds > kMfmaLdsMax) return false;
+    constexpr bool kFusable = ADDR == kAddrPaged;
+    const void* fn = fused ? reinterpret_cast<const void*>(&stream_mfma_kernel<D, RG, TG, 1, ADDR, kFusable, true>)
+                           : reinterpret_cast<const void*>(&stream_mfma_kernel<D, RG, TG, 1, ADDR, false, true>);
+    if (!reserve_lds(fn, (int)kMfmaLdsMax)) {
+        *rc = fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
+        return true;
+    }
+    const int slots = fill_workgroups(fn, kMaxWaves * kSW, lds);
+    if (slots <= 0) {
+        *rc = fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
+        return true;
+    }
+    // every kv head's workgroups take the same key split; nwg even keeps column w on XCD w mod 8
+    a.nwg = slots / a.Hkv > 0 ? slots / a.Hkv : 1;
+    if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
+    if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
+    a.lead = PKV_LEAD_IW;
+    const dim3 grid(a.nwg, a.Hkv);
+    if (fused)
+        hipLaunchKernelGGL((stream_mfma_kernel<D, RG, TG, 1, ADDR, kFusable, true>), grid, dim3(kMaxWaves * kSW), lds, st, a);
+    else
+        hipLaunchKernelGGL((stream_mfma_kernel<D, RG, TG, 1, ADDR, false, true>), grid, dim3(kMaxWaves * kSW), lds, st, a);
+    if (hipGetLastError() != hipSuccess) {
+        *rc = fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
+        return true;
+    }
+    hipLaunchKernelGGL((stream_merge_kernel<D, double>), dim3(a.rows_seq, a.batch + (fused ? 1 : 0)),
+                       dim3(merge_threads<D>()), 0, st, a);
+    *rc = PKV_OK;
+    return true;
+}
+
 template <int D, int RG, int TG, int WPH, int ADDR>
 int32_t launch_mfma_addr(StreamArgs a, hipStream_t st) {
+    if constexpr (D == 256 && WPH == 1 && RG == 2 && TG == 1 && ADDR != kAddrSparse) {
+        int32_t rc = PKV_OK;
+        if (launch_mfma_iw<ADDR>(a, st, &rc)) return rc;
+    }
     // WPH > 1: the waves of a head meet at a barrier every batch, so a workgroup holds few
     // heads (a barrier waits for every wave of the workgroup).
     constexpr int kHeadsMax = WPH == 1 ? kMaxWaves : PKV_MFMA_HEADS_PER_WG;
