@@ -84,7 +84,9 @@ constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
 // config 2 unchanged. Larger values up to twice these measured the same. The interleaved
 // fp64 layout (eight waves on one kv head, a cross-wave exchange at each piece's end) pays
 // more per piece: config 5's verify 121.5 (16) / 118.2 (48) / 116.4-117.5 (96) /
-// 116.3 (128) / 118.8 (192) / 122.3 us (256), four traced runs each.
+// 116.3 (128) / 118.8 (192) / 122.3 us (256), four traced runs each; the interleaved bf16
+// kernel (16-token batches) 71.5 (32) / 69.6 (64) / 68.8 (128) / 65.6-65.8 (256) /
+// 64.7 (384) / 66.4 (512) / 67.7 us (768), three each.
 #ifndef PKV_LEAD_VEC
 #define PKV_LEAD_VEC 16
 #endif
@@ -96,6 +98,9 @@ constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
 #endif
 #ifndef PKV_LEAD_IW
 #define PKV_LEAD_IW 128
+#endif
+#ifndef PKV_LEAD_BF16_IW
+#define PKV_LEAD_BF16_IW 384
 #endif
 constexpr int kEvenW = PKV_STREAM_EVEN_W;        // even workgroup's share of a pair, / 1024
 
@@ -1794,7 +1799,18 @@ __device__ inline uint16_t bf16_rne_bits(float x) {
 }
 __device__ inline float bf16_bits_to_float(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-template <int ADDR>
+// Interleaved waves (IW), as in the fp64 kernel: grid (nwg, Hkv), the eight waves of a
+// workgroup take the 16-token batches of one kv head's pieces in turn and combine their
+// (m, l, o) through LDS (fp32, after the hi/lo fold) once the next piece's first batch is
+// requested. The eight staging buffers leave room for three 8 KiB exchange regions, so the
+// sum takes four rounds: waves 4-6 into 0-2, 7 into 3, 2-3 into 0-1, 1 into 0. Config 5's
+// bf16 verify: 60.4 + 6.7 -> 59.7 + 4.9 us (stream + merge in the trace), traffic 1.149 ->
+// 1.025 x algorithmic.
+constexpr int kBfRedRegion = 8192 + 32;  // o of the 32 hi-column lanes (8 rows x 256), then l
+constexpr int kBfRedO = 256 + 32;        // m [8 waves][8 rows] (floats), 8 bad flags
+__host__ __device__ constexpr size_t bf_iw_red_bytes() { return kBfRedO + 3 * (size_t)kBfRedRegion; }
+
+template <int ADDR, bool IW = false>
 __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(StreamArgs a) {
     constexpr int D = 256;
     static_assert(ADDR == kAddrPaged, "paged pools");
@@ -1808,14 +1824,14 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
     const int wave = ufirst(tid / kSW);
-    const int w = blockIdx.y;
+    const int w = IW ? blockIdx.x : blockIdx.y;  // the workgroup's key range
     const int B = a.batch;
     const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, nullptr);  // no fused append
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
     const int k1 = min(total, sp.start(w + 1));
-    const int g = blockIdx.x * kMaxWaves + wave;  // this wave's KV head
+    const int g = IW ? (int)blockIdx.y : blockIdx.x * kMaxWaves + wave;  // this wave's KV head
     if (g >= a.Hkv) return;
 
     const int rows = a.G * a.q_cnt;
@@ -1829,6 +1845,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
     const float sl2 = a.scale * kLog2e;
     char* sK = reinterpret_cast<char*>(smem) + mfma_stage_offset(B, false) + (size_t)wave * kBfStage;
     char* sV = sK + kBfTok * kBfRow;
+    // IW: the waves' exchange area, after the eight staging buffers
+    char* const red = reinterpret_cast<char*>(smem) + mfma_stage_offset(B, false) + (size_t)kMaxWaves * kBfStage;
 
     // Copy offsets: instruction j moves tokens 2j, 2j + 1 of the batch (lanes 0-31, 32-63);
     // lane p of a row loads the global chunk that belongs at its LDS position.
@@ -1860,6 +1878,155 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         }
         s = lo;
     }
+    // The piece's row max (log2 units), this lane's share of the row sum, O^T. IW: a piece
+    // is finished (the waves' exchange, then wave 0's stores) once the next piece's first
+    // batch has been requested, so that batch's latency covers the exchange.
+    float m = -INFINITY;
+    float l = 0.f;
+    f32x4 o[16];  // O^T: d-tile u holds dims 16u + 4 grp + r of column l16
+    int pend_s = -1, pend_rows = 0, pend_nb = 0;  // IW: the piece still to finish
+    bool pend_single = false, pend_bad = false;
+    const bool idle = IW && wave != 0;
+    // nb: the piece's batches (IW: waves past its last batch hold (-inf, 0, 0)).
+    auto finish = [&](int fs, bool fsingle, int frows, int nb, bool fbad) {
+        // O^T hi + lo columns; the row sum over the four lane groups
+        l = allreduce_hi<16>(l, OpSum());
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[u][r] += dpp<kRor8>(o[u][r]);
+        if constexpr (IW) {
+            // The waves' rows into wave 0's: the rows' common max, then the rescaled o (the
+            // 32 hi-column lanes, which hold the rows after the fold) and l summed. Uniform
+            // branches: every wave meets the same barriers. The next piece's copies are in
+            // flight, so the LDS accesses are untracked and the barriers wait for LDS only.
+            if (nb > 1) {
+                uint32_t lo = lane;  // opaque: the addresses are formed here
+                asm volatile("" : "+v"(lo));
+                const uint32_t rm = lds_addr(red);  // m of [wave][row] (floats)
+                const uint32_t rbad = rm + 256;     // [wave] (ints)
+                const uint32_t rro = lo & 7;        // this lane's row
+                auto sync = [&]() {
+                    __builtin_amdgcn_s_waitcnt(kLgkm0);
+                    __builtin_amdgcn_s_barrier();
+                    asm volatile("" ::: "memory");
+                };
+                if (lane < 8) lds_w32(rm + 32 * wave + 4 * lo, __float_as_int(m));  // row = lane
+                if (lane == 0) lds_w32(rbad + 4 * wave, fbad ? 1 : 0);
+                sync();
+                int mv[kMaxWaves], bv[kMaxWaves];
+                static_for<0, kMaxWaves>([&](auto V) {
+                    constexpr int v = decltype(V)::value;
+                    mv[v] = lds_r32<32 * v>(rm + 4 * rro);
+                    bv[v] = lds_r32<4 * v>(rbad + 0 * lo);
+                });
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(mv[0]));
+#pragma unroll
+                for (int v = 0; v < kMaxWaves; ++v) asm volatile("" : "+v"(mv[v]), "+v"(bv[v]));
+                bool any_bad = false;
+                float M = -INFINITY;
+#pragma unroll
+                for (int v = 0; v < kMaxWaves; ++v) {
+                    any_bad = any_bad || bv[v] != 0;
+                    M = fmaxf(M, __int_as_float(mv[v]));
+                }
+                fbad = any_bad;
+                const float f = m == -INFINITY ? 0.f : exp2f(m - M);
+                l *= f;
+#pragma unroll
+                for (int u = 0; u < 16; ++u) o[u] *= f;
+                m = M;
+                // Region r: d-tile u of hi-column lane j = 8 grp + l16 at byte 16 (32 u + j),
+                // then l [row].
+                const uint32_t reg0 = lds_addr(red + kBfRedO);
+                const uint32_t jo = 16 * ((lo >> 4) * 8 + (lo & 7));
+                auto put = [&](int r) {
+                    const uint32_t rs = reg0 + r * kBfRedRegion;  // uniform
+                    if (hi_col) {
+#pragma unroll
+                        for (int u = 0; u < 16; ++u) lds_w128(rs + jo + 512 * u, __builtin_bit_cast(i32x4, o[u]));
+                    }
+                    if (lane < 8) lds_w32(rs + 8192 + 4 * lo, __float_as_int(l));
+                };
+                auto add = [&](int r) {  // in two halves of eight reads
+                    const uint32_t rs = reg0 + r * kBfRedRegion;  // uniform
+                    if (hi_col) {
+                        static_for<0, 2>([&](auto H) {
+                            constexpr int h = decltype(H)::value;
+                            i32x4 v[8];
+                            static_for<0, 8>([&](auto U) {
+                                constexpr int u = decltype(U)::value;
+                                v[u] = lds_b128<512 * (8 * h + u)>(rs + jo);
+                            });
+                            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]));
+#pragma unroll
+                            for (int u = 0; u < 8; ++u) {
+                                asm volatile("" : "+v"(v[u]));
+                                o[8 * h + u] += __builtin_bit_cast(f32x4, v[u]);
+                            }
+                        });
+                    }
+                    int lv = lds_r32<8192>(rs + 4 * rro);
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lv));
+                    l += __int_as_float(lv);
+                };
+                if (nb > 4) {  // waves 4-6 into 0-2 (regions 0-2), then every region read
+                    if (wave >= 4 && wave < 7) put(wave - 4);
+                    sync();
+                    if (wave < 3) add(wave);
+                    sync();
+                }
+                if (nb > 7) {  // wave 7 into 3 (region 0)
+                    if (wave == 7) put(0);
+                    sync();
+                    if (wave == 3) add(0);
+                }
+                if (nb > 2) {  // waves 2, 3 into 0, 1 (regions 2, 1; region 0 may still be read)
+                    if (wave == 2) put(2);
+                    if (wave == 3) put(1);
+                    sync();
+                    if (wave == 0) add(2);
+                    if (wave == 1) add(1);
+                }
+                if (wave == 1) put(1);  // wave 1 into 0 (region 1, which wave 1 read last)
+                sync();
+                if (wave == 0) add(1);
+            }
+        }
+        if (idle) {
+            // IW: every wave but 0 has handed its rows over
+        } else if (fsingle) {
+            if (hi_col && rr < frows) {
+                const float inv = 1.f / (l + 1e-10f);
+                float* op = a.out + out_row(a, fs, g, rr) * D + 4 * grp;
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    float4 v;
+                    v.x = fbad ? __builtin_nanf("") : o[u][0] * inv;
+                    v.y = fbad ? __builtin_nanf("") : o[u][1] * inv;
+                    v.z = fbad ? __builtin_nanf("") : o[u][2] * inv;
+                    v.w = fbad ? __builtin_nanf("") : o[u][3] * inv;
+                    *reinterpret_cast<float4*>(op + 16 * u) = v;
+                }
+            }
+        } else {
+            const size_t slot = (size_t)(w + fs) * a.rows_seq;
+            float* po = static_cast<float*>(a.part_o);
+            float* pml = static_cast<float*>(a.part_ml);
+            if (hi_col && rr < rows) {
+                const int row = (rr / a.G) * a.Hq + g * a.G + rr % a.G;
+                float* dst = po + (slot + row) * D + 4 * grp;
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    *reinterpret_cast<float4*>(dst + 16 * u) = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
+                if (grp == 0) {  // the merge takes natural-log units
+                    pml[(slot + row) * 2 + 0] = fbad ? __builtin_nanf("") : m * kLn2;
+                    pml[(slot + row) * 2 + 1] = l;
+                }
+            }
+        }
+    };
+
     int pre_s = -1, pre_raw = 0;  // the next piece's first page ids (pre_s: its sequence)
     for (; s < B; ++s) {
         const int ps = ufirst(s_pre[s]);
@@ -1885,14 +2052,15 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
             pre_s == s ? pre_raw : trow[min((t0 >> a.bs_shift) + lane, last_page)];
         asm volatile("" ::: "memory");
         float4 qraw[8][2];
-        {
+        auto load_q = [&]() {  // IW: after the piece before is finished (fewer registers live)
             const float* qp = a.q + out_row(a, s, g, min(rr, rows - 1)) * D + 8 * grp;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 qraw[c][0] = *reinterpret_cast<const float4*>(qp + 32 * c);
                 qraw[c][1] = *reinterpret_cast<const float4*>(qp + 32 * c + 4);
             }
-        }
+        };
+        if constexpr (!IW) load_q();
         asm volatile("" ::: "memory");
         // The next sequence's first 64 page ids, for its piece after this one (a piece
         // starts at its sequence's first key).
@@ -1917,12 +2085,6 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
             bad = bad || (lane_ok && !id_ok);
             vpg = lane_ok && id_ok ? first_raw : 0;
         }
-        float m = -INFINITY;  // reference max of this lane's row (log2 units)
-        float l = 0.f;        // this lane's share of the row sum (its 4 of every 16 tokens)
-        f32x4 o[16];          // O^T: d-tile u holds dims 16u + 4 grp + r of column l16
-#pragma unroll
-        for (int u = 0; u < 16; ++u) o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-
         auto issue = [&](int t) {
             const int tl = min(t + kBfTok - 1, tb - 1);
             if ((tl >> a.bs_shift) - pgbase >= kSW) {  // next 64 page ids
@@ -1950,7 +2112,17 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
             }
         };
 
-        issue(t0);
+        constexpr int kStepT = IW ? kMaxWaves * kBfTok : kBfTok;  // from one of a wave's batches to the next
+        const int t1 = IW ? t0 + kBfTok * wave : t0;               // this wave's first batch
+        if (t1 < tb) issue(t1);
+        if constexpr (IW) {  // the piece before, while this one's first batch is on its way
+            if (pend_s >= 0) finish(pend_s, pend_single, pend_rows, pend_nb, pend_bad);
+            load_q();
+        }
+        m = -INFINITY;
+        l = 0.f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         // Q^T as the B operand of step c: column l16 = row rr, dims 32c + 8 grp + e; its hi
         // (column < 8) or lo part, zero for rows past `rows`.
         bf16x8 qreg[8];
@@ -1969,7 +2141,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
                 }
             }
         }
-        for (int t = t0; t < tb; t += kBfTok) {
+        int it = 0;  // this wave's batch index in the piece
+        for (int t = t1; t < tb; t += kStepT, ++it) {
             __builtin_amdgcn_s_waitcnt(0);  // this batch is in LDS
             if (t + kBfTok > tb - 1 && (tb & 1)) {
                 // the batch holds the row after the sequence's last key: zero its V rows
@@ -1994,12 +2167,12 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
             for (int i = 4; i < 8; ++i) asm volatile("" : "+v"(kr[i]));
 #pragma unroll
             for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(vr[i]));
-            if (t + kBfTok < tb) issue(t + kBfTok);
+            if (t + kStepT < tb) issue(t + kStepT);
 
             // S^T over the 8 steps of 32 dims, then hi + lo
             // The two waves of a SIMD (w, w + 4) take turns at the higher priority, batch by
             // batch, so one runs ahead on the matrix cores while the other computes its softmax.
-            if ((((t - t0) / kBfTok) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+            if ((it + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
             else __builtin_amdgcn_s_setprio(0);
             f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -2041,43 +2214,18 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
                 o[u] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vr[u]), pb, o[u], 0, 0, 0);
         }
         bad = __any(bad);
-
-        // O^T hi + lo columns; the row sum over the four lane groups
-        l = allreduce_hi<16>(l, OpSum());
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[u][r] += dpp<kRor8>(o[u][r]);
-        if (single) {
-            if (hi_col && rr < rows_s) {
-                const float inv = 1.f / (l + 1e-10f);
-                float* op = a.out + out_row(a, s, g, rr) * D + 4 * grp;
-#pragma unroll
-                for (int u = 0; u < 16; ++u) {
-                    float4 v;
-                    v.x = bad ? __builtin_nanf("") : o[u][0] * inv;
-                    v.y = bad ? __builtin_nanf("") : o[u][1] * inv;
-                    v.z = bad ? __builtin_nanf("") : o[u][2] * inv;
-                    v.w = bad ? __builtin_nanf("") : o[u][3] * inv;
-                    *reinterpret_cast<float4*>(op + 16 * u) = v;
-                }
-            }
+        if constexpr (IW) {
+            pend_s = s;
+            pend_single = single;
+            pend_rows = rows_s;
+            pend_nb = (tb - t0 + kBfTok - 1) / kBfTok;
+            pend_bad = bad;
         } else {
-            const size_t slot = (size_t)(w + s) * a.rows_seq;
-            float* po = static_cast<float*>(a.part_o);
-            float* pml = static_cast<float*>(a.part_ml);
-            if (hi_col && rr < rows) {
-                const int row = (rr / a.G) * a.Hq + g * a.G + rr % a.G;
-                float* dst = po + (slot + row) * D + 4 * grp;
-#pragma unroll
-                for (int u = 0; u < 16; ++u)
-                    *reinterpret_cast<float4*>(dst + 16 * u) = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
-                if (grp == 0) {  // the merge takes natural-log units
-                    pml[(slot + row) * 2 + 0] = bad ? __builtin_nanf("") : m * kLn2;
-                    pml[(slot + row) * 2 + 1] = l;
-                }
-            }
+            finish(s, single, rows_s, 1, bad);
         }
+    }
+    if constexpr (IW) {
+        if (pend_s >= 0) finish(pend_s, pend_single, pend_rows, pend_nb, pend_bad);
     }
 }
 
@@ -2404,6 +2552,26 @@ int32_t launch_bf16_mfma(StreamArgs a, hipStream_t st) {
     const size_t lds = mfma_stage_offset(a.batch, false) + (size_t)waves * kBfStage;
     if (lds > kMfmaLdsMax || a.keys || a.ring_size > 0 || a.bs_shift < 1 || a.nr.k_new)
         return launch_r<256, uint16_t, 4, 2>(a, st);
+    // Interleaved waves (grid (nwg, Hkv), eight waves per kv head) where the batch's LDS fits.
+    const size_t lds_iw = mfma_stage_offset(a.batch, false) + (size_t)kMaxWaves * kBfStage + bf_iw_red_bytes();
+    if (lds_iw <= kMfmaLdsMax) {
+        const void* fn = reinterpret_cast<const void*>(&stream_bf16_mfma_kernel<kAddrPaged, true>);
+        if (!reserve_lds(fn, (int)kMfmaLdsMax))
+            return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
+        const int slots = fill_workgroups(fn, kMaxWaves * kSW, lds_iw);
+        if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
+        a.nwg = slots / a.Hkv > 0 ? slots / a.Hkv : 1;
+        if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
+        if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
+        a.lead = PKV_LEAD_BF16_IW;
+        hipLaunchKernelGGL((stream_bf16_mfma_kernel<kAddrPaged, true>), dim3(a.nwg, a.Hkv), dim3(kMaxWaves * kSW),
+                           lds_iw, st, a);
+        if (hipGetLastError() != hipSuccess)
+            return fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
+        hipLaunchKernelGGL((stream_merge_kernel<256, float>), dim3(a.rows_seq, a.batch), dim3(merge_threads<256>()), 0,
+                           st, a);
+        return PKV_OK;
+    }
     const void* fn = reinterpret_cast<const void*>(&stream_bf16_mfma_kernel<kAddrPaged>);
     if (!reserve_lds(fn, (int)kMfmaLdsMax))
         return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
