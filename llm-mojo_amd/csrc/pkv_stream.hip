@@ -99,6 +99,9 @@ constexpr int kPerMin = PKV_STREAM_PER_MIN;      // fewest keys per workgroup
 #ifndef PKV_LEAD_IW
 #define PKV_LEAD_IW 128
 #endif
+#ifndef PKV_LEAD_VEC_IW
+#define PKV_LEAD_VEC_IW 16
+#endif
 #ifndef PKV_LEAD_BF16_IW
 #define PKV_LEAD_BF16_IW 384
 #endif
@@ -666,7 +669,28 @@ __device__ inline void copy_new_rows(const StreamArgs& a, const int* s_meta, con
 // R query rows per wave; WPH waves per KV head split the head's rows (WPH = 2 gives two
 // waves of R rows each, reading the same K/V: the second read of a row slice hits the cache).
 // ADDR: kAddrPaged, kAddrRing (key t at row ring_base + t % ring_size) or kAddrSparse.
-template <int D, typename KV, int R, int WPH, int ADDR>
+// Vector kernel, interleaved waves: the exchange area after the per-sequence ints (and a
+// fused append's plan): m [8 waves][4 rows], 8 bad flags, then four regions of a wave's
+// accumulators (at most 4 rows x 4 doubles per lane) and its rows' l.
+constexpr int kVecRedM = 8 * 4 * 8;
+constexpr int kVecRedO = kVecRedM + 64;
+constexpr int kVecRedRegion = 4 * 4 * 8 * 64 + 64;
+__host__ __device__ constexpr size_t vec_red_offset(int batch, bool fused) {
+    return ((size_t)(stream_seq_ints(batch) + (fused ? 3 * batch + 2 : 0)) * sizeof(int) + 15) & ~(size_t)15;
+}
+__host__ __device__ constexpr size_t vec_red_bytes() { return kVecRedO + 4 * (size_t)kVecRedRegion; }
+
+// IW (interleaved waves; head_dim 256, one wave per kv head, paged or ring keys): grid
+// (nwg, Hkv), the eight waves of a workgroup take the batches of one kv head's pieces in
+// turn and combine their (m, l, acc) through LDS at each piece's end, as the fp64 MFMA
+// kernel's interleaved form does; a piece then leaves one partial per kv head. The
+// accumulators are a few KiB per wave, so the exchange runs right after the piece's last
+// batch. Against one wave per kv head (same box): config 2 209.3-211.0 -> 205.9 us per
+// launch (sliding layer 81.5 -> 78.7, global 322.9 -> 318.6 us in the trace), config 3
+// 355.8-356.6 -> 346.1-347.4 us, config 5's step 1.098-1.100 -> 1.073-1.080 ms (its MTP
+// reads); lead-in 16 / 64 / 128 / 256 keys on config 2: 205.9 / 205.8-205.9 / 206.1-206.4 /
+// 209.7 us.
+template <int D, typename KV, int R, int WPH, int ADDR, bool IW = false>
 __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamArgs a) {
     using Acc = typename SKV<KV>::Acc;
     constexpr int kElt = SKV<KV>::kElt;
@@ -689,20 +713,27 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
     const int tid = threadIdx.x;
     const int lane = tid & (kSW - 1);
     const int wave = ufirst(tid / kSW);
-    const int w = blockIdx.y;
+    const int w = IW ? blockIdx.x : blockIdx.y;  // the workgroup's key range
     const int B = a.batch;
     constexpr bool PAGED = ADDR == kAddrPaged;
+    static_assert(!IW || (WPH == 1 && D == 256 && ADDR != kAddrSparse), "interleaved waves");
 
     const KeySplit sp = stream_setup<D, ADDR>(a, s_pre, s_lo, s_meta, s_al);
     const bool fused = PAGED && fused_append(a);
-    if (fused) copy_new_rows<D, KV, WPH>(a, s_meta, s_al, blockIdx.x * (kMaxWaves / WPH), wave, lane, w);
+    if (fused) {
+        if constexpr (IW) copy_new_rows<D, KV, kMaxWaves>(a, s_meta, s_al, blockIdx.y, wave, lane, w);
+        else copy_new_rows<D, KV, WPH>(a, s_meta, s_al, blockIdx.x * (kMaxWaves / WPH), wave, lane, w);
+    }
     const int total = ufirst(s_pre[B]);
     const int k0 = sp.start(w);
     if (k0 >= total) return;
     const int k1 = min(total, sp.start(w + 1));
-    const int g = blockIdx.x * (kMaxWaves / WPH) + wave / WPH;  // this wave's KV head
-    const int rb = (wave % WPH) * R;  // first of this wave's rows of the head
+    // this wave's KV head (IW: the workgroup's, whose pieces wave 0 stores)
+    const int g = IW ? (int)blockIdx.y : blockIdx.x * (kMaxWaves / WPH) + wave / WPH;
+    const int rb = IW ? 0 : (wave % WPH) * R;  // first of this wave's rows of the head
     if (g >= a.Hkv) return;
+    // IW: the waves' exchange area, after the per-sequence ints (and the allocation plan)
+    char* const red = reinterpret_cast<char*>(smem) + vec_red_offset(B, fused);
 
     const int rows = a.G * a.q_cnt;
     const size_t row_bytes = (size_t)a.Hkv * D * kElt;
@@ -878,7 +909,8 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             }
         }
 
-        for (int t = ta; t < tb; t += U) {
+        constexpr int kStepT = IW ? kMaxWaves * U : U;  // from one of a wave's batches to the next
+        for (int t = IW ? ta + U * wave : ta; t < tb; t += kStepT) {
             const int tl = min(t + U - 1, tb - 1);
             if (SPARSE && tl - pgbase >= kSW) load_pages(t);  // the next 64 listed keys
             if (ADDR == kAddrPaged && (tl >> a.bs_shift) - pgbase >= kSW) load_pages(t);  // next 64 pages
@@ -966,7 +998,70 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         }
         bad = __any(bad);
 
-        if (single) {
+        if constexpr (IW) {
+            // The waves' rows into wave 0's: the rows' common max, then the rescaled acc and l
+            // summed in three rounds (waves 4-7 into 0-3, 2-3 into 0-1, 1 into 0). The branches
+            // are uniform over the workgroup, so every wave meets the same barriers.
+            const int nb = (tb - ta + U - 1) / U;  // batches of the piece
+            if (nb > 1) {
+                Acc* rm = reinterpret_cast<Acc*>(red);                      // m of [wave][row]
+                int* rbad = reinterpret_cast<int*>(red + kVecRedM);         // [wave]
+                if (lane == r_own * REP && u_own == 0) rm[wave * 4 + r_own] = m_own;
+                if (lane == 0) rbad[wave] = bad ? 1 : 0;
+                __syncthreads();
+                bool any_bad = false;
+                Acc M = (Acc)-INFINITY;
+#pragma unroll
+                for (int v = 0; v < kMaxWaves; ++v) {
+                    any_bad = any_bad || rbad[v] != 0;
+                    M = fmax(M, rm[v * 4 + r_own]);
+                }
+                bad = any_bad;
+                const Acc f_own = m_own == (Acc)-INFINITY ? (Acc)0 : exp_acc(m_own - M);
+                l_own *= f_own;
+                m_own = M;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const Acc f = bcast(f_own, r * REP);
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[r][e] *= f;
+                }
+                // Region: element (r, e) of lane L at Acc index (r EPL + e) 64 + L, then l [row]
+                auto region = [&](int i) { return reinterpret_cast<Acc*>(red + kVecRedO + (size_t)i * kVecRedRegion); };
+                auto put = [&](int i) {
+                    Acc* ro = region(i);
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int e = 0; e < EPL; ++e) ro[(r * EPL + e) * kSW + lane] = acc[r][e];
+                    if (lane == r_own * REP && u_own == 0) ro[R * EPL * kSW + r_own] = l_own;
+                };
+                auto add = [&](int i) {
+                    const Acc* ro = region(i);
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int e = 0; e < EPL; ++e) acc[r][e] += ro[(r * EPL + e) * kSW + lane];
+                    l_own += ro[R * EPL * kSW + r_own];
+                };
+                if (nb > 4) {  // waves 4-7 into 0-3 (regions 0-3)
+                    if (wave >= 4) put(wave - 4);
+                    __syncthreads();
+                    if (wave < 4) add(wave);
+                }
+                if (nb > 2) {  // waves 2, 3 into 0, 1 (regions 2, 3, which only they read before)
+                    if (wave == 2 || wave == 3) put(wave);
+                    __syncthreads();
+                    if (wave < 2) add(wave + 2);
+                }
+                if (wave == 1) put(1);  // wave 1 into 0 (region 1, which only wave 1 read before)
+                __syncthreads();
+                if (wave == 0) add(1);
+            }
+        }
+        if (IW && wave != 0) {
+            // every wave but 0 has handed its rows over
+        } else if (single) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 if (rb + r < rows_s) {
@@ -2409,6 +2504,28 @@ int32_t launch_addr(StreamArgs a, hipStream_t st) {
     const int threads = waves * kSW;
     const bool fused = ADDR == kAddrPaged && a.nr.k_new && a.j0 == 0;
     const size_t lds = stream_vector_lds(a.batch, fused);
+    if constexpr (D == 256 && WPH == 1 && ADDR != kAddrSparse) {
+        // Interleaved waves: grid (nwg, Hkv), eight waves per kv head.
+        const size_t lds_iw = vec_red_offset(a.batch, fused) + vec_red_bytes();
+        if (lds_iw <= kStreamLdsMax) {
+            const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH, ADDR, true>);
+            if (lds_iw > 64 * 1024 && !reserve_lds(fn, (int)kStreamLdsMax))
+                return fail(PKV_ERR_HIP, "pkv_attend: could not reserve the kernel's LDS");
+            const int slots = fill_workgroups(fn, kMaxWaves * kSW, lds_iw);
+            if (slots <= 0) return fail(PKV_ERR_HIP, "pkv_attend: occupancy query failed");
+            a.nwg = slots / a.Hkv > 0 ? slots / a.Hkv : 1;
+            if (a.nwg > a.nwg_cap) a.nwg = a.nwg_cap;
+            if (a.nwg > 1) a.nwg &= ~1;  // whole pairs (key_split)
+            a.lead = PKV_LEAD_VEC_IW;
+            hipLaunchKernelGGL((stream_attend_kernel<D, KV, R, WPH, ADDR, true>), dim3(a.nwg, a.Hkv),
+                               dim3(kMaxWaves * kSW), lds_iw, st, a);
+            if (hipGetLastError() != hipSuccess)
+                return fail(PKV_ERR_HIP, "pkv_attend: the attention launch failed");
+            hipLaunchKernelGGL((stream_merge_kernel<D, Acc>), dim3(a.rows_seq, a.batch + (fused ? 1 : 0)),
+                               dim3(merge_threads<D>()), 0, st, a);
+            return PKV_OK;
+        }
+    }
     const void* fn = reinterpret_cast<const void*>(&stream_attend_kernel<D, KV, R, WPH, ADDR>);
     if (lds > kStreamLdsMax)  // stream_attend refuses such batches before any launch
         return fail(PKV_ERR_UNSUPPORTED, "pkv_attend: batch too large for the kernel's LDS");
