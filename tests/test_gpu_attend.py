@@ -294,11 +294,23 @@ def test_verify_bf16_mfma(gpu, hq, hkv, q_len, bs, window):
 def test_batch_4096_large_lds(gpu, q_len):
     """The largest batch pkv_attend takes: the stream kernels keep 5 ints per sequence in
     LDS, ~80 KiB at 4096, above the 64 KiB a kernel gets without opting in (the vector
-    kernel for decode; the fp64 MFMA kernel, 8 rows per kv head, for 4 queries)."""
+    kernel for decode, interleaved; the fp64 MFMA kernel, 8 rows per kv head, for 4 queries,
+    in its one-wave-per-kv-head form, since the interleaved form's exchange area no longer
+    fits)."""
     print(f"[attend] batch 4096, q_len {q_len}", flush=True)
     rng = np.random.default_rng(4096 + q_len)
     ctx = rng.integers(1, 48, 4096)
     _batched_case(rng, 4096, q_len, ctx, 2, 1, 256, 16, 0, F32, 0.0625)
+
+
+def test_bf16_verify_batch_512(gpu):
+    """bf16 pools, 8 rows per kv head, 512 sequences: the interleaved bf16 MFMA kernel's
+    exchange area no longer fits beside the per-sequence ints, so the launch takes the
+    one-wave-per-kv-head form of the same kernel."""
+    print("[attend] bf16 verify, batch 512", flush=True)
+    rng = np.random.default_rng(512)
+    ctx = rng.integers(1, 300, 512)
+    _batched_case(rng, 512, 4, ctx, 16, 8, 256, 16, 0, BF16, 0.0625)
 
 
 def test_gqa8_d512(gpu):
