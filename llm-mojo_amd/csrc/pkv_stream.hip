@@ -1900,7 +1900,8 @@ __device__ inline float bf16_bits_to_float(uint16_t b) { return __uint_as_float(
 // requested. The eight staging buffers leave room for three 8 KiB exchange regions, so the
 // sum takes four rounds: waves 4-6 into 0-2, 7 into 3, 2-3 into 0-1, 1 into 0. Config 5's
 // bf16 verify: 60.4 + 6.7 -> 59.7 + 4.9 us (stream + merge in the trace), traffic 1.149 ->
-// 1.025 x algorithmic.
+// 1.025 x algorithmic. Every wave then holds the same rows, so the hi / lo split of Q is
+// shared: wave v splits step v and the eight steps go round through LDS (64.6 -> 63.1 us).
 constexpr int kBfRedRegion = 8192 + 32;  // o of the 32 hi-column lanes (8 rows x 256), then l
 constexpr int kBfRedO = 256 + 32;        // m [8 waves][8 rows] (floats), 8 bad flags
 __host__ __device__ constexpr size_t bf_iw_red_bytes() { return kBfRedO + 3 * (size_t)kBfRedRegion; }
@@ -2091,9 +2092,11 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         if (idle) {
             // IW: every wave but 0 has handed its rows over
         } else if (fsingle) {
+            int gofs = 4 * grp;
+            if constexpr (IW) asm volatile("" : "+v"(gofs));
             if (hi_col && rr < frows) {
                 const float inv = 1.f / (l + 1e-10f);
-                float* op = a.out + out_row(a, fs, g, rr) * D + 4 * grp;
+                float* op = a.out + out_row(a, fs, g, rr) * D + gofs;
 #pragma unroll
                 for (int u = 0; u < 16; ++u) {
                     float4 v;
@@ -2105,12 +2108,16 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
                 }
             }
         } else {
+            // IW: the lane's offset from an opaque copy (formed here, not kept in registers
+            // across the kernel)
+            int gofs = 4 * grp;
+            if constexpr (IW) asm volatile("" : "+v"(gofs));
             const size_t slot = (size_t)(w + fs) * a.rows_seq;
             float* po = static_cast<float*>(a.part_o);
             float* pml = static_cast<float*>(a.part_ml);
             if (hi_col && rr < rows) {
                 const int row = (rr / a.G) * a.Hq + g * a.G + rr % a.G;
-                float* dst = po + (slot + row) * D + 4 * grp;
+                float* dst = po + (slot + row) * D + gofs;
 #pragma unroll
                 for (int u = 0; u < 16; ++u)
                     *reinterpret_cast<float4*>(dst + 16 * u) = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
@@ -2147,15 +2154,21 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
             pre_s == s ? pre_raw : trow[min((t0 >> a.bs_shift) + lane, last_page)];
         asm volatile("" ::: "memory");
         float4 qraw[8][2];
-        auto load_q = [&]() {  // IW: after the piece before is finished (fewer registers live)
+        // IW: wave v requests only step v of every lane's Q (its share of the hi / lo split
+        // below); the other steps come through LDS.
+        float4 qstep[2];
+        if constexpr (IW) {
+            const float* qp = a.q + out_row(a, s, g, min(rr, rows - 1)) * D + 8 * grp + 32 * wave;
+            qstep[0] = *reinterpret_cast<const float4*>(qp);
+            qstep[1] = *reinterpret_cast<const float4*>(qp + 4);
+        } else {
             const float* qp = a.q + out_row(a, s, g, min(rr, rows - 1)) * D + 8 * grp;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 qraw[c][0] = *reinterpret_cast<const float4*>(qp + 32 * c);
                 qraw[c][1] = *reinterpret_cast<const float4*>(qp + 32 * c + 4);
             }
-        };
-        if constexpr (!IW) load_q();
+        }
         asm volatile("" ::: "memory");
         // The next sequence's first 64 page ids, for its piece after this one (a piece
         // starts at its sequence's first key).
@@ -2212,7 +2225,6 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         if (t1 < tb) issue(t1);
         if constexpr (IW) {  // the piece before, while this one's first batch is on its way
             if (pend_s >= 0) finish(pend_s, pend_single, pend_rows, pend_nb, pend_bad);
-            load_q();
         }
         m = -INFINITY;
         l = 0.f;
@@ -2221,20 +2233,44 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_bf16_mfma_kernel(Strea
         // Q^T as the B operand of step c: column l16 = row rr, dims 32c + 8 grp + e; its hi
         // (column < 8) or lo part, zero for rows past `rows`.
         bf16x8 qreg[8];
-        {
-            const bool qlive = rr < rows;
+        const bool qlive = rr < rows;
+        auto split = [&](const float4& q0, const float4& q1) {
+            const float xv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            bf16x8 r;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = qlive ? xv[e] : 0.f;
+                const uint16_t h = bf16_rne_bits(x);
+                const uint16_t b16 = hi_col ? h : bf16_rne_bits(x - bf16_bits_to_float(h));
+                r[e] = __builtin_bit_cast(__bf16, b16);
+            }
+            return r;
+        };
+        if constexpr (IW) {
+            // Every wave holds the same rows: wave v splits step v into LDS (exchange region 0,
+            // which no finish uses between this barrier and the next piece's first one) and
+            // reads the eight steps back. The LDS accesses are untracked (copies in flight).
+            uint32_t lo = lane;
+            asm volatile("" : "+v"(lo));
+            const uint32_t qst = lds_addr(red + kBfRedO) + 16 * lo;
+            lds_w128(qst + 1024 * wave, __builtin_bit_cast(i32x4, split(qstep[0], qstep[1])));
+            __builtin_amdgcn_s_waitcnt(kLgkm0);
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            i32x4 qv[8];
+            static_for<0, 8>([&](auto C) {
+                constexpr int c = decltype(C)::value;
+                qv[c] = lds_b128<1024 * c>(qst);
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(qv[0]));
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const float xv[8] = {qraw[c][0].x, qraw[c][0].y, qraw[c][0].z, qraw[c][0].w,
-                                     qraw[c][1].x, qraw[c][1].y, qraw[c][1].z, qraw[c][1].w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float x = qlive ? xv[e] : 0.f;
-                    const uint16_t h = bf16_rne_bits(x);
-                    const uint16_t b16 = hi_col ? h : bf16_rne_bits(x - bf16_bits_to_float(h));
-                    qreg[c][e] = __builtin_bit_cast(__bf16, b16);
-                }
+                asm volatile("" : "+v"(qv[c]));
+                qreg[c] = __builtin_bit_cast(bf16x8, qv[c]);
             }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) qreg[c] = split(qraw[c][0], qraw[c][1]);
         }
         int it = 0;  // this wave's batch index in the piece
         for (int t = t1; t < tb; t += kStepT, ++it) {
