@@ -759,6 +759,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
         }
         s = lo;
     }
+    int pre_s = -1, pre_raw = 0;  // paged: the next piece's first page ids (pre_s: its sequence)
     for (; s < B; ++s) {
         const int ps = ufirst(s_pre[s]);
         const int pe = ufirst(s_pre[s + 1]);
@@ -838,7 +839,7 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
             pgbase = ta >> a.bs_shift;
             const int pg = min(pgbase + lane, last_page);
             const int32_t* src = (pg >= g_lo && pg < g_hi) ? a.nr.free_list + (g_top - pg) : trow + pg;
-            first_raw = *src;
+            first_raw = pre_s == s ? pre_raw : *src;
         }
         asm volatile("" ::: "memory");  // issued before the query rows
         float qraw[R][EPL];
@@ -851,6 +852,23 @@ __global__ __launch_bounds__(kMaxWaves * kSW) void stream_attend_kernel(StreamAr
                 qraw[r][e] = v.x;
                 qraw[r][e + 1] = v.y;
             }
+        }
+        // Paged: the next sequence's first 64 page ids, for its piece after this one (a piece
+        // starts at its sequence's first key), requested with this piece's first loads.
+        if (ADDR == kAddrPaged && s + 1 < B && ufirst(s_pre[s + 1]) + a.lead < k1 &&
+            ufirst(s_pre[s + 2]) > ufirst(s_pre[s + 1])) {
+            const int lo_n = ufirst(s_lo[s + 1]);
+            const int tb_n = lo_n + min(k1, ufirst(s_pre[s + 2])) - ufirst(s_pre[s + 1]) - a.lead;
+            const int pg = min((lo_n >> a.bs_shift) + lane, (tb_n - 1) >> a.bs_shift);
+            const int32_t* src = a.tables + (size_t)(s + 1) * a.table_stride + pg;
+            if (fused) {  // the blocks granted to it come from the free list
+                const SeqAlloc al = seq_alloc(s_al, B, a.num_blocks, s + 1);
+                const int n_lo = ufirst(al.len), n_hi = n_lo + ufirst(al.granted);
+                const int n_top = ufirst(al.fc) - 1 - ufirst(al.pref) + n_lo;
+                if (pg >= n_lo && pg < n_hi) src = a.nr.free_list + (n_top - pg);
+            }
+            pre_raw = *src;
+            pre_s = s + 1;
         }
         asm volatile("" ::: "memory");  // the query rows go out before the table lookup
         // (branch-free from here on, so the compiler does not move a load into a branch)
